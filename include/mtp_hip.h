@@ -1,0 +1,121 @@
+/*
+ * mtp_hip.h -- C-ABI of the MI355X (gfx950) hot path of mlx-train-perf.
+ *
+ * Two parts, each replacing the reference's mx.fast.metal_kernel launch layer:
+ *   (A) fused linear cross-entropy (LCE): logit-free forward (per-token NLL, log-sum-exp,
+ *       target logit) and the dL/dH backward that recomputes vocab tiles, over a dense bf16 or a
+ *       4-bit affine group-quantized (group size 64) head;
+ *   (B) flash attention forward and backward with GQA, causal and packed-segment masks, saving
+ *       only O and the per-row log-sum-exp L.
+ *
+ * Conventions (all entry points):
+ *   - Plain pointers and sizes; the caller allocates every tensor and the workspace and owns the
+ *     stream (a hipStream_t passed as void*; NULL = the default stream). The library never
+ *     allocates device memory and never synchronizes the host.
+ *   - Tensors are dense row-major; bf16 values are stored as uint16 bit patterns.
+ *   - Return 0 on success or a negative MTP_ERR_* code; mtp_last_error() then returns a
+ *     thread-local message naming the offending argument.
+ *   - Calls are stream-ordered and re-entrant: there is no global mutable state besides the
+ *     thread-local error message.
+ */
+#ifndef MTP_HIP_H
+#define MTP_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTP_ABI_VERSION 1
+
+/* Error codes; the Python layer maps them onto the reference's typed exceptions
+ * (src/mlx_train_perf/errors.py:1-76). */
+#define MTP_OK 0
+#define MTP_ERR_INPUT (-1)       /* LossInputError / AttentionInputError: bad shape or value  */
+#define MTP_ERR_UNSUPPORTED (-2) /* UnsupportedHeadError / UnsupportedAttentionError          */
+#define MTP_ERR_WORKSPACE (-3)   /* LaunchBudgetError: workspace missing or too small         */
+#define MTP_ERR_RUNTIME (-4)     /* HIP launch failure                                        */
+
+/* Head kinds (reference: src/mlx_train_perf/core/loss.py:30-47, DenseHead / QuantizedHead). */
+#define MTP_HEAD_DENSE 0 /* w: bf16 [V][D]                                                        */
+#define MTP_HEAD_Q4 1    /* w_q: u32 [V][D/8] (8 nibbles, low first); scales, biases: bf16 [V][D/64] */
+
+const char* mtp_last_error(void);
+int mtp_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * (A) Fused linear cross-entropy
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes needed by mtp_lce_fwd (per-token partial maxima and sums per vocab split).
+ * Replaces the per-tile lse/tgt chaining buffers of core/kernel/launch.py:75-100. */
+size_t mtp_lce_fwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind);
+
+/* Forward. hidden: bf16 [n][d]; targets: int64 [n]; outputs fp32 [n] each:
+ *   lse[t] = logsumexp_v(hidden[t] . w[v]), tgt[t] = hidden[t] . w[targets[t]],
+ *   nll[t] = lse[t] - tgt[t].
+ * Rows whose target equals ignore_index get nll = 0 and tgt = 0 (lse is still computed).
+ * A target outside [0, v) that is not ignore_index leaves tgt = 0 (nll = lse), as the reference
+ * kernel does when validate_targets=False (core/kernel/source.py:46,143-144).
+ * Replaces: launch.forward (core/kernel/launch.py:75-100) + kernel K1 (core/kernel/source.py:25-190)
+ * for head_kind DENSE, and launch.forward_quantized (core/kernel/launch.py:336-373) + kernel K2
+ * (core/kernel/source.py:199-340) for head_kind Q4. */
+int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
+                const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt,
+                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Vocab columns per backward chunk for a workspace budget (bytes); a multiple of 256. */
+int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
+
+/* Workspace bytes needed by mtp_lce_bwd at a given chunk: the bf16 gradient tile buffer
+ * [n][chunk] plus, when more than one chunk is needed, an fp32 [n][d] dH accumulator. */
+size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk);
+
+/* Backward, frozen head: d_hidden[t] = coef[t] * sum_v (exp(z[t][v] - lse[t]) - [v == targets[t]]) w[v]
+ * with coef[t] = d_nll[t] (0 for ignored rows); d_hidden is bf16 [n][d].
+ * lse is the forward's saved output (no recompute of the forward pass).
+ * Replaces: the kernel-path vjp _ce_frozen_vjp / quantized _ce_vjp (core/loss.py:279-298,322-349)
+ * that call chunked_backward (core/chunked.py:52-90); design of the fused 2-GEMM backward K4
+ * (core/kernel/source.py:475-611). */
+int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
+                const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                int32_t head_kind, int64_t ignore_index, const float* lse, const float* d_nll,
+                void* d_hidden, int64_t chunk, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * (B) Flash attention. Layouts (attention/reference.py:22-25): q [b][hq][s][dh],
+ * k, v [b][hkv][s][dh], o like q, lse fp32 [b][hq][s] (natural log). GQA: query head h reads
+ * kv head h / (hq / hkv) (attention/reference.py:37-39). dh in {64, 96, 128}.
+ * Packed mode: seg_id and seg_start are int32 [b][s] (attention/segments.py:9-19); key j is
+ * visible to query i iff seg_id[i] == seg_id[j] and j <= i (segments.py:22-29). Both NULL means
+ * plain causal. causal must be 1 (the reference kernel serves causal only, api.py:109-113).
+ * ------------------------------------------------------------------------------------------- */
+
+/* Forward: o = softmax(scale * q k^T + mask) v, lse = row logsumexp of the masked scaled scores.
+ * Replaces: launch_flash_fwd (attention/kernel/launch.py:386-441) + kernel K7
+ * (attention/kernel/source.py:262-580). */
+int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t hq, int64_t hkv,
+                 int64_t s, int64_t dh, float scale, int32_t causal, const int32_t* seg_id,
+                 const int32_t* seg_start, void* o, float* lse, void* stream);
+
+/* Workspace bytes for mtp_attn_bwd: the fp32 row term D = rowsum(dO * O), [b][hq][s]. */
+size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh);
+
+/* Backward from the saved (o, lse): dq like q, dk and dv like k (summed over each kv head's
+ * query-head group); all bf16.
+ * Replaces: launch_bwd_D (attention/kernel/launch.py:765-787, kernel K8), launch_bwd_dq
+ * (launch.py:985-1049, kernel K10) and launch_bwd_dkv (launch.py:1225-1293, kernel K12). */
+int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse,
+                 const void* d_o, int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh,
+                 float scale, int32_t causal, const int32_t* seg_id, const int32_t* seg_start,
+                 void* d_q, void* d_k, void* d_v, void* workspace, size_t workspace_bytes,
+                 void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTP_HIP_H */

@@ -1,0 +1,713 @@
+// Flash attention forward and backward for gfx950 (GQA, causal, packed segments).
+//
+// Semantics follow the reference oracles: O = softmax(scale * Q K^T + mask) V with an fp32 softmax,
+// L = row logsumexp of the masked scaled scores (attention/reference.py:42-116); the backward uses
+// the FlashAttention equations D = rowsum(dO * O), P = exp(S - L), dV = P^T dO, dP = dO V^T,
+// dS = P * (dP - D), dQ = scale dS K, dK = scale dS^T Q, with dK and dV summed over the query-head
+// group of each kv head (attention/api.py:126-194). Query head h reads kv head h / (Hq / Hkv).
+// Packed mode: key j is visible to query i iff seg_id[i] == seg_id[j] and j <= i
+// (attention/segments.py:22-29); seg_start (non-decreasing, gapless layout) only bounds loops.
+//
+// Kernel structure (all MFMA 32x32x16 bf16, fp32 accumulate, 4 waves per workgroup):
+//   attn_fwd:     a wave owns 32 queries of one head; a workgroup holds up to 4 heads of one GQA
+//                 group so every K/V tile staged in LDS feeds 128 query rows. Scores are computed
+//                 transposed (keys x queries) so each lane owns one query column: the online
+//                 softmax is lane-local plus one exchange with lane^32, and the probability tile
+//                 feeds the P.V MFMA directly from registers.
+//   attn_bwd_dq:  same ownership as the forward; recomputes S^T and dP^T per key tile and
+//                 accumulates dQ^T in registers (rows are owned, no atomics).
+//   attn_bwd_dkv: a wave owns 32 keys of one kv head; the workgroup sweeps every query tile of
+//                 every head in the group and accumulates dK^T, dV^T in registers (no atomics).
+// Operand tiles in LDS: "natural" tiles keep 64 rows x head_dim with a 16-byte row pad;
+// "transposed" tiles keep head_dim rows x 64 positions in the 128-byte swizzled layout, with the
+// middle two 4-position quads of every 16-position group swapped so that one 16-byte read yields
+// the MFMA contraction slots that match the accumulator layout of the preceding product.
+#include "mtp_common.hpp"
+#include "mtp_launch.hpp"
+
+namespace mtp {
+
+constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
+
+template <int DH>
+struct AttnCfg {
+  static constexpr int kNatStride = DH * 2 + 16;
+  static constexpr int kNatBytes = kKT * kNatStride;
+  static constexpr int kTBytes = DH * 128;
+  static constexpr int kDK = DH / 16;  // MFMA contraction steps over head_dim
+  static constexpr int kDB = DH / 32;  // 32-row output blocks over head_dim
+};
+
+// Stored quad of logical quad q (4 positions) inside a transposed row.
+__device__ __forceinline__ int quad_pos(int q) {
+  const int ql = q & 3;
+  return (q & ~3) | (ql == 1 ? 2 : (ql == 2 ? 1 : ql));
+}
+__device__ __forceinline__ int t_off(int d, int sq) { return lds_off(d, sq >> 1) + ((sq & 1) << 3); }
+
+// One thread's 8-row x 8-column block of a 64-row tile with DH columns (row stride DH elements).
+template <int DH>
+struct BlockLoad {
+  u32x4 x[8];
+  int rb, cb;
+  bool active;
+
+  __device__ __forceinline__ void init(int b) {
+    active = b < DH;
+    rb = b / (DH / 8);
+    cb = b % (DH / 8);
+  }
+  __device__ __forceinline__ void load(const bf16_t* base, int rows_valid) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = 8 * rb + i;
+      if (active && r < rows_valid) {
+        x[i] = *reinterpret_cast<const u32x4*>(base + (long)r * DH + 8 * cb);
+      } else {
+        x[i] = zero4();
+      }
+    }
+  }
+  __device__ __forceinline__ void store_nat(char* lds) const {
+    if (!active) return;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+      *reinterpret_cast<u32x4*>(lds + (8 * rb + i) * AttnCfg<DH>::kNatStride + 16 * cb) = x[i];
+  }
+  __device__ __forceinline__ void store_t(char* lds) const {
+    if (!active) return;
+    u32x4 y[8];
+    transpose8x8(x, y);
+    const int q0 = quad_pos(2 * rb), q1 = quad_pos(2 * rb + 1);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int d = 8 * cb + j;
+      *reinterpret_cast<u32x2*>(lds + t_off(d, q0)) = u32x2{y[j][0], y[j][1]};
+      *reinterpret_cast<u32x2*>(lds + t_off(d, q1)) = u32x2{y[j][2], y[j][3]};
+    }
+  }
+};
+
+template <int DH>
+__device__ __forceinline__ bf16x8 nat_frag(const char* tile, int row, int ks, int h) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + row * AttnCfg<DH>::kNatStride + 32 * ks + 16 * h));
+}
+__device__ __forceinline__ bf16x8 t_frag(const char* tile, int row, int ks, int h) {
+  return as_bf16x8(lds_read16(tile, lds_off(row, 2 * ks + h)));
+}
+
+__device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1); }
+
+// ------------------------------------------------------------------------------------------
+// Forward
+// ------------------------------------------------------------------------------------------
+template <int DH, bool PACKED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                     const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
+                     bf16_t* __restrict__ o, float* __restrict__ lse, int B, int Hq, int Hkv, int S,
+                     float scale_log2) {
+  using C = AttnCfg<DH>;
+  constexpr int kStage = C::kNatBytes + C::kTBytes + 256;
+  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+
+  const int G = Hq / Hkv;
+  const int hpw = heads_per_wg(G);
+  const int P = 32 * (4 / hpw);
+  const int npb = (S + P - 1) / P;
+  const int hgb = Hq / hpw;  // head groups per batch entry
+  const int nhg = B * hgb;
+  const int g = blockIdx.x;
+  const int hg = g % nhg;
+  const int pb = npb - 1 - g / nhg;  // heaviest (latest) query blocks first
+  const int bidx = hg / hgb;
+  const int h0 = (hg % hgb) * hpw;
+  const int kvh = h0 / G;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int head = h0 + (w % hpw);
+  const int qw0 = pb * P + 32 * (w / hpw);
+  const int qi = qw0 + col;
+  const bool qvalid = qi < S;
+  const bool wave_has = qw0 < S;
+  const int wq_last = wave_has ? ((qw0 + 31 < S) ? qw0 + 31 : S - 1) : 0;
+
+  const bf16_t* qh = q + (long)(bidx * Hq + head) * S * DH;
+  const bf16_t* kh = k + (long)(bidx * Hkv + kvh) * S * DH;
+  const bf16_t* vh = v + (long)(bidx * Hkv + kvh) * S * DH;
+  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  bf16x8 qf[C::kDK];
+#pragma unroll
+  for (int ks = 0; ks < C::kDK; ++ks)
+    qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(qh + (long)qi * DH + 16 * ks + 8 * hf))
+                    : as_bf16x8(zero4());
+
+  const int wg_q0 = pb * P;
+  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  int kv_begin = 0;
+  if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
+  const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
+
+  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
+  if (PACKED) {
+    my_seg = qvalid ? sid[qi] : -2;
+    w_sst_first = wave_has ? sst[qw0] : 0;
+    w_sst_last = wave_has ? sst[wq_last] : 0;
+  }
+
+  float m = kNegInf, l = 0.f;
+  f32x16 oacc[C::kDB];
+#pragma unroll
+  for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
+
+  const bool isV = tid >= 128;
+  BlockLoad<DH> bl;
+  bl.init(isV ? tid - 128 : tid);
+  int seg_reg = 0;
+
+  auto load_tile = [&](int t) {
+    const int kv0 = kv_begin + t * kKT;
+    bl.load((isV ? vh : kh) + (long)kv0 * DH, S - kv0);
+    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
+  };
+  auto store_tile = [&](char* st) {
+    if (isV) bl.store_t(st + C::kNatBytes);
+    else bl.store_nat(st);
+    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + C::kNatBytes + C::kTBytes)[tid] = seg_reg;
+  };
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(lds);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const char* cur = lds + (t & 1) * kStage;
+    const int kv0 = kv_begin + t * kKT;
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(t + 1);
+    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    if (!skip) {
+      f32x16 sacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < C::kDK; ++ks) sacc[kb] = mfma32(nat_frag<DH>(cur, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
+      }
+      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int* segs = reinterpret_cast<const int*>(cur + C::kNatBytes + C::kTBytes);
+      float mt = kNegInf;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float x = sacc[kb][r] * scale_log2;
+          if (need_mask) {
+            const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+            const int j = kv0 + jl;
+            bool ok = (j <= qi) && (j < S) && qvalid;
+            if (PACKED) ok = ok && (segs[jl] == my_seg);
+            if (!ok) x = kNegInf;
+          }
+          sacc[kb][r] = x;
+          mt = fmaxf(mt, x);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float mn = fmaxf(m, mt);
+      const float base = (mn == kNegInf) ? 0.f : mn;
+      const float alpha = fast_exp2(m - base);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
+      bf16x8 pf[4];
+      float ls = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(sacc[kb][r] - base);
+          ls += p;
+          pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
+        }
+      l += ls;
+      const char* vt = cur + C::kNatBytes;
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) oacc[db] = mfma32(t_frag(vt, 32 * db + col, ks, hf), pf[ks], oacc[db]);
+    }
+    if (more) store_tile(lds + ((t + 1) & 1) * kStage);
+    __syncthreads();
+  }
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
+  if (qvalid) {
+    bf16_t* oh = o + ((long)(bidx * Hq + head) * S + qi) * DH;
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        const u32x2 pk{pack_bf16x2(oacc[db][4 * rq] * inv, oacc[db][4 * rq + 1] * inv),
+                       pack_bf16x2(oacc[db][4 * rq + 2] * inv, oacc[db][4 * rq + 3] * inv)};
+        *reinterpret_cast<u32x2*>(oh + d) = pk;
+      }
+    if (hf == 0) lse[(long)(bidx * Hq + head) * S + qi] = (m + fast_log2(lt)) * kLn2;
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward pre-pass: D[row] = sum_d dO[row][d] * O[row][d] (fp32). 8 lanes per row.
+// ------------------------------------------------------------------------------------------
+template <int DH>
+__global__ __launch_bounds__(256) void attn_bwd_dvec_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ d_o,
+                                                            float* __restrict__ dvec, long rows) {
+  const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
+  float acc = 0.f;
+  if (row < rows) {
+    for (int c = sub; c < DH / 8; c += 8) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(o + row * DH + 8 * c);
+      const u32x4 b = *reinterpret_cast<const u32x4*>(d_o + row * DH + 8 * c);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        acc = __builtin_fmaf(bf16lo(a[p]), bf16lo(b[p]), acc);
+        acc = __builtin_fmaf(bf16hi(a[p]), bf16hi(b[p]), acc);
+      }
+    }
+  }
+  acc += __shfl_xor(acc, 4, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 1, 64);
+  if (row < rows && sub == 0) dvec[row] = acc;
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward dQ (query-row owners; no atomics).
+// ------------------------------------------------------------------------------------------
+template <int DH, bool PACKED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                        const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
+                        const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
+                        bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
+  using C = AttnCfg<DH>;
+  constexpr int kStage = 2 * C::kNatBytes + C::kTBytes + 256;  // K, V natural; K^T; key segment ids
+  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+
+  const int G = Hq / Hkv;
+  const int hpw = heads_per_wg(G);
+  const int P = 32 * (4 / hpw);
+  const int npb = (S + P - 1) / P;
+  const int hgb = Hq / hpw;
+  const int nhg = B * hgb;
+  const int g = blockIdx.x;
+  const int hg = g % nhg;
+  const int pb = npb - 1 - g / nhg;
+  const int bidx = hg / hgb;
+  const int h0 = (hg % hgb) * hpw;
+  const int kvh = h0 / G;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int head = h0 + (w % hpw);
+  const int qw0 = pb * P + 32 * (w / hpw);
+  const int qi = qw0 + col;
+  const bool qvalid = qi < S;
+  const bool wave_has = qw0 < S;
+  const int wq_last = wave_has ? ((qw0 + 31 < S) ? qw0 + 31 : S - 1) : 0;
+
+  const long qrow = (long)(bidx * Hq + head) * S;
+  const bf16_t* qh = q + qrow * DH;
+  const bf16_t* doh = d_o + qrow * DH;
+  const bf16_t* kh = k + (long)(bidx * Hkv + kvh) * S * DH;
+  const bf16_t* vh = v + (long)(bidx * Hkv + kvh) * S * DH;
+  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  bf16x8 qf[C::kDK], df[C::kDK];
+#pragma unroll
+  for (int ks = 0; ks < C::kDK; ++ks) {
+    qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(qh + (long)qi * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+    df[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(doh + (long)qi * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+  }
+  const float l2q = qvalid ? lse[qrow + qi] * kLog2e : 0.f;
+  const float dq_row = qvalid ? dvec[qrow + qi] : 0.f;
+
+  const int wg_q0 = pb * P;
+  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  int kv_begin = 0;
+  if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
+  const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
+
+  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
+  if (PACKED) {
+    my_seg = qvalid ? sid[qi] : -2;
+    w_sst_first = wave_has ? sst[qw0] : 0;
+    w_sst_last = wave_has ? sst[wq_last] : 0;
+  }
+
+  f32x16 acc[C::kDB];
+#pragma unroll
+  for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+  const bool isV = tid >= 128;
+  BlockLoad<DH> bl;
+  bl.init(isV ? tid - 128 : tid);
+  int seg_reg = 0;
+  auto load_tile = [&](int t) {
+    const int kv0 = kv_begin + t * kKT;
+    bl.load((isV ? vh : kh) + (long)kv0 * DH, S - kv0);
+    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
+  };
+  auto store_tile = [&](char* st) {
+    if (isV) {
+      bl.store_nat(st + C::kNatBytes);
+    } else {
+      bl.store_nat(st);
+      bl.store_t(st + 2 * C::kNatBytes);
+    }
+    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + 2 * C::kNatBytes + C::kTBytes)[tid] = seg_reg;
+  };
+
+  if (ntiles > 0) {
+    load_tile(0);
+    store_tile(lds);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const char* cur = lds + (t & 1) * kStage;
+    const int kv0 = kv_begin + t * kKT;
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(t + 1);
+    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    if (!skip) {
+      f32x16 sacc[2], pacc[2];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[kb][r] = 0.f;
+          pacc[kb][r] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::kDK; ++ks) {
+          sacc[kb] = mfma32(nat_frag<DH>(cur, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
+          pacc[kb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * kb + col, ks, hf), df[ks], pacc[kb]);
+        }
+      }
+      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int* segs = reinterpret_cast<const int*>(cur + 2 * C::kNatBytes + C::kTBytes);
+      bf16x8 sf[4];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(sacc[kb][r] * scale_log2 - l2q);
+          if (need_mask) {
+            const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+            const int j = kv0 + jl;
+            bool ok = (j <= qi) && (j < S) && qvalid;
+            if (PACKED) ok = ok && (segs[jl] == my_seg);
+            if (!ok) p = 0.f;
+          }
+          sf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
+        }
+      const char* kt = cur + 2 * C::kNatBytes;
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc[db] = mfma32(t_frag(kt, 32 * db + col, ks, hf), sf[ks], acc[db]);
+    }
+    if (more) store_tile(lds + ((t + 1) & 1) * kStage);
+    __syncthreads();
+  }
+
+  if (qvalid) {
+    bf16_t* out = dq + (qrow + qi) * DH;
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        const u32x2 pk{pack_bf16x2(acc[db][4 * rq] * scale, acc[db][4 * rq + 1] * scale),
+                       pack_bf16x2(acc[db][4 * rq + 2] * scale, acc[db][4 * rq + 3] * scale)};
+        *reinterpret_cast<u32x2*>(out + d) = pk;
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward dK, dV (key-row owners, GQA group summed in registers; no atomics).
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ int upper_bound_i32(const int32_t* a, int n, int x) {
+  int lo = 0, hi = n;  // first index with a[i] > x
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] > x) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
+
+template <int DH, bool PACKED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                         const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
+                         const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
+                         bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
+                         float scale_log2, float scale) {
+  using C = AttnCfg<DH>;
+  // Q, dO natural; Q^T, dO^T; then L*log2e, D and segment ids of the 64 queries.
+  constexpr int kStage = 2 * C::kNatBytes + 2 * C::kTBytes + 3 * 256;
+  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+
+  const int G = Hq / Hkv;
+  const int nkv = B * Hkv;
+  const int g = blockIdx.x;
+  const int kvi = g % nkv;
+  const int kt = g / nkv;  // earliest keys (most work under the causal mask) first
+  const int bidx = kvi / Hkv;
+  const int kvh = kvi % Hkv;
+  const int k0 = kt * 128;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int kw0 = k0 + 32 * w;
+  const int kj = kw0 + col;
+  const bool kvalid = kj < S;
+  const bool wave_has = kw0 < S;
+
+  const long krow = (long)(bidx * Hkv + kvh) * S;
+  const bf16_t* kh = k + krow * DH;
+  const bf16_t* vh = v + krow * DH;
+  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  bf16x8 kf[C::kDK], vf[C::kDK];
+#pragma unroll
+  for (int ks = 0; ks < C::kDK; ++ks) {
+    kf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(kh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+    vf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(vh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+  }
+  const int my_seg = (PACKED && kvalid) ? sid[kj] : -3;
+
+  const int q_begin = (k0 / kKT) * kKT;
+  int q_end = S;
+  if (PACKED) {
+    const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
+    q_end = upper_bound_i32(sst, S, klast);
+  }
+  const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
+  const int niter = G * ntq;
+
+  f32x16 dka[C::kDB], dva[C::kDB];
+#pragma unroll
+  for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dka[db][r] = 0.f;
+      dva[db][r] = 0.f;
+    }
+
+  const bool isD = tid >= 128;
+  BlockLoad<DH> bl;
+  bl.init(isD ? tid - 128 : tid);
+  float l2_reg = 0.f, d_reg = 0.f;
+  int seg_reg = 0;
+  auto load_tile = [&](int it) {
+    const int hh = it / ntq, tq = it % ntq;
+    const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
+    const int q0 = q_begin + tq * kKT;
+    bl.load((isD ? d_o : q) + (qrow + q0) * DH, S - q0);
+    if (tid < kKT) {
+      const int qq = q0 + tid;
+      const bool ok = qq < S;
+      l2_reg = ok ? lse[qrow + qq] * kLog2e : 0.f;
+      d_reg = ok ? dvec[qrow + qq] : 0.f;
+      if (PACKED) seg_reg = ok ? sid[qq] : -1;
+    }
+  };
+  auto store_tile = [&](char* st) {
+    const int off = isD ? C::kNatBytes : 0;
+    bl.store_nat(st + off);
+    bl.store_t(st + 2 * C::kNatBytes + (isD ? C::kTBytes : 0));
+    if (tid < kKT) {
+      float* sc = reinterpret_cast<float*>(st + 2 * C::kNatBytes + 2 * C::kTBytes);
+      sc[tid] = l2_reg;
+      sc[64 + tid] = d_reg;
+      reinterpret_cast<int*>(sc + 128)[tid] = seg_reg;
+    }
+  };
+
+  if (niter > 0) {
+    load_tile(0);
+    store_tile(lds);
+  }
+  __syncthreads();
+  for (int it = 0; it < niter; ++it) {
+    const char* cur = lds + (it & 1) * kStage;
+    const int q0 = q_begin + (it % ntq) * kKT;
+    const bool more = it + 1 < niter;
+    if (more) load_tile(it + 1);
+    bool skip = !wave_has || (q0 + kKT - 1 < kw0);
+    int sst_last = 0;
+    if (PACKED && !skip) {
+      skip = sst[q0] > kw0 + 31;
+      sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
+    }
+    if (!skip) {
+      f32x16 sacc[2], pacc[2];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[qb][r] = 0.f;
+          pacc[qb][r] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::kDK; ++ks) {
+          sacc[qb] = mfma32(nat_frag<DH>(cur, 32 * qb + col, ks, hf), kf[ks], sacc[qb]);
+          pacc[qb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * qb + col, ks, hf), vf[ks], pacc[qb]);
+        }
+      }
+      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
+      const float* l2s = reinterpret_cast<const float*>(cur + 2 * C::kNatBytes + 2 * C::kTBytes);
+      const float* ds_ = l2s + 64;
+      const int* segs = reinterpret_cast<const int*>(l2s + 128);
+      bf16x8 pf[4], sf[4];
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * rq + u;
+            float p = fast_exp2(sacc[qb][r] * scale_log2 - l4[u]);
+            if (need_mask) {
+              const int qq = q0 + ql0 + u;
+              bool ok = (kj <= qq) && (qq < S) && kvalid;
+              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
+              if (!ok) p = 0.f;
+            }
+            pf[2 * qb + (r >> 3)][r & 7] = (__bf16)p;
+            sf[2 * qb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[qb][r] - d4[u]));
+          }
+        }
+      const char* qt = cur + 2 * C::kNatBytes;
+      const char* dt = qt + C::kTBytes;
+#pragma unroll
+      for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+          dva[db] = mfma32(t_frag(dt, 32 * db + col, ks, hf), pf[ks], dva[db]);
+          dka[db] = mfma32(t_frag(qt, 32 * db + col, ks, hf), sf[ks], dka[db]);
+        }
+    }
+    if (more) store_tile(lds + ((it + 1) & 1) * kStage);
+    __syncthreads();
+  }
+
+  if (kvalid) {
+    bf16_t* ko = dk + (krow + kj) * DH;
+    bf16_t* vo = dv + (krow + kj) * DH;
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        *reinterpret_cast<u32x2*>(ko + d) =
+            u32x2{pack_bf16x2(dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale),
+                  pack_bf16x2(dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale)};
+        *reinterpret_cast<u32x2*>(vo + d) = u32x2{pack_bf16x2(dva[db][4 * rq], dva[db][4 * rq + 1]),
+                                                  pack_bf16x2(dva[db][4 * rq + 2], dva[db][4 * rq + 3])};
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Launchers
+// ------------------------------------------------------------------------------------------
+namespace {
+int fwd_grid(const AttnShape& sh) {
+  const int G = sh.hq / sh.hkv;
+  const int hpw = (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1);
+  const int P = 32 * (4 / hpw);
+  return ((sh.s + P - 1) / P) * sh.b * (sh.hq / hpw);
+}
+
+template <int DH>
+hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v, const int32_t* sid,
+                  const int32_t* sst, bf16_t* o, float* lse, hipStream_t st) {
+  const float sl2 = sh.scale * kLog2e;
+  dim3 grid(fwd_grid(sh)), block(256);
+  if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
+  else hipLaunchKernelGGL((attn_fwd_kernel<DH, false>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
+  return hipGetLastError();
+}
+
+template <int DH>
+hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
+                  const float* lse, const bf16_t* d_o, const int32_t* sid, const int32_t* sst, bf16_t* dq,
+                  bf16_t* dk, bf16_t* dv, float* dvec, hipStream_t st) {
+  const long rows = (long)sh.b * sh.hq * sh.s;
+  dim3 block(256);
+  hipLaunchKernelGGL(attn_bwd_dvec_kernel<DH>, dim3((unsigned)((rows + 31) / 32)), block, 0, st, o, d_o, dvec, rows);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const float sl2 = sh.scale * kLog2e;
+  dim3 qgrid(fwd_grid(sh));
+  if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
+  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_attn_fwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,
+                           const int32_t* seg_id, const int32_t* seg_start, bf16_t* o, float* lse,
+                           hipStream_t stream) {
+  switch (sh.dh) {
+    case 64: return fwd_dh<64>(sh, q, k, v, seg_id, seg_start, o, lse, stream);
+    case 96: return fwd_dh<96>(sh, q, k, v, seg_id, seg_start, o, lse, stream);
+    case 128: return fwd_dh<128>(sh, q, k, v, seg_id, seg_start, o, lse, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_attn_bwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,
+                           const bf16_t* o, const float* lse, const bf16_t* d_o, const int32_t* seg_id,
+                           const int32_t* seg_start, bf16_t* dq, bf16_t* dk, bf16_t* dv, float* dvec,
+                           hipStream_t stream) {
+  switch (sh.dh) {
+    case 64: return bwd_dh<64>(sh, q, k, v, o, lse, d_o, seg_id, seg_start, dq, dk, dv, dvec, stream);
+    case 96: return bwd_dh<96>(sh, q, k, v, o, lse, d_o, seg_id, seg_start, dq, dk, dv, dvec, stream);
+    case 128: return bwd_dh<128>(sh, q, k, v, o, lse, d_o, seg_id, seg_start, dq, dk, dv, dvec, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace mtp

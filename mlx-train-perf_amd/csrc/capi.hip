@@ -1,0 +1,204 @@
+// C-ABI entry points: argument validation, workspace planning and launch.
+// Every function validates shapes, alignment and workspace before any launch and reports a
+// negative MTP_ERR_* code with a thread-local message; nothing here allocates device memory or
+// synchronizes the host.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "../../include/mtp_hip.h"
+#include "mtp_launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return MTP_OK;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr int64_t kMaxDim = (int64_t(1) << 31) - 1;
+constexpr int64_t kTile = 256;
+
+size_t lce_fwd_ws(int64_t n, int64_t v) {
+  return (size_t)2 * (size_t)mtp::lce_fwd_nsplit(n, v) * (size_t)n * sizeof(float);
+}
+
+int check_lce_common(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
+                     const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                     int32_t head_kind) {
+  if (n < 1 || d < 1 || v < 1) return fail(MTP_ERR_INPUT, "n, d, v must be >= 1 (got n=%lld d=%lld v=%lld)", (long long)n, (long long)d, (long long)v);
+  if (n > kMaxDim || d > kMaxDim || v > kMaxDim) return fail(MTP_ERR_INPUT, "n, d, v must each be < 2^31");
+  if (!hidden || !targets) return fail(MTP_ERR_INPUT, "hidden and targets must be non-null");
+  if (!aligned16(hidden)) return fail(MTP_ERR_UNSUPPORTED, "hidden must be 16-byte aligned");
+  if (head_kind == MTP_HEAD_DENSE) {
+    if (!w) return fail(MTP_ERR_INPUT, "dense head: w must be non-null");
+    if (!aligned16(w)) return fail(MTP_ERR_UNSUPPORTED, "dense head: w must be 16-byte aligned");
+    if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires d %% 8 == 0 for a dense head (got d=%lld); use impl='chunked'", (long long)d);
+  } else if (head_kind == MTP_HEAD_Q4) {
+    if (!w_q || !scales || !biases) return fail(MTP_ERR_INPUT, "quantized head: w_q, scales and biases must be non-null");
+    if (!aligned16(w_q)) return fail(MTP_ERR_UNSUPPORTED, "quantized head: w_q must be 16-byte aligned");
+    if (d % 64 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires the quantized head's hidden dim to be a multiple of 64 (got d=%lld); use impl='chunked'", (long long)d);
+  } else {
+    return fail(MTP_ERR_UNSUPPORTED, "unknown head_kind %d", (int)head_kind);
+  }
+  return MTP_OK;
+}
+
+mtp::LceHead make_head(const void* w, const uint32_t* w_q, const void* scales, const void* biases, int32_t head_kind) {
+  mtp::LceHead h;
+  h.q4 = head_kind == MTP_HEAD_Q4;
+  h.w = static_cast<const mtp::bf16_t*>(w);
+  h.wq = w_q;
+  h.sc = static_cast<const mtp::bf16_t*>(scales);
+  h.bi = static_cast<const mtp::bf16_t*>(biases);
+  return h;
+}
+
+int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+int check_attn(const void* q, const void* k, const void* v, int64_t b, int64_t hq, int64_t hkv, int64_t s,
+               int64_t dh, int32_t causal, const int32_t* seg_id, const int32_t* seg_start) {
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1) return fail(MTP_ERR_INPUT, "b, hq, hkv, s must be >= 1");
+  if (hq % hkv != 0) return fail(MTP_ERR_INPUT, "Hq=%lld must be a multiple of Hkv=%lld for GQA grouping", (long long)hq, (long long)hkv);
+  if (b * hq * s > kMaxDim || s > (int64_t(1) << 24)) return fail(MTP_ERR_INPUT, "b*hq*s must be < 2^31 and s < 2^24");
+  if (dh != 64 && dh != 96 && dh != 128) return fail(MTP_ERR_UNSUPPORTED, "kernel impl only supports head_dim in (64, 96, 128) (got %lld); use impl='reference'", (long long)dh);
+  if (!causal) return fail(MTP_ERR_UNSUPPORTED, "kernel impl only supports causal=True (got causal=False); use impl='reference'");
+  if ((seg_id == nullptr) != (seg_start == nullptr)) return fail(MTP_ERR_INPUT, "seg_id and seg_start must be both given or both null");
+  if (!q || !k || !v) return fail(MTP_ERR_INPUT, "q, k, v must be non-null");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(MTP_ERR_UNSUPPORTED, "q, k, v must be 16-byte aligned");
+  return MTP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mtp_last_error(void) { return g_err; }
+
+int mtp_abi_version(void) { return MTP_ABI_VERSION; }
+
+size_t mtp_lce_fwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind) {
+  (void)d;
+  (void)head_kind;
+  if (n < 1 || v < 1) return 0;
+  return lce_fwd_ws(n, v);
+}
+
+int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,
+                const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
+                float* nll, float* lse, float* tgt, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
+  if (rc) return rc;
+  if (!nll || !lse || !tgt) return fail(MTP_ERR_INPUT, "nll, lse, tgt outputs must be non-null");
+  const size_t need = lce_fwd_ws(n, v);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "lce forward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  hipError_t e = mtp::launch_lce_fwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
+                                     targets, (int)n, (int)d, (int)v, (long long)ignore_index, nll, lse, tgt,
+                                     static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+  if (n < 1 || d < 1 || v < 1) return 0;
+  const int64_t vpad = round_up(v, kTile);
+  // One chunk if the whole padded vocab fits the budget; otherwise the budget also carries the
+  // fp32 dH accumulator.
+  if ((size_t)n * (size_t)vpad * 2 <= budget_bytes) return vpad;
+  const size_t acc = (size_t)n * (size_t)d * 4;
+  const size_t rest = budget_bytes > acc ? budget_bytes - acc : 0;
+  int64_t c = (int64_t)(rest / ((size_t)n * 2)) / kTile * kTile;
+  if (c < kTile) c = kTile;
+  if (c > vpad) c = vpad;
+  return c;
+}
+
+size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk) {
+  (void)head_kind;
+  if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
+  const int64_t nchunks = (v + chunk - 1) / chunk;
+  size_t bytes = (size_t)n * (size_t)chunk * 2;
+  if (nchunks > 1) bytes += (size_t)n * (size_t)d * 4;
+  return bytes;
+}
+
+int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,
+                const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
+                const float* lse, const float* d_nll, void* d_hidden, int64_t chunk, void* workspace,
+                size_t workspace_bytes, void* stream) {
+  int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
+  if (rc) return rc;
+  if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
+  if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
+  if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
+  const size_t need = mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "lce backward needs a workspace of %zu bytes at chunk=%lld (got %zu)", need, (long long)chunk, workspace ? workspace_bytes : (size_t)0);
+  if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
+  mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
+  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)n * (size_t)chunk * 2);
+  hipError_t e = mtp::launch_lce_bwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
+                                     targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
+                                     static_cast<mtp::bf16_t*>(d_hidden), gbuf, acc32, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t hq, int64_t hkv, int64_t s,
+                 int64_t dh, float scale, int32_t causal, const int32_t* seg_id, const int32_t* seg_start, void* o,
+                 float* lse, void* stream) {
+  int rc = check_attn(q, k, v, b, hq, hkv, s, dh, causal, seg_id, seg_start);
+  if (rc) return rc;
+  if (!o || !lse) return fail(MTP_ERR_INPUT, "o and lse must be non-null");
+  if (!aligned16(o)) return fail(MTP_ERR_UNSUPPORTED, "o must be 16-byte aligned");
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale};
+  hipError_t e = mtp::launch_attn_fwd(sh, static_cast<const mtp::bf16_t*>(q), static_cast<const mtp::bf16_t*>(k),
+                                      static_cast<const mtp::bf16_t*>(v), seg_id, seg_start,
+                                      static_cast<mtp::bf16_t*>(o), lse, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "attention forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh) {
+  (void)hkv;
+  (void)dh;
+  if (b < 1 || hq < 1 || s < 1) return 0;
+  return (size_t)b * (size_t)hq * (size_t)s * sizeof(float);
+}
+
+int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* d_o,
+                 int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh, float scale, int32_t causal,
+                 const int32_t* seg_id, const int32_t* seg_start, void* d_q, void* d_k, void* d_v, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  int rc = check_attn(q, k, v, b, hq, hkv, s, dh, causal, seg_id, seg_start);
+  if (rc) return rc;
+  if (!o || !lse || !d_o || !d_q || !d_k || !d_v) return fail(MTP_ERR_INPUT, "o, lse, d_o, d_q, d_k, d_v must be non-null");
+  if (!aligned16(o) || !aligned16(d_o) || !aligned16(d_q) || !aligned16(d_k) || !aligned16(d_v))
+    return fail(MTP_ERR_UNSUPPORTED, "o, d_o, d_q, d_k, d_v must be 16-byte aligned");
+  const size_t need = mtp_attn_bwd_workspace_bytes(b, hq, hkv, s, dh);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "attention backward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale};
+  hipError_t e = mtp::launch_attn_bwd(sh, static_cast<const mtp::bf16_t*>(q), static_cast<const mtp::bf16_t*>(k),
+                                      static_cast<const mtp::bf16_t*>(v), static_cast<const mtp::bf16_t*>(o), lse,
+                                      static_cast<const mtp::bf16_t*>(d_o), seg_id, seg_start,
+                                      static_cast<mtp::bf16_t*>(d_q), static_cast<mtp::bf16_t*>(d_k),
+                                      static_cast<mtp::bf16_t*>(d_v), static_cast<float*>(workspace),
+                                      static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "attention backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+// Internal launcher interface between the HIP kernel translation units and the C-ABI.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mtp {
+
+typedef uint16_t bf16_t;
+
+// MI355X has 256 compute units in 8 XCDs; launch geometry is a pure function of the problem
+// shape so that results do not depend on the device a call lands on.
+constexpr int kNumCU = 256;
+
+struct LceHead {
+  int q4;                 // 0: dense bf16 [V][D]; 1: 4-bit affine, group size 64
+  const bf16_t* w;        // dense weight
+  const uint32_t* wq;     // packed nibbles [V][D/8]
+  const bf16_t* sc;       // scales [V][D/64]
+  const bf16_t* bi;       // biases [V][D/64]
+};
+
+int lce_fwd_nsplit(long N, long V);
+
+hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
+                          long long ignore_index, float* nll, float* lse, float* tgt, float* ws,
+                          hipStream_t stream);
+
+hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
+                          const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
+                          bf16_t* dH, bf16_t* Gbuf, float* acc32, hipStream_t stream);
+
+struct AttnShape {
+  int b, hq, hkv, s, dh;
+  float scale;
+};
+
+hipError_t launch_attn_fwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,
+                           const int32_t* seg_id, const int32_t* seg_start, bf16_t* o, float* lse,
+                           hipStream_t stream);
+
+hipError_t launch_attn_bwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,
+                           const bf16_t* o, const float* lse, const bf16_t* d_o, const int32_t* seg_id,
+                           const int32_t* seg_start, bf16_t* dq, bf16_t* dk, bf16_t* dv, float* dvec,
+                           hipStream_t stream);
+
+}  // namespace mtp

@@ -1,0 +1,306 @@
+"""Public loss API: HeadRef seam, impl resolution, autograd wiring (mirror of
+src/mlx_train_perf/core/loss.py on torch tensors).
+
+Residual contract (loss.py:1-7): the kernel autograd Function returns (nll_rows, lse, tgt); only
+`lse` is saved for the backward; this public wrapper consumes nll_rows and applies `reduction`
+outside the Function. Aux outputs never leak.
+
+MI355X specifics:
+- `impl="kernel"` (and `"auto"`) runs the HIP kernels of libmtp_hip.so: the logit-free forward and
+  the chunked-recompute dL/dH backward. Hidden and dense weights must be bf16 on a gfx950 device.
+- `ignore_index` (default -100): ignored rows get nll = 0, a zero gradient, and are excluded from
+  `reduction="mean"`, which is exactly the trainer adapter's `(nll * mask).sum() / ntoks`
+  (adapters/mlx_lm.py:212-216). With no ignored rows every reduction equals the reference's.
+- No silent fallback: an unsupported config raises the reference's typed errors.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+
+from mlx_train_perf import _compat, _native
+from mlx_train_perf.core import chunked as _chunked
+from mlx_train_perf.core.naive import naive_linear_ce
+from mlx_train_perf.core.quant import dequantize
+from mlx_train_perf.errors import LossInputError, UnsupportedHeadError
+from mlx_train_perf.plan import launch as _plan
+
+# The MI355X kernels compute in bf16 MFMA with fp32 accumulation.
+_KERNEL_DTYPES = (torch.bfloat16,)
+_KERNEL_ROW_TILE = 256  # token rows per workgroup tile (reported as Resolution.row_tiles)
+_DEFAULT_CHUNK = 8192   # chunked-impl vocab chunk (the reference's kernel tile, loss.py:25)
+
+
+@dataclass(frozen=True, slots=True, kw_only=True)
+class DenseHead:
+    weight: torch.Tensor      # (V, D); tied embeddings pass the same tensor
+    trainable: bool = True
+
+
+@dataclass(frozen=True, slots=True, kw_only=True)
+class QuantizedHead:
+    w_q: torch.Tensor         # int32 bit patterns of uint32 words (V, D/8)
+    scales: torch.Tensor      # (V, D/64)
+    biases: torch.Tensor      # (V, D/64)
+    group_size: int = 64
+    bits: int = 4             # frozen by definition -- no d_head path exists
+
+
+HeadRef = DenseHead | QuantizedHead
+
+
+def tied_head(embedding_weight: torch.Tensor, *, trainable: bool = False) -> DenseHead:
+    return DenseHead(weight=embedding_weight, trainable=trainable)
+
+
+@dataclass(frozen=True, slots=True, kw_only=True)
+class Resolution:
+    impl: Literal["kernel", "chunked", "naive"]
+    row_tiles: int | None
+    provisional: bool
+    reason: str
+
+
+def _quantized_head_d(head: QuantizedHead) -> int:
+    return head.w_q.shape[-1] * (32 // head.bits)
+
+
+def _require_kernel_supported(*, head: HeadRef, dtype: torch.dtype) -> None:
+    """Structural gate for the kernel impl (reference loss.py:65-91): raises UnsupportedHeadError,
+    naming the 'chunked' alternative, for any head/dtype combination the kernel cannot serve."""
+    if dtype not in _KERNEL_DTYPES:
+        raise UnsupportedHeadError(
+            f"kernel impl on MI355X supports bf16 hidden states (got {dtype}); use impl='chunked' "
+            "for other dtypes."
+        )
+    if isinstance(head, QuantizedHead):
+        if head.bits != 4:
+            raise UnsupportedHeadError(
+                f"kernel impl only supports 4-bit quantized heads (got bits={head.bits}); "
+                "use impl='chunked' for other bit widths."
+            )
+        if head.group_size != 64:
+            raise UnsupportedHeadError(
+                "kernel impl only supports group_size=64 quantized heads (got "
+                f"group_size={head.group_size}); use impl='chunked' for other group sizes."
+            )
+        d = _quantized_head_d(head)
+        if d % 64 != 0:
+            raise UnsupportedHeadError(
+                "kernel impl requires the quantized head's hidden dim to be a multiple of "
+                f"64 (got d={d}); use impl='chunked'."
+            )
+    else:
+        d = head.weight.shape[-1]
+        if d % 8 != 0:
+            raise UnsupportedHeadError(
+                f"kernel impl requires the hidden dim to be a multiple of 8 (got d={d}); use impl='chunked'."
+            )
+        if head.trainable:
+            raise UnsupportedHeadError(
+                "kernel impl on MI355X serves frozen heads (LoRA/QLoRA): dL/dW is not built; pass "
+                "DenseHead(weight=..., trainable=False) or use impl='chunked' for a trainable head."
+            )
+
+
+def resolve_impl(*, head: HeadRef, dtype: torch.dtype, n: int, impl: str = "auto",
+                 allow_unverified_mlx: bool = False) -> Resolution:
+    """Resolve `auto|kernel|chunked|naive` (reference loss.py:94-123). `auto` and `kernel` resolve
+    identically and never fall back; `allow_unverified_mlx` relaxes the device-architecture gate
+    (the MI355X analogue of the reference's mlx version gate)."""
+    if n <= 0:
+        raise LossInputError(f"n must be positive (hidden's row count); got n={n}")
+    if impl == "chunked":
+        return Resolution(impl="chunked", row_tiles=None, provisional=False, reason="explicit impl='chunked' opt-in")
+    if impl == "naive":
+        return Resolution(impl="naive", row_tiles=None, provisional=False, reason="explicit impl='naive' opt-in")
+    if impl not in ("auto", "kernel"):
+        raise LossInputError(f"unknown impl {impl!r}; expected one of 'auto', 'kernel', 'chunked', 'naive'")
+    _require_kernel_supported(head=head, dtype=dtype)
+    _compat.check_device_verified(allow_unverified=allow_unverified_mlx, error=UnsupportedHeadError)
+    plan = _plan.lce_plan(n=n, v=_head_v(head))
+    reason = (f"kernel: {_KERNEL_ROW_TILE}-row x 256-vocab MFMA tiles, {plan.fwd_splits} vocab splits "
+              f"for n={n}")
+    return Resolution(impl="kernel", row_tiles=_KERNEL_ROW_TILE, provisional=False, reason=reason)
+
+
+def _head_v(head: HeadRef) -> int:
+    return head.weight.shape[0] if isinstance(head, DenseHead) else head.w_q.shape[0]
+
+
+def _validate_inputs(*, hidden: torch.Tensor, head: HeadRef, targets: torch.Tensor, validate_targets: bool,
+                     ignore_index: int) -> None:
+    """Reference loss.py:126-186, plus the ignore_index exemption in the range check."""
+    if hidden.dim() not in (2, 3):
+        raise LossInputError(f"hidden must be 2D (N,D) or 3D (B,S,D), got shape {tuple(hidden.shape)}")
+    leading = tuple(hidden.shape[:-1])
+    n_total = 1
+    for size in leading:
+        n_total *= size
+    if n_total <= 0:
+        raise LossInputError(f"hidden must have at least one row, got leading dims {leading}")
+    if tuple(targets.shape) != leading:
+        raise LossInputError(f"targets shape {tuple(targets.shape)} must match hidden's leading dims {leading}")
+    if targets.dtype.is_floating_point or targets.dtype.is_complex or targets.dtype == torch.bool:
+        raise LossInputError(f"targets must be an integer dtype, got {targets.dtype}")
+    d = hidden.shape[-1]
+    if isinstance(head, DenseHead):
+        if head.weight.dim() != 2 or head.weight.shape[-1] != d:
+            raise LossInputError(f"head.weight's last dim ({head.weight.shape[-1]}) must match hidden's D ({d})")
+        if hidden.dtype != head.weight.dtype:
+            raise LossInputError(
+                f"hidden dtype {hidden.dtype} must match dense head weight dtype {head.weight.dtype}"
+            )
+        v = head.weight.shape[0]
+    else:
+        head_d = _quantized_head_d(head)
+        if head_d != d:
+            raise LossInputError(
+                f"quantized head implies D={head_d} (from w_q shape and bits), which does not match hidden's D={d}"
+            )
+        v = head.w_q.shape[0]
+    if validate_targets:
+        # A host sync, skipped on the trusted training path (validate_targets=False).
+        valid = targets[targets != ignore_index]
+        if valid.numel():
+            tmin = int(valid.min().item())
+            tmax = int(valid.max().item())
+            if tmin < 0 or tmax >= v:
+                raise LossInputError(f"targets must satisfy 0 <= t < V={v} (or equal ignore_index); got range [{tmin}, {tmax}]")
+
+
+def _reduce(nll: torch.Tensor, *, reduction: str, leading: tuple[int, ...], targets2: torch.Tensor,
+            ignore_index: int) -> torch.Tensor:
+    if reduction == "none":
+        return nll.reshape(leading)
+    if reduction == "mean":
+        valid = (targets2 != ignore_index)
+        return nll.sum() / valid.sum().clamp(min=1).to(nll.dtype)
+    return nll.sum()
+
+
+def _mask_ignored(nll: torch.Tensor, targets2: torch.Tensor, ignore_index: int) -> torch.Tensor:
+    return torch.where(targets2 == ignore_index, torch.zeros_like(nll), nll)
+
+
+def _naive_nll(hidden2, head, targets2, ignore_index):
+    safe = torch.where(targets2 == ignore_index, torch.zeros_like(targets2), targets2)
+    if isinstance(head, DenseHead):
+        w = head.weight if head.trainable else head.weight.detach()
+        nll = naive_linear_ce(hidden2, w, safe)
+    else:
+        w = dequantize(head.w_q, head.scales, head.biases, group_size=head.group_size, bits=head.bits,
+                       dtype=hidden2.dtype)
+        nll = naive_linear_ce(hidden2, w, safe)
+    return _mask_ignored(nll, targets2, ignore_index)
+
+
+def _chunked_nll(hidden2, head, targets2, ignore_index, chunk_size):
+    safe = torch.where(targets2 == ignore_index, torch.zeros_like(targets2), targets2).long()
+    if isinstance(head, DenseHead):
+        w = head.weight if head.trainable else head.weight.detach()
+        nll = _chunked.make_chunked_dense(chunk_size)(hidden2, w, safe)
+    else:
+        q = _chunked.QuantSpec(w_q=head.w_q, scales=head.scales, biases=head.biases,
+                               group_size=head.group_size, bits=head.bits)
+        nll = _chunked.make_chunked_quantized(chunk_size, q)(hidden2, safe)
+    return _mask_ignored(nll, targets2, ignore_index)
+
+
+VJP_CALLS: dict[str, int] = {}
+
+
+class _KernelLCE(torch.autograd.Function):
+    """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only."""
+
+    @staticmethod
+    def forward(ctx, hidden2, targets2, w, w_q, scales, biases, head_kind, ignore_index, bwd_chunk):
+        lib = _native.load()
+        n, d = hidden2.shape
+        v = w.shape[0] if head_kind == _native.HEAD_DENSE else w_q.shape[0]
+        dev = hidden2.device
+        nll = torch.empty(n, dtype=torch.float32, device=dev)
+        lse = torch.empty(n, dtype=torch.float32, device=dev)
+        tgt = torch.empty(n, dtype=torch.float32, device=dev)
+        ws_bytes = lib.mtp_lce_fwd_workspace_bytes(n, d, v, head_kind)
+        ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+        rc = lib.mtp_lce_fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
+                             _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ignore_index,
+                             nll.data_ptr(), lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), ws_bytes,
+                             _native.stream_of(hidden2))
+        _native.check(rc, domain="loss")
+        ctx.save_for_backward(hidden2, targets2, lse)
+        ctx.head = (w, w_q, scales, biases, head_kind, v)
+        ctx.ignore_index = ignore_index
+        ctx.bwd_chunk = bwd_chunk
+        ctx.mark_non_differentiable(lse, tgt)
+        return nll, lse, tgt
+
+    @staticmethod
+    def backward(ctx, d_nll, _d_lse, _d_tgt):
+        VJP_CALLS["kernel"] = VJP_CALLS.get("kernel", 0) + 1
+        lib = _native.load()
+        hidden2, targets2, lse = ctx.saved_tensors
+        w, w_q, scales, biases, head_kind, v = ctx.head
+        n, d = hidden2.shape
+        chunk = ctx.bwd_chunk or lib.mtp_lce_bwd_chunk(n, d, v, _plan.lce_bwd_budget_bytes())
+        chunk = min(max(256, (chunk + 255) // 256 * 256), (v + 255) // 256 * 256)
+        ws_bytes = lib.mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
+        d_hidden = torch.empty_like(hidden2)
+        ct = d_nll.to(torch.float32).contiguous()
+        rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
+                             _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ctx.ignore_index,
+                             lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(), chunk, ws.data_ptr(), ws_bytes,
+                             _native.stream_of(hidden2))
+        _native.check(rc, domain="loss")
+        return d_hidden, None, None, None, None, None, None, None, None
+
+
+def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor, *, ignore_index: int = -100,
+                         bwd_chunk: int | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """(nll, lse, tgt) from the kernel impl, differentiable in hidden2 through `nll` (test/bench seam)."""
+    _compat.require_gpu_tensor(hidden2, error=UnsupportedHeadError)
+    h = hidden2.contiguous()
+    t = targets2.to(torch.int64).contiguous()
+    if isinstance(head, DenseHead):
+        args = (head.weight.detach().contiguous(), None, None, None, _native.HEAD_DENSE)
+    else:
+        args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
+    return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0))
+
+
+def linear_cross_entropy(
+    hidden: torch.Tensor,
+    head: HeadRef,
+    targets: torch.Tensor,
+    *,
+    impl: Literal["auto", "kernel", "chunked", "naive"] = "auto",
+    chunk_size: int | None = None,
+    reduction: Literal["none", "mean", "sum"] = "mean",
+    allow_unverified_mlx: bool = False,
+    validate_targets: bool = True,
+    ignore_index: int = -100,
+) -> torch.Tensor:
+    """Fused linear cross-entropy of `hidden @ head.T` against `targets` (reference loss.py:358-392).
+
+    `chunk_size`: vocab chunk of the chunked impl; for the kernel impl, the backward's vocab chunk
+    (rounded up to a multiple of 256; default: planned from the workspace budget)."""
+    if reduction not in ("none", "mean", "sum"):
+        raise LossInputError(f"unknown reduction {reduction!r}; expected 'none', 'mean', or 'sum'")
+    _validate_inputs(hidden=hidden, head=head, targets=targets, validate_targets=validate_targets,
+                     ignore_index=ignore_index)
+    leading = tuple(hidden.shape[:-1])
+    hidden2 = hidden.reshape(-1, hidden.shape[-1])
+    targets2 = targets.reshape(-1)
+    n = hidden2.shape[0]
+    res = resolve_impl(head=head, dtype=hidden2.dtype, n=n, impl=impl, allow_unverified_mlx=allow_unverified_mlx)
+    if res.impl == "naive":
+        nll = _naive_nll(hidden2, head, targets2, ignore_index)
+    elif res.impl == "chunked":
+        nll = _chunked_nll(hidden2, head, targets2, ignore_index, _DEFAULT_CHUNK if chunk_size is None else chunk_size)
+    else:
+        nll, _, _ = kernel_forward_parts(hidden2, head, targets2, ignore_index=ignore_index, bwd_chunk=chunk_size)
+    return _reduce(nll, reduction=reduction, leading=leading, targets2=targets2, ignore_index=ignore_index)

@@ -1,0 +1,98 @@
+"""Launch planning for the LCE and attention kernels (pure integer math, CPU-testable).
+
+The reference plans Metal dispatches against a GPU-watchdog time budget
+(core/kernel/launch.py:63-72; attention/kernel/launch.py:160-299). On MI355X there is no display
+watchdog on compute queues, so every op is one launch sequence and the planner's job is geometry and
+workspace: how many vocab splits the LCE forward uses, how wide a backward vocab chunk may be for a
+workspace budget, and the attention grid. The integer formulas here mirror the C-ABI's
+(mlx-train-perf_amd/csrc/lce_kernels.hip lce_fwd_nsplit; capi.hip mtp_lce_bwd_chunk) so that plans
+can be checked and sized on the CPU; a GPU test asserts they agree with the library.
+"""
+from __future__ import annotations
+
+import os
+from dataclasses import dataclass
+
+NUM_CU = 256        # MI355X compute units (8 XCDs x 32)
+TILE = 256          # LCE workgroup tile edge (rows and vocab columns)
+ATTN_TILE = 64      # attention key/query tile
+DEFAULT_LCE_BWD_BUDGET = 1 << 30  # bytes of backward workspace (bf16 gradient chunk + fp32 dH)
+
+
+def lce_bwd_budget_bytes() -> int:
+    return int(os.environ.get("MTP_LCE_BWD_BUDGET", DEFAULT_LCE_BWD_BUDGET))
+
+
+def causal_pairs(n: int) -> int:
+    """Exact (query, key) pairs under a causal mask (attention/kernel/launch.py:160-168)."""
+    return n * (n + 1) // 2
+
+
+def packed_pairs(lengths: list[int]) -> int:
+    """Visible pairs of a block-diagonal causal (packed) layout."""
+    return sum(causal_pairs(n) for n in lengths)
+
+
+def lce_fwd_splits(n: int, v: int) -> int:
+    rtiles = -(-n // TILE)
+    vtiles = -(-v // TILE)
+    ns = -(-NUM_CU // rtiles)
+    if ns >= 8:
+        ns = -(-ns // 8) * 8
+    return max(1, min(ns, vtiles))
+
+
+def lce_fwd_workspace_bytes(n: int, v: int) -> int:
+    return 2 * lce_fwd_splits(n, v) * n * 4
+
+
+def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
+    vpad = -(-v // TILE) * TILE
+    if n * vpad * 2 <= budget:
+        return vpad
+    acc = n * d * 4
+    rest = max(budget - acc, 0)
+    c = (rest // (n * 2)) // TILE * TILE
+    return min(max(c, TILE), vpad)
+
+
+def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int) -> int:
+    nchunks = -(-v // chunk)
+    return n * chunk * 2 + (n * d * 4 if nchunks > 1 else 0)
+
+
+@dataclass(frozen=True)
+class LcePlan:
+    fwd_splits: int
+    fwd_workspace_bytes: int
+    bwd_chunk: int
+    bwd_chunks: int
+    bwd_workspace_bytes: int
+
+
+def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None) -> LcePlan:
+    b = lce_bwd_budget_bytes() if budget is None else budget
+    chunk = lce_bwd_chunk(n, d, v, b)
+    return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=lce_fwd_workspace_bytes(n, v),
+                   bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
+                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk))
+
+
+def attn_heads_per_workgroup(hq: int, hkv: int) -> int:
+    g = hq // hkv
+    return 4 if g % 4 == 0 else (2 if g % 2 == 0 else 1)
+
+
+@dataclass(frozen=True)
+class AttnPlan:
+    heads_per_workgroup: int
+    fwd_workgroups: int
+    dkv_workgroups: int
+    bwd_workspace_bytes: int
+
+
+def attn_plan(*, b: int, hq: int, hkv: int, s: int) -> AttnPlan:
+    hpw = attn_heads_per_workgroup(hq, hkv)
+    p = 32 * (4 // hpw)
+    return AttnPlan(heads_per_workgroup=hpw, fwd_workgroups=-(-s // p) * b * (hq // hpw),
+                    dkv_workgroups=-(-s // 128) * b * hkv, bwd_workspace_bytes=b * hq * s * 4)

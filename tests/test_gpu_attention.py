@@ -1,0 +1,111 @@
+"""GPU parity of the flash-attention kernels against the CPU oracle (oracle/attention.py).
+
+Tolerances (north star): attention outputs and gradients within 1e-2 relative-L2 in bf16; the
+reference's forward pin for bf16 O (tests/test_attention_kernel_fwd.py:459-466, 1.2e-2 max-abs) is
+also asserted, and L within 2e-3 absolute (fp32 logsumexp of bf16-input scores).
+"""
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+from oracle import attention as oatt
+from tests._inputs import attn_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [  # (b, hq, hkv, s, d)
+    (1, 4, 4, 64, 64),
+    (1, 4, 2, 61, 64),
+    (2, 4, 2, 257, 128),
+    (1, 32, 8, 64, 128),
+    (1, 4, 1, 130, 96),
+    (1, 8, 2, 300, 128),
+    (1, 6, 2, 200, 128),
+]
+
+
+def _segs(lengths, b=1):
+    sid, sst = oatt.segments_from_lengths(lengths)
+    return sid[None].repeat(b, 1), sst[None].repeat(b, 1)
+
+
+def _run_kernel(q, k, v, do, scale, seg=None):
+    from mlx_train_perf.attention.api import kernel_backward, kernel_forward
+
+    qd, kd, vd, dod = (x.cuda().contiguous() for x in (q, k, v, do))
+    sid = sst = None
+    if seg is not None:
+        sid, sst = (x.cuda().contiguous() for x in seg)
+    o, lse = kernel_forward(qd, kd, vd, scale=scale, seg_id=sid, seg_start=sst)
+    dq, dk, dv = kernel_backward(qd, kd, vd, o, lse, dod, scale=scale, seg_id=sid, seg_start=sst)
+    torch.cuda.synchronize()
+    return [x.cpu() for x in (o, lse, dq, dk, dv)]
+
+
+def _check(res, q, k, v, do, scale, seg_id=None):
+    o, lse, dq, dk, dv = res
+    oo, ol = oatt.attention_forward(q, k, v, scale=scale, seg_id=seg_id, dtype=torch.float64)
+    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, seg_id=seg_id, dtype=torch.float64)
+    assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
+    assert rel_l2(o, oo) <= 1e-2
+    assert (o.double() - oo).abs().max() <= 1.2e-2 * max(1.0, oo.abs().max().item())
+    assert (lse.double() - ol).abs().max() <= 2e-3
+    for got, want in ((dq, odq), (dk, odk), (dv, odv)):
+        assert torch.isfinite(got.float()).all()
+        assert rel_l2(got, want) <= 1e-2
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_causal_parity(shape):
+    b, hq, hkv, s, d = shape
+    print(f"[attn causal] {shape}", flush=True)
+    q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=s + d)
+    scale = 1.0 / math.sqrt(d)
+    _check(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
+
+
+@pytest.mark.parametrize(("lengths", "hq", "hkv", "d"), [
+    ([3, 5, 56], 4, 2, 64),
+    ([100, 37, 120], 4, 1, 128),
+    ([64, 64, 64, 64], 8, 2, 128),
+    ([1, 200, 9, 90], 4, 4, 96),
+])
+def test_packed_parity(lengths, hq, hkv, d):
+    print(f"[attn packed] {lengths} hq={hq} hkv={hkv} d={d}", flush=True)
+    s = sum(lengths)
+    q, k, v, do = attn_inputs(1, hq, hkv, s, d, seed=len(lengths) * 11 + d)
+    scale = 1.0 / math.sqrt(d)
+    seg = _segs(lengths)
+    _check(_run_kernel(q, k, v, do, scale, seg=seg), q, k, v, do, scale, seg_id=seg[0])
+
+
+def test_single_segment_packed_equals_causal_bitwise():
+    q, k, v, do = attn_inputs(1, 8, 2, 200, 128, seed=4)
+    scale = 1.0 / math.sqrt(128)
+    a = _run_kernel(q, k, v, do, scale)
+    b = _run_kernel(q, k, v, do, scale, seg=_segs([200]))
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_row0_closed_form():
+    # Row 0 attends only to itself: O[h, 0] = V[kv(h), 0], L[h, 0] = scale * q0 . k0
+    q, k, v, do = attn_inputs(1, 4, 2, 64, 64, seed=2)
+    scale = 0.125
+    o, lse, *_ = _run_kernel(q, k, v, do, scale)
+    for h in range(4):
+        kv = h // 2
+        assert torch.allclose(o[0, h, 0].float(), v[0, kv, 0].float(), atol=1e-2)
+        want = scale * (q[0, h, 0].double() @ k[0, kv, 0].double())
+        assert abs(lse[0, h, 0].item() - want.item()) <= 1e-3
+
+
+def test_deterministic_repeat():
+    q, k, v, do = attn_inputs(1, 8, 2, 300, 128, seed=8)
+    a = _run_kernel(q, k, v, do, 0.1)
+    b = _run_kernel(q, k, v, do, 0.1)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)

@@ -1,0 +1,115 @@
+"""GPU parity of the fused linear cross-entropy kernels against the CPU oracle (oracle/lce.py).
+
+Tolerances (north star): per-token loss within 2e-3 relative, d_hidden within 1e-2 relative-L2 in
+bf16. The reference's own pins are also checked where they apply: forward nll max-abs vs the
+fp32-exact naive 5e-6-class for bf16 inputs becomes an absolute 2e-3 band here because the MI355X
+kernel accumulates bf16 products on MFMA (fp32 accumulate) and the oracle runs in fp64; the backward
+max-abs pin of the reference (tests/test_kernel_backward_parity.py:85,154: 5e-3 in bf16) is kept.
+"""
+from __future__ import annotations
+
+import pytest
+import torch
+
+from oracle import lce as olce
+from oracle import quant as oquant
+from tests._inputs import lce_inputs, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+IGN = -100
+
+
+def _kernel(h, w, t, *, head="dense", chunk=None, wq=None, sc=None, bi=None):
+    from mlx_train_perf.core.loss import DenseHead, QuantizedHead, kernel_forward_parts
+
+    dev = "cuda"
+    hd = h.to(dev).requires_grad_(True)
+    if head == "dense":
+        hr = DenseHead(weight=w.to(dev), trainable=False)
+    else:
+        hr = QuantizedHead(w_q=wq.to(dev), scales=sc.to(dev), biases=bi.to(dev))
+    nll, lse, tgt = kernel_forward_parts(hd, hr, t.to(dev), ignore_index=IGN, bwd_chunk=chunk)
+    return hd, nll, lse, tgt
+
+
+def _cotangent(t, seed=5):
+    g = torch.Generator().manual_seed(seed)
+    return torch.rand(t.shape[0], generator=g) + 0.5  # non-uniform, like the adapter's masked mean
+
+
+@pytest.mark.parametrize(("n", "d", "v"), [(64, 64, 1024), (65, 192, 1027), (300, 512, 5000), (257, 128, 300),
+                                           (1024, 512, 32000)])
+def test_forward_parity_dense(n, d, v):
+    print(f"[lce fwd dense] n={n} d={d} v={v}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n + d + v)
+    _, nll, lse, tgt = _kernel(h, w, t)
+    onll, olse, otgt = olce.forward(h, w, t, ignore_index=IGN)
+    nll, lse, tgt = nll.cpu().double(), lse.cpu().double(), tgt.cpu().double()
+    assert torch.isfinite(lse).all()
+    assert (lse - olse).abs().max() <= 2e-3 * olse.abs().max()
+    assert ((nll - onll).abs() <= 2e-3 * onll.abs() + 1e-4).all()
+    assert ((tgt - otgt).abs() <= 1e-4 + 1e-4 * otgt.abs()).all()
+    ign = t == IGN
+    assert (nll[ign] == 0).all() and (tgt[ign] == 0).all()
+
+
+@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (65, 192, 1027, 256),
+                                                    (300, 512, 5000, 1024), (257, 128, 300, 256),
+                                                    (1024, 512, 32000, None), (512, 256, 9000, 2048)])
+def test_backward_parity_dense(n, d, v, chunk):
+    print(f"[lce bwd dense] n={n} d={d} v={v} chunk={chunk}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n * 7 + v)
+    hd, nll, lse, _ = _kernel(h, w, t, chunk=chunk)
+    ct = _cotangent(t)
+    nll.backward(ct.to("cuda"))
+    dh = hd.grad.cpu()
+    _, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(dh, odh) <= 1e-2
+    assert (dh.double() - odh).abs().max() <= 5e-3
+    assert (dh[t == IGN] == 0).all()
+
+
+@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (65, 192, 1027, 256),
+                                                    (300, 512, 5000, 1024)])
+def test_quantized_parity(n, d, v, chunk):
+    print(f"[lce q4] n={n} d={d} v={v} chunk={chunk}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=13 + n, w_std=0.05)
+    wq, sc, bi = oquant.quantize_affine(w.float(), group_size=64, scale_dtype=torch.bfloat16)
+    wdq = oquant.dequantize_affine(wq, sc, bi, group_size=64, dtype=torch.float32)
+    hd, nll, lse, tgt = _kernel(h, None, t, head="q4", chunk=chunk, wq=wq, sc=sc, bi=bi)
+    onll, olse, otgt = olce.forward(h, wdq, t, ignore_index=IGN)
+    # The kernel rounds dequantized weights to bf16 before MFMA (the reference's 8e-3 pin covers the
+    # same bf16-dequant effect, tests/test_kernel_quant_parity.py:54-64).
+    assert (nll.cpu().double() - onll).abs().max() <= 8e-3
+    ct = _cotangent(t)
+    nll.backward(ct.to("cuda"))
+    odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+
+
+def test_public_api_mean_matches_oracle():
+    from mlx_train_perf import DenseHead, linear_cross_entropy
+
+    h, w, t = lce_inputs(300, 256, 4000, seed=3)
+    hd = h.cuda().requires_grad_(True)
+    loss = linear_cross_entropy(hd, DenseHead(weight=w.cuda(), trainable=False), t.cuda(), reduction="mean")
+    loss.backward()
+    onll, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
+    valid = t != IGN
+    oloss = onll[valid].sum() / valid.sum()
+    assert abs(loss.item() - oloss.item()) <= 2e-3 * abs(oloss.item())
+    ct = valid.double() / valid.sum()
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+
+
+def test_deterministic_repeat():
+    h, w, t = lce_inputs(300, 256, 5000, seed=9)
+    outs = []
+    for _ in range(2):
+        hd, nll, lse, tgt = _kernel(h, w, t, chunk=1024)
+        nll.backward(torch.ones_like(nll))
+        outs.append((nll.detach().cpu(), hd.grad.cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
