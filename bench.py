@@ -1,0 +1,297 @@
+"""Bench harness: fused linear cross-entropy fwd+bwd on one MI355X, with the
+flash-attention (config 4, 5) and QLoRA (config 3) timings reported beside it.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+
+One step = one LCE forward + backward (dL/dH, frozen head) at N=8192 (batch 1 x seq 8192), D=4096,
+V=151936, bf16, synthetic seeded inputs resident in HBM before the timed region. Prints ONE JSON line.
+
+Per the reference's bench discipline (src/mlx_train_perf/bench/worker.py:93-142,
+scripts/bench_attention_op.py:225-296): seeded inputs, warm-up outside the window, timed window
+bracketed by device synchronization; forward marginal peak memory measured the worker's way
+(max_memory_allocated - allocated_before after a reset).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+sys.path.insert(0, str(ROOT / "mlx-train-perf_amd"))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (no sparsity)
+PEAK_HBM_GBS = 8000.0
+
+N, D, V = 8192, 4096, 151936
+IGNORE = -100
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def lce_inputs_gpu(n, d, v, seed=0, ignore_frac=0.05):
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    h = torch.randn(n, d, generator=g, device="cuda")
+    h = (h / torch.sqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    w = (torch.randn(v, d, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device="cuda")
+    k = int(round(ignore_frac * n))
+    t[torch.randperm(n, generator=g, device="cuda")[:k]] = IGNORE
+    return h, w, t
+
+
+def time_region(fn, steps, warmup):
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        fn()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
+def mfma_ceiling_tflops():
+    import torch
+
+    from mlx_train_perf import _native
+
+    lib = _native.load()
+    blocks, iters = 1024, 20000
+    out = torch.zeros(blocks, device="cuda")
+    s = torch.cuda.current_stream().cuda_stream
+    lib.mtp_bench_mfma_ceiling(blocks, 100, out.data_ptr(), s)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    lib.mtp_bench_mfma_ceiling(blocks, iters, out.data_ptr(), s)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1)
+    flops = blocks * 4 * 4 * iters * 32768.0
+    return flops / (ms * 1e-3) / 1e12
+
+
+def bench_lce(steps, warmup, head_kind="dense"):
+    """LCE fwd+bwd step timing + per-phase event timing of the forward kernel window."""
+    import torch
+
+    from mlx_train_perf.core.loss import DenseHead, QuantizedHead, kernel_forward_parts
+    from mlx_train_perf.core.quant import quantize
+    from mlx_train_perf.plan import launch as plan
+
+    h, w, t = lce_inputs_gpu(N, D, V)
+    if head_kind == "dense":
+        head = DenseHead(weight=w, trainable=False)
+    else:
+        wq, sc, bi = quantize(w)
+        del w
+        head = QuantizedHead(w_q=wq, scales=sc, biases=bi)
+    hd = h.detach().requires_grad_(True)
+    valid = (t != IGNORE)
+    ct = (valid.float() / valid.sum()).contiguous()  # cotangent of the masked mean
+
+    def step():
+        hd.grad = None
+        nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        nll.backward(ct)
+
+    sec = time_region(step, steps, warmup)
+
+    # Live per-phase durations with events on the launch stream: [fwd][bwd] per step.
+    stream = torch.cuda.current_stream()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        hd.grad = None
+        evs[i][0].record(stream)
+        nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        evs[i][1].record(stream)
+        nll.backward(ct)
+        evs[i][2].record(stream)
+    torch.cuda.synchronize()
+    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+
+    # Forward marginal peak (bench/worker.py:117-132 semantics).
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    with torch.no_grad():
+        nll, _, _ = kernel_forward_parts(h, head, t, ignore_index=IGNORE)
+    torch.cuda.synchronize()
+    fwd_peak = torch.cuda.max_memory_allocated() - before
+    del nll
+    p = plan.lce_plan(n=N, v=V, d=D)
+    return {"sec_per_step": sec, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_marginal_peak_gb": fwd_peak / 1e9,
+            "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks}
+
+
+def bench_attention(steps, warmup, packed=False):
+    import torch
+
+    from mlx_train_perf.attention.api import kernel_backward, kernel_forward
+    from mlx_train_perf.plan import launch as plan
+
+    b, hq, hkv, dh = 1, 32, 8, 128
+    s = 16384 if packed else 8192
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(b, hq, s, dh, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(b, hkv, s, dh, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(b, hkv, s, dh, generator=g, device="cuda").to(torch.bfloat16)
+    do = torch.randn(b, hq, s, dh, generator=g, device="cuda").to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(dh)
+    sid = sst = None
+    if packed:
+        import random
+
+        rng = random.Random(0)
+        lens, used = [], 0
+        while used < s:
+            n_ = min(rng.randint(64, 2048), s - used)
+            lens.append(n_)
+            used += n_
+        ids, starts, pos = [], [], 0
+        for i, n_ in enumerate(lens):
+            ids += [i] * n_
+            starts += [pos] * n_
+            pos += n_
+        sid = torch.tensor([ids], dtype=torch.int32, device="cuda")
+        sst = torch.tensor([starts], dtype=torch.int32, device="cuda")
+        pairs = plan.packed_pairs(lens)
+    else:
+        pairs = plan.causal_pairs(s)
+    state = {}
+
+    def fwd():
+        state["o"], state["l"] = kernel_forward(q, k, v, scale=scale, seg_id=sid, seg_start=sst)
+
+    def fwdbwd():
+        fwd()
+        kernel_backward(q, k, v, state["o"], state["l"], do, scale=scale, seg_id=sid, seg_start=sst)
+
+    fwd_s = time_region(fwd, steps, warmup)
+    fb_s = time_region(fwdbwd, steps, warmup)
+    flops_fb = 2.0 * 7 * dh * hq * b * pairs
+    out = {"seq": s, "fwd_ms": fwd_s * 1e3, "fwdbwd_ms": fb_s * 1e3, "bwd_ms": (fb_s - fwd_s) * 1e3,
+           "pairs_per_head": pairs, "algorithmic_tflop": flops_fb / 1e12,
+           "tflops": flops_fb / fb_s / 1e12, "mfma_frac": flops_fb / fb_s / 1e12 / PEAK_BF16_TFLOPS}
+    if packed:
+        out["segments"] = len(lens)
+    return out
+
+
+def cpu_baseline(budget_s: float = 20.0):
+    """The oracle (PyTorch-CPU fp32 restatement of the reference's naive path) on a bounded sample
+    of the same workload: `rows` tokens of the flagship LCE fwd+bwd (full D, V)."""
+    import torch
+
+    from oracle import lce as olce
+
+    if "OMP_NUM_THREADS" not in os.environ:  # the GPU box sets it to its CPU share
+        torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(V, D, generator=g) * 0.02).to(torch.bfloat16).to(torch.float32)  # bf16 values, fp32 storage
+
+    def run(rows):
+        h = torch.randn(rows, D, generator=g)
+        h = (h / torch.sqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+        t = torch.randint(0, V, (rows,), generator=g)
+        t0 = time.perf_counter()
+        nll, lse, _ = olce.forward(h, w, t, ignore_index=IGNORE, dtype=torch.float32)
+        olce.backward(h, w, t, lse, torch.full((rows,), 1.0 / rows), ignore_index=IGNORE, dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    run(8)  # warm-up outside the window
+    rows = 16
+    dt = run(rows)
+    # scale the sample toward the budget (linear in rows), capped
+    rows = int(max(16, min(1024, rows * budget_s / max(dt, 1e-3) * 0.5)))
+    dt = run(rows)
+    return {"value": rows / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"LCE fwd+bwd on {rows} of the {N} tokens (D={D}, V={V}), oracle/lce.py fp32, "
+                      f"{dt:.1f} s; CPU {_cpu_model()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build runs on one GPU; "
+              "see DESIGN.md for how the path would shard)", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+
+    lce = bench_lce(args.steps, args.warmup, "dense")
+    sec = lce["sec_per_step"]
+    flops_step = 6.0 * N * V * D
+    fwd_flops = 2.0 * N * V * D
+    ach = fwd_flops / (lce["fwd_ms"] * 1e-3) / 1e12
+    result = {
+        "metric": "fused-LCE fwd+bwd tokens/s @N8192 V151936 D4096 (bf16, frozen head)",
+        "value": N / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded: H~N(0,1) RMS-normalized, W~N(0,0.02), 5% ignore_index)",
+        "config": {"workload": "lce_fwd_bwd_n8192_d4096_v151936_bf16_frozen_head", "tokens": N, "d": D, "v": V,
+                   "parallelism": "none (1 GPU)"},
+        "roofline": {"bound": "mfma", "kernel": "lce_fwd_kernel<0> (+ lce_fwd_finalize_kernel in the event window)",
+                     "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
+                     "traffic": None},
+        "step_mfma_frac": flops_step / sec / 1e12 / PEAK_BF16_TFLOPS,
+        "lce": {**lce, "step_tflops": flops_step / sec / 1e12},
+    }
+    try:
+        result["mfma_ceiling_tflops"] = mfma_ceiling_tflops()
+    except Exception as exc:  # measurement utility only
+        result["mfma_ceiling_tflops"] = f"failed: {exc}"
+    if not args.no_extras:
+        torch.cuda.empty_cache()
+        q4 = bench_lce(max(3, args.steps // 4), 1, "q4")
+        result["qlora_lce"] = {**q4, "tokens_per_s": N / q4["sec_per_step"],
+                               "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
+        torch.cuda.empty_cache()
+        result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, packed=False)
+        result["attention_packed_s16384"] = bench_attention(args.steps, args.warmup, packed=True)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,103 @@
+"""The C-ABI library (CPU lane): it loads, exports every symbol the headers declare, reports the
+same plans as the Python planner, and refuses invalid calls with typed codes before any launch.
+No call here reaches a GPU launch: every case fails validation or is a pure size query."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mlx_train_perf import _native
+from mlx_train_perf.plan import launch as plan
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols() -> set[str]:
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        names |= set(re.findall(r"\b(mtp_\w+)\s*\(", h.read_text()))
+    return names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.load()
+    declared = _declared_symbols()
+    assert {"mtp_lce_fwd", "mtp_lce_bwd", "mtp_attn_fwd", "mtp_attn_bwd"} <= declared
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert set(_native.SIGNATURES) >= declared - set()  # every export has a Python signature
+    assert lib.mtp_abi_version() == 1
+
+
+@pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1)])
+def test_plans_agree_with_python_planner(n, d, v):
+    lib = _native.load()
+    assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, 0) == plan.lce_fwd_workspace_bytes(n, v)
+    for budget in (1 << 20, 1 << 26, 1 << 30, 1 << 34):
+        c = lib.mtp_lce_bwd_chunk(n, d, v, budget)
+        assert c == plan.lce_bwd_chunk(n, d, v, budget)
+        assert c % 256 == 0 and c >= 256
+        assert lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, c) == plan.lce_bwd_workspace_bytes(n, d, v, c)
+    assert lib.mtp_attn_bwd_workspace_bytes(1, 32, 8, 8192, 128) == plan.attn_plan(b=1, hq=32, hkv=8, s=8192).bwd_workspace_bytes
+
+
+FAKE = 0x100000  # aligned, never dereferenced: every call below fails validation first
+
+
+def _lce_fwd(**kw):
+    lib = _native.load()
+    a = dict(hidden=FAKE, w=FAKE, w_q=None, scales=None, biases=None, targets=FAKE, n=16, d=64, v=100, head=0,
+             ign=-100, nll=FAKE, lse=FAKE, tgt=FAKE, ws=FAKE, ws_bytes=0, stream=None)
+    a.update(kw)
+    return lib.mtp_lce_fwd(a["hidden"], a["w"], a["w_q"], a["scales"], a["biases"], a["targets"], a["n"], a["d"],
+                           a["v"], a["head"], a["ign"], a["nll"], a["lse"], a["tgt"], a["ws"], a["ws_bytes"], a["stream"])
+
+
+def test_lce_refusals():
+    assert _lce_fwd(n=0) == _native.MTP_ERR_INPUT
+    assert _lce_fwd(targets=None) == _native.MTP_ERR_INPUT
+    assert _lce_fwd(d=33) == _native.MTP_ERR_UNSUPPORTED
+    assert _lce_fwd(hidden=FAKE + 2) == _native.MTP_ERR_UNSUPPORTED
+    assert _lce_fwd(head=1, w=None, w_q=FAKE, scales=FAKE, biases=FAKE, d=96) == _native.MTP_ERR_UNSUPPORTED
+    assert _lce_fwd(head=7) == _native.MTP_ERR_UNSUPPORTED
+    assert _lce_fwd(ws_bytes=8) == _native.MTP_ERR_WORKSPACE
+    assert "workspace" in _native.last_error()
+    lib = _native.load()
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, 100, FAKE, 1 << 20, None)
+    assert rc == _native.MTP_ERR_INPUT and "multiple of 256" in _native.last_error()
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, 256, FAKE, 16, None)
+    assert rc == _native.MTP_ERR_WORKSPACE
+
+
+def test_attention_refusals():
+    lib = _native.load()
+
+    def fwd(**kw):
+        a = dict(b=1, hq=4, hkv=2, s=16, dh=64, causal=1, sid=None, sst=None)
+        a.update(kw)
+        return lib.mtp_attn_fwd(FAKE, FAKE, FAKE, a["b"], a["hq"], a["hkv"], a["s"], a["dh"], 0.1, a["causal"],
+                                a["sid"], a["sst"], (FAKE if kw.get("o", True) else None), FAKE, None)
+
+    assert fwd(hq=3) == _native.MTP_ERR_INPUT
+    assert fwd(dh=80) == _native.MTP_ERR_UNSUPPORTED
+    assert fwd(causal=0) == _native.MTP_ERR_UNSUPPORTED
+    assert fwd(sid=FAKE) == _native.MTP_ERR_INPUT
+    assert fwd(o=False) == _native.MTP_ERR_INPUT
+    rc = lib.mtp_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 4, 2, 16, 64, 0.1, 1, None, None, FAKE, FAKE, FAKE,
+                          FAKE, 4, None)
+    assert rc == _native.MTP_ERR_WORKSPACE
+
+
+def test_error_mapping_to_typed_exceptions():
+    from mlx_train_perf.errors import LaunchBudgetError, LossInputError, UnsupportedAttentionError
+
+    with pytest.raises(LossInputError):
+        _native.check(_native.MTP_ERR_INPUT, domain="loss")
+    with pytest.raises(UnsupportedAttentionError):
+        _native.check(_native.MTP_ERR_UNSUPPORTED, domain="attention")
+    with pytest.raises(LaunchBudgetError):
+        _native.check(_native.MTP_ERR_WORKSPACE, domain="loss")
+    assert ctypes.c_int(_native.MTP_OK).value == 0

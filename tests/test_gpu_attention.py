@@ -109,3 +109,15 @@ def test_deterministic_repeat():
     b = _run_kernel(q, k, v, do, 0.1)
     for x, y in zip(a, b):
         assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("name", ["attn_causal_b1_hq4_hkv2_s61_d64.npz", "attn_packed_b1_hq4_hkv2_s61_d64.npz"])
+def test_golden_fixtures(name):
+    from tests._golden import load
+
+    g = load(name)
+    seg = (g["seg_id"], g["seg_start"]) if "seg_id" in g else None
+    o, lse, dq, dk, dv = _run_kernel(g["q"], g["k"], g["v"], g["d_o"], float(g["scale"]), seg=seg)
+    assert rel_l2(o, g["o"]) <= 1e-2 and (lse.double() - g["lse"]).abs().max() <= 2e-3
+    for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+        assert rel_l2(got, g[key]) <= 1e-2

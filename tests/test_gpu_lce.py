@@ -113,3 +113,19 @@ def test_deterministic_repeat():
         nll.backward(torch.ones_like(nll))
         outs.append((nll.detach().cpu(), hd.grad.cpu()))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
+def test_golden_fixtures():
+    from tests._golden import load
+
+    g = load("lce_dense_n64_d64_v1024.npz")
+    hd, nll, lse, tgt = _kernel(g["hidden"], g["weight"], g["targets"])
+    nll.backward(g["cotangent"].float().cuda())
+    assert ((nll.cpu().double() - g["nll"]).abs() <= 2e-3 * g["nll"].abs() + 1e-4).all()
+    assert (lse.cpu().double() - g["lse"]).abs().max() <= 2e-3
+    assert rel_l2(hd.grad.cpu(), g["d_hidden"]) <= 1e-2
+    q = load("lce_q4_n32_d128_v512.npz")
+    hd, nll, lse, tgt = _kernel(q["hidden"], None, q["targets"], head="q4", wq=q["w_q"], sc=q["scales"], bi=q["biases"])
+    nll.backward(q["cotangent"].float().cuda())
+    assert (nll.cpu().double() - q["nll"]).abs().max() <= 8e-3
+    assert rel_l2(hd.grad.cpu(), q["d_hidden"]) <= 1e-2

@@ -1,0 +1,60 @@
+"""Launch/memory planner math (CPU): exact causal pair counts by brute force (reference
+tests/test_attention_launch_plan.py:61), packed pair counts, LCE split/chunk invariants."""
+from __future__ import annotations
+
+import pytest
+
+from mlx_train_perf.plan import launch as plan
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 31, 64, 257])
+def test_causal_pairs_brute_force(n):
+    assert plan.causal_pairs(n) == sum(1 for i in range(n) for j in range(n) if j <= i)
+
+
+def test_flagship_pair_count():
+    assert plan.causal_pairs(8192) == 33_558_528
+    flops = 2 * 7 * 128 * 32 * plan.causal_pairs(8192)
+    assert abs(flops / 1e12 - 1.924) < 1e-3
+
+
+def test_packed_pairs_sum_of_segments():
+    assert plan.packed_pairs([3, 5]) == 6 + 15
+    assert plan.packed_pairs([8]) == plan.causal_pairs(8)
+
+
+@pytest.mark.parametrize(("n", "v"), [(8192, 151936), (1024, 32000), (65, 1027), (1, 1), (300, 300)])
+def test_lce_forward_splits(n, v):
+    ns = plan.lce_fwd_splits(n, v)
+    vt = -(-v // 256)
+    rt = -(-n // 256)
+    assert 1 <= ns <= vt
+    if vt >= 256:
+        assert rt * ns >= 256  # at least one workgroup per CU
+    assert plan.lce_fwd_workspace_bytes(n, v) == 8 * ns * n
+
+
+def test_flagship_forward_workspace_under_10mb():
+    p = plan.lce_plan(n=8192, v=151936, d=4096)
+    assert p.fwd_workspace_bytes + 3 * 8192 * 4 < 0.01e9
+    assert p.fwd_splits == 8
+
+
+@pytest.mark.parametrize("budget", [1 << 20, 1 << 28, 1 << 30, 1 << 33])
+def test_backward_chunk_fits_budget_when_possible(budget):
+    n, d, v = 8192, 4096, 151936
+    c = plan.lce_bwd_chunk(n, d, v, budget)
+    ws = plan.lce_bwd_workspace_bytes(n, d, v, c)
+    assert c % 256 == 0
+    if c > 256:
+        assert ws <= budget
+    if budget >= n * (-(-v // 256) * 256) * 2:
+        assert -(-v // c) == 1 and ws == n * c * 2
+
+
+def test_attention_plan():
+    p = plan.attn_plan(b=1, hq=32, hkv=8, s=8192)
+    assert p.heads_per_workgroup == 4
+    assert p.fwd_workgroups == (8192 // 32) * 8
+    assert p.dkv_workgroups == 64 * 8
+    assert plan.attn_heads_per_workgroup(6, 3) == 2 and plan.attn_heads_per_workgroup(3, 1) == 1
