@@ -22,6 +22,8 @@ namespace mtp {
 
 constexpr int kTile = 256;
 constexpr int kBK = 64;
+constexpr int kThreads = 512;          // 8 waves: 2 per SIMD
+constexpr int kNJ = 2;                 // 32-wide MFMA blocks per wave along the B rows
 constexpr int kLdsBytes = 4 * 32768;  // A0, B0, A1, B1 (each 256 rows x 128 B)
 
 // ------------------------------------------------------------------------------------------
@@ -35,15 +37,15 @@ struct RowKLoader {
   long ld;
   int nrows;   // number of valid rows counted from row0
   int K;
-  u32x4 r[8];
+  u32x4 r[4];
 
   __device__ __forceinline__ void load(int kt) {
     const int tid = threadIdx.x;
     const int c = tid & 7;
     const int k = kt * kBK + 8 * c;
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int row = (tid >> 3) + 32 * p;
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 64 * p;
       if (row < nrows && k < K) {
         r[p] = *reinterpret_cast<const u32x4*>(base + (long)row * ld + k);
       } else {
@@ -55,8 +57,8 @@ struct RowKLoader {
     const int tid = threadIdx.x;
     const int c = tid & 7;
 #pragma unroll
-    for (int p = 0; p < 8; ++p) {
-      const int row = (tid >> 3) + 32 * p;
+    for (int p = 0; p < 4; ++p) {
+      const int row = (tid >> 3) + 64 * p;
       lds_write16(lds, lds_off(row, c), r[p]);
     }
   }
@@ -71,32 +73,27 @@ struct Q4RowKLoader {
   const bf16_t* bi;
   int nrows;
   int K;
-  u32x4 q0, q1;
+  u32x4 q0;
   float s, b;
 
+  // Thread t owns half a row: row t >> 1, words 4 * (t & 1) .. +3 (chunks of 8 values each).
   __device__ __forceinline__ void load(int kt) {
-    const int row = threadIdx.x;
+    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
     if (row < nrows) {
-      const uint32_t* p = wq + (long)row * (K >> 3) + kt * 8;
-      q0 = *reinterpret_cast<const u32x4*>(p);
-      q1 = *reinterpret_cast<const u32x4*>(p + 4);
+      q0 = *reinterpret_cast<const u32x4*>(wq + (long)row * (K >> 3) + kt * 8 + 4 * half);
       const long g = (long)row * (K >> 6) + kt;
       s = bf16_to_f32(sc[g]);
       b = bf16_to_f32(bi[g]);
     } else {
       q0 = zero4();
-      q1 = zero4();
       s = 0.f;
       b = 0.f;
     }
   }
   __device__ __forceinline__ void store(char* lds) const {
-    const int row = threadIdx.x;
+    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
 #pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      const uint32_t w = (c < 4) ? q0[c & 3] : q1[c & 3];
-      lds_write16(lds, lds_off(row, c), dequant8(w, s, b));
-    }
+    for (int c = 0; c < 4; ++c) lds_write16(lds, lds_off(row, 4 * half + c), dequant8(q0[c], s, b));
   }
 };
 
@@ -117,7 +114,7 @@ struct TransLoader {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = kt * kBK + 8 * vb + i;
-      if (k < kvalid && d < dvalid) {
+      if (tid < 256 && k < kvalid && d < dvalid) {
         x[i] = *reinterpret_cast<const u32x4*>(w + (long)k * ld + d);
       } else {
         x[i] = zero4();
@@ -126,6 +123,7 @@ struct TransLoader {
   }
   __device__ __forceinline__ void store(char* lds) const {
     const int tid = threadIdx.x;
+    if (tid >= 256) return;
     const int vb = tid >> 5, db = tid & 31;
     u32x4 y[8];
     transpose8x8(x, y);
@@ -157,7 +155,7 @@ struct Q4TransLoader {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = kt * kBK + 8 * vb + i;
-      if (k < kvalid && d < dvalid) {
+      if (tid < 256 && k < kvalid && d < dvalid) {
         q[i] = wq[(long)k * (D >> 3) + word];
         const long g = (long)k * (D >> 6) + grp;
         s[i] = bf16_to_f32(sc[g]);
@@ -171,6 +169,7 @@ struct Q4TransLoader {
   }
   __device__ __forceinline__ void store(char* lds) const {
     const int tid = threadIdx.x;
+    if (tid >= 256) return;
     const int vb = tid >> 5, db = tid & 31;
     u32x4 x[8], y[8];
 #pragma unroll
@@ -182,12 +181,12 @@ struct Q4TransLoader {
 };
 
 // ------------------------------------------------------------------------------------------
-// 256x256 tile GEMM core: acc[bi][bj] (wave sub-tile 128x128) += A_tile . B_tile^T over nk
-// K-slabs of 64. Wave w covers A rows 128*(w&1).. and B rows 128*(w>>1)..
+// 256x256 tile GEMM core: acc[bi][bj] (wave sub-tile 128x64) += A_tile . B_tile^T over nk
+// K-slabs of 64. Wave w (of 8) covers A rows 128*(w&1).. and B rows 64*(w>>1)..
 // Ends with a barrier, so the caller may reuse all of LDS in its epilogue.
 // ------------------------------------------------------------------------------------------
 template <class LA, class LB>
-__device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, f32x16 (&acc)[4][4]) {
+__device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, f32x16 (&acc)[4][kNJ]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int wa = w & 1, wb = w >> 1;
@@ -196,7 +195,7 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < kNJ; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
@@ -217,15 +216,15 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int c = 2 * ks + lhalf;
-      bf16x8 a[4], b[4];
+      bf16x8 a[4], b[kNJ];
 #pragma unroll
       for (int i = 0; i < 4; ++i) a[i] = as_bf16x8(lds_read16(cA, lds_off(128 * wa + 32 * i + lrow, c)));
 #pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = as_bf16x8(lds_read16(cB, lds_off(128 * wb + 32 * j + lrow, c)));
+      for (int j = 0; j < kNJ; ++j) b[j] = as_bf16x8(lds_read16(cB, lds_off(64 * wb + 32 * j + lrow, c)));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < kNJ; ++j) acc[i][j] = mfma32(a[i], b[j], acc[i][j]);
     }
     if (more) {
       char* nA = lds + ((kt & 1) ? 0 : 65536);
@@ -242,7 +241,7 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
 // token columns, so the vocab reduction is lane-local except for one final exchange.
 // ------------------------------------------------------------------------------------------
 template <int Q4>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                     const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
@@ -262,9 +261,9 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   const int t0 = rt * kTile;
   const int nk = (D + kBK - 1) / kBK;
 
-  float m[4], s[4];
+  float m[kNJ], s[kNJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kNJ; ++j) {
     m[j] = kNegInf;
     s[j] = 0.f;
   }
@@ -277,7 +276,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
 
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int v0 = vt * kTile;
-    f32x16 acc[4][4];
+    f32x16 acc[4][kNJ];
     if constexpr (Q4) {
       Q4RowKLoader la;
       la.wq = Wq + (long)v0 * (D >> 3);
@@ -296,7 +295,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     }
     const bool tail = (v0 + kTile) > V;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < kNJ; ++j) {
       float mx = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -324,7 +323,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
 
   // Merge the two lane halves (different vocab rows, same tokens).
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kNJ; ++j) {
     const float mo = __shfl_xor(m[j], 32, 64);
     const float so = __shfl_xor(s[j], 32, 64);
     lse2_merge(m[j], s[j], mo, so);
@@ -334,8 +333,8 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   float* xs = xm + 256;
   if (wa == 1 && lhalf == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tl = 128 * wb + 32 * j + lcol;
+    for (int j = 0; j < kNJ; ++j) {
+      const int tl = 64 * wb + 32 * j + lcol;
       xm[tl] = m[j];
       xs[tl] = s[j];
     }
@@ -343,8 +342,8 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   __syncthreads();
   if (wa == 0 && lhalf == 0) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int tl = 128 * wb + 32 * j + lcol;
+    for (int j = 0; j < kNJ; ++j) {
+      const int tl = 64 * wb + 32 * j + lcol;
       lse2_merge(m[j], s[j], xm[tl], xs[tl]);
       const int t = t0 + tl;
       if (t < N) {
@@ -427,7 +426,7 @@ __global__ __launch_bounds__(256) void lce_fwd_finalize_kernel(
 // one XCD share the same weight rows in L2.
 // ------------------------------------------------------------------------------------------
 template <int Q4>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                       const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                       const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
@@ -451,7 +450,7 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   const int nk = (D + kBK - 1) / kBK;
   const int vlim = v_end < V ? v_end : V;
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][kNJ];
   RowKLoader lb;
   lb.base = H + (long)t0 * D;
   lb.ld = D;
@@ -477,8 +476,8 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   // Epilogue: stage the bf16 G tile as [token][vocab] (512 B rows, 16-byte chunks swizzled by
   // row & 31), then write it out with coalesced 16-byte stores.
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int tl = 128 * wb + 32 * j + lcol;
+  for (int j = 0; j < kNJ; ++j) {
+    const int tl = 64 * wb + 32 * j + lcol;
     const int t = t0 + tl;
     float coef = 0.f, l2 = 0.f;
     long long y = -1;
@@ -507,8 +506,8 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   }
   __syncthreads();
 #pragma unroll 4
-  for (int p = 0; p < 32; ++p) {
-    const int id = tid + 256 * p;
+  for (int p = 0; p < 16; ++p) {
+    const int id = tid + kThreads * p;
     const int row = id >> 5, c = id & 31;
     const int t = t0 + row;
     if (t < N) {
@@ -523,7 +522,7 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
 // mode 0: acc32 = part; 1: acc32 += part; 2: dH = bf16(acc32 + part); 3: dH = bf16(part).
 // ------------------------------------------------------------------------------------------
 template <int Q4>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16_t* __restrict__ W,
                        const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                        const bf16_t* __restrict__ Bi, int N, int D, int V, int v_begin, int v_end,
@@ -547,7 +546,7 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const int vlim = v_end < V ? v_end : V;
   const int nk = kc / kBK;
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][kNJ];
   RowKLoader la;
   la.base = G + (long)t0 * ldg;
   la.ld = ldg;
@@ -579,8 +578,8 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
       const int t = t0 + 128 * wa + 32 * i + 8 * (r >> 2) + 4 * lhalf + (r & 3);
       if (t >= N) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int d = d0 + 128 * wb + 32 * j + lcol;
+      for (int j = 0; j < kNJ; ++j) {
+        const int d = d0 + 64 * wb + 32 * j + lcol;
         if (d >= D) continue;
         const long o = (long)t * D + d;
         const float v = acc[i][j][r];
@@ -618,7 +617,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
   float* pm = ws;
   float* ps = ws + (long)ns * N;
   const int rtiles = (N + kTile - 1) / kTile;
-  dim3 grid(rtiles * ns), block(256);
+  dim3 grid(rtiles * ns), block(kThreads);
   if (h.q4) {
     hipLaunchKernelGGL(lce_fwd_kernel<1>, grid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, N, D, V, ns, pm, ps);
   } else {
@@ -626,12 +625,12 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dim3 fgrid((N + 3) / 4);
+  dim3 fgrid((N + 3) / 4), fblock(256);
   if (h.q4) {
-    hipLaunchKernelGGL(lce_fwd_finalize_kernel<1>, fgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, N,
+    hipLaunchKernelGGL(lce_fwd_finalize_kernel<1>, fgrid, fblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, N,
                        D, V, ns, pm, ps, ignore_index, nll, lse, tgt);
   } else {
-    hipLaunchKernelGGL(lce_fwd_finalize_kernel<0>, fgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, N,
+    hipLaunchKernelGGL(lce_fwd_finalize_kernel<0>, fgrid, fblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, N,
                        D, V, ns, pm, ps, ignore_index, nll, lse, tgt);
   }
   return hipGetLastError();
@@ -643,7 +642,7 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   const int nchunks = (V + chunk - 1) / chunk;
-  dim3 block(256);
+  dim3 block(kThreads);
   for (int c = 0; c < nchunks; ++c) {
     const int vb = c * chunk;
     const int ve = (vb + chunk < V) ? vb + chunk : V;
