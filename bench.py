@@ -239,6 +239,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--parts", default="lce,qlora,attention",
+                    help="comma list of lce, qlora, attention (lce is the headline line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build runs on one GPU; "
@@ -280,11 +282,13 @@ def main():
         result["mfma_ceiling_tflops"] = mfma_ceiling_tflops()
     except Exception as exc:  # measurement utility only
         result["mfma_ceiling_tflops"] = f"failed: {exc}"
-    if not args.no_extras:
+    parts = set(args.parts.split(","))
+    if not args.no_extras and "qlora" in parts:
         torch.cuda.empty_cache()
         q4 = bench_lce(max(3, args.steps // 4), 1, "q4")
         result["qlora_lce"] = {**q4, "tokens_per_s": N / q4["sec_per_step"],
                                "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
+    if not args.no_extras and "attention" in parts:
         torch.cuda.empty_cache()
         result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, packed=False)
         result["attention_packed_s16384"] = bench_attention(args.steps, args.warmup, packed=True)

@@ -102,7 +102,7 @@ __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : (
 // Forward
 // ------------------------------------------------------------------------------------------
 template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                      const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                      bf16_t* __restrict__ o, float* __restrict__ lse, int B, int Hq, int Hkv, int S,

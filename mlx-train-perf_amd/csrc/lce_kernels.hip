@@ -26,6 +26,12 @@ constexpr int kThreads = 512;          // 8 waves: 2 per SIMD
 constexpr int kNJ = 2;                 // 32-wide MFMA blocks per wave along the B rows
 constexpr int kLdsBytes = 4 * 32768;  // A0, B0, A1, B1 (each 256 rows x 128 B)
 
+// Interior tiles use the direct-to-LDS ring core when MTP_LCE_RING is 1, else the
+// register-staged double-buffered core.
+#ifndef MTP_LCE_RING
+#define MTP_LCE_RING 0
+#endif
+
 // ------------------------------------------------------------------------------------------
 // Operand loaders. Each produces a 256-row x 64-k bf16 tile in LDS (swizzled layout).
 // ------------------------------------------------------------------------------------------
@@ -39,17 +45,28 @@ struct RowKLoader {
   int K;
   u32x4 r[4];
 
+  // FULL: every row and k of the slab is in range (interior tiles): no predication, a uniform
+  // base pointer plus 32-bit per-thread offsets.
+  template <bool FULL>
   __device__ __forceinline__ void load(int kt) {
     const int tid = threadIdx.x;
     const int c = tid & 7;
     const int k = kt * kBK + 8 * c;
+    if constexpr (FULL) {
+      const bf16_t* b = base + kt * kBK;
+      const int o = (tid >> 3) * (int)ld + 8 * c;
+      const int step = 64 * (int)ld;
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const int row = (tid >> 3) + 64 * p;
-      if (row < nrows && k < K) {
-        r[p] = *reinterpret_cast<const u32x4*>(base + (long)row * ld + k);
-      } else {
-        r[p] = zero4();
+      for (int p = 0; p < 4; ++p) r[p] = *reinterpret_cast<const u32x4*>(b + o + p * step);
+    } else {
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const int row = (tid >> 3) + 64 * p;
+        if (row < nrows && k < K) {
+          r[p] = *reinterpret_cast<const u32x4*>(base + (long)row * ld + k);
+        } else {
+          r[p] = zero4();
+        }
       }
     }
   }
@@ -77,9 +94,10 @@ struct Q4RowKLoader {
   float s, b;
 
   // Thread t owns half a row: row t >> 1, words 4 * (t & 1) .. +3 (chunks of 8 values each).
+  template <bool FULL>
   __device__ __forceinline__ void load(int kt) {
     const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
-    if (row < nrows) {
+    if (FULL || row < nrows) {
       q0 = *reinterpret_cast<const u32x4*>(wq + (long)row * (K >> 3) + kt * 8 + 4 * half);
       const long g = (long)row * (K >> 6) + kt;
       s = bf16_to_f32(sc[g]);
@@ -107,10 +125,20 @@ struct TransLoader {
   int dvalid;        // columns that exist from d0
   u32x4 x[8];
 
+  template <bool FULL>
   __device__ __forceinline__ void load(int kt) {
     const int tid = threadIdx.x;
     const int vb = tid >> 5, db = tid & 31;
     const int d = 8 * db;
+    if constexpr (FULL) {
+      if (tid < 256) {
+        const bf16_t* b = w + (long)kt * kBK * ld;
+        const int o = 8 * vb * (int)ld + d;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(b + o + i * (int)ld);
+      }
+      return;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = kt * kBK + 8 * vb + i;
@@ -146,6 +174,7 @@ struct Q4TransLoader {
   uint32_t q[8];
   float s[8], b[8];
 
+  template <bool FULL>
   __device__ __forceinline__ void load(int kt) {
     const int tid = threadIdx.x;
     const int vb = tid >> 5, db = tid & 31;
@@ -155,7 +184,7 @@ struct Q4TransLoader {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int k = kt * kBK + 8 * vb + i;
-      if (tid < 256 && k < kvalid && d < dvalid) {
+      if (tid < 256 && (FULL || (k < kvalid && d < dvalid))) {
         q[i] = wq[(long)k * (D >> 3) + word];
         const long g = (long)k * (D >> 6) + grp;
         s[i] = bf16_to_f32(sc[g]);
@@ -185,7 +214,7 @@ struct Q4TransLoader {
 // K-slabs of 64. Wave w (of 8) covers A rows 128*(w&1).. and B rows 64*(w>>1)..
 // Ends with a barrier, so the caller may reuse all of LDS in its epilogue.
 // ------------------------------------------------------------------------------------------
-template <class LA, class LB>
+template <bool FULL, class LA, class LB>
 __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, f32x16 (&acc)[4][kNJ]) {
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
@@ -199,8 +228,8 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  la.load(0);
-  lb.load(0);
+  la.template load<FULL>(0);
+  lb.template load<FULL>(0);
   la.store(lds);
   lb.store(lds + 32768);
   __syncthreads();
@@ -210,8 +239,8 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
     const char* cB = cA + 32768;
     const bool more = (kt + 1) < nk;
     if (more) {
-      la.load(kt + 1);
-      lb.load(kt + 1);
+      la.template load<FULL>(kt + 1);
+      lb.template load<FULL>(kt + 1);
     }
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -233,6 +262,272 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
     }
     __syncthreads();
   }
+}
+
+// ------------------------------------------------------------------------------------------
+// Interior-tile GEMM core: a 4-stage LDS ring, BK = 32 per stage (A 16 KiB + B 16 KiB).
+// Row-major bf16 operands are copied global -> LDS by the direct-to-LDS path
+// (global_load_lds_dwordx4, no staging registers) three stages ahead; operands that need
+// register work (4-bit dequant, W transpose) load one stage ahead into registers and are written
+// to LDS at the end of the iteration. Stage rows are 64 B (4 chunks), chunk c of row r stored at
+// slot c ^ ((r >> 1) & 3): conflict-free for the MFMA fragment reads (8 consecutive rows, one chunk).
+// Waits are explicit (s_waitcnt + s_barrier) so the direct-to-LDS copies stay in flight across
+// iterations.
+// ------------------------------------------------------------------------------------------
+constexpr int kRBK = 32;
+constexpr int kRing = 4;
+constexpr int kStageBytes = 32768;
+
+__device__ __forceinline__ int ring_off(int row, int c) { return row * 64 + ((c ^ ((row >> 1) & 3)) << 4); }
+
+// s_waitcnt with vmcnt <= VM and lgkmcnt <= 0 (LGKM0) or unconstrained; expcnt unconstrained.
+template <int VM, bool LGKM0>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(VM >= 0 && VM < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8) | ((VM >> 4) << 14));
+}
+
+// Direct-to-LDS row-major operand: each wave copies rows 32w .. 32w+31 (two 1 KiB instructions).
+struct DmaRowK {
+  static constexpr int kDma = 2;
+  static constexpr bool kReg = false;
+  const bf16_t* base;  // row 0 of the tile, k = 0
+  int o0, o1;          // per-lane element offsets of the two instructions
+  __device__ __forceinline__ void init(const bf16_t* b, int ld) {
+    base = b;
+    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+    const int c = (l & 3) ^ ((l >> 3) & 3);
+    o0 = (32 * w + (l >> 2)) * ld + 8 * c;
+    o1 = o0 + 16 * ld;
+  }
+  __device__ __forceinline__ void dma(int kt, char* tile) const {
+    const int w = threadIdx.x >> 6;
+    const bf16_t* b = base + kt * kRBK;
+    __builtin_amdgcn_global_load_lds(b + o0, tile + 2048 * w, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(b + o1, tile + 2048 * w + 1024, 16, 0, 0);
+  }
+  __device__ __forceinline__ void reg_load(int) {}
+  __device__ __forceinline__ void commit(char*) const {}
+};
+
+// 4-bit rows: thread t dequantizes 16 values (two words) of row t >> 1 per stage.
+struct Q4RingRowK {
+  static constexpr int kDma = 0;
+  static constexpr bool kReg = true;
+  const uint32_t* wq;
+  const bf16_t* sc;
+  const bf16_t* bi;
+  int K;
+  u32x2 q;
+  float s, b;
+  __device__ __forceinline__ void dma(int, char*) const {}
+  __device__ __forceinline__ void reg_load(int kt) {
+    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
+    q = *reinterpret_cast<const u32x2*>(wq + (long)row * (K >> 3) + kt * 4 + 2 * half);
+    const long g = (long)row * (K >> 6) + (kt >> 1);
+    s = bf16_to_f32(sc[g]);
+    b = bf16_to_f32(bi[g]);
+  }
+  __device__ __forceinline__ void commit(char* tile) const {
+    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
+    lds_write16(tile, ring_off(row, 2 * half), dequant8(q[0], s, b));
+    lds_write16(tile, ring_off(row, 2 * half + 1), dequant8(q[1], s, b));
+  }
+};
+
+// Transposed dense operand (tile rows are columns d of W [v][d]; k runs over v): threads 0..127
+// each load an 8 (v) x 8 (d) block and transpose it in registers.
+struct TransRing {
+  static constexpr int kDma = 0;
+  static constexpr bool kReg = true;
+  const bf16_t* w;  // row v = chunk start, column d0
+  int ld;
+  u32x4 x[8];
+  __device__ __forceinline__ void dma(int, char*) const {}
+  __device__ __forceinline__ void reg_load(int kt) {
+    const int tid = threadIdx.x;
+    if (tid >= 128) return;
+    const int vb = tid & 3, db = tid >> 2;
+    const bf16_t* b = w + (long)kt * kRBK * ld;
+    const int o = 8 * vb * ld + 8 * db;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(b + o + i * ld);
+  }
+  __device__ __forceinline__ void commit(char* tile) const {
+    const int tid = threadIdx.x;
+    if (tid >= 128) return;
+    const int vb = tid & 3, db = tid >> 2;
+    u32x4 y[8];
+    transpose8x8(x, y);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lds_write16(tile, ring_off(8 * db + j, vb), y[j]);
+  }
+};
+
+// Transposed 4-bit operand: threads 0..127 dequantize an 8 (v) x 8 (d) block and transpose it.
+struct Q4TransRing {
+  static constexpr int kDma = 0;
+  static constexpr bool kReg = true;
+  const uint32_t* wq;  // row v = chunk start
+  const bf16_t* sc;
+  const bf16_t* bi;
+  int D, d0;
+  uint32_t q[8];
+  float s[8], b[8];
+  __device__ __forceinline__ void dma(int, char*) const {}
+  __device__ __forceinline__ void reg_load(int kt) {
+    const int tid = threadIdx.x;
+    if (tid >= 128) return;
+    const int vb = tid & 3, db = tid >> 2;
+    const int word = (d0 >> 3) + db;
+    const int grp = (d0 + 8 * db) >> 6;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const long k = (long)kt * kRBK + 8 * vb + i;
+      q[i] = wq[k * (D >> 3) + word];
+      s[i] = bf16_to_f32(sc[k * (D >> 6) + grp]);
+      b[i] = bf16_to_f32(bi[k * (D >> 6) + grp]);
+    }
+  }
+  __device__ __forceinline__ void commit(char* tile) const {
+    const int tid = threadIdx.x;
+    if (tid >= 128) return;
+    const int vb = tid & 3, db = tid >> 2;
+    u32x4 x[8], y[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) x[i] = dequant8(q[i], s[i], b[i]);
+    transpose8x8(x, y);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lds_write16(tile, ring_off(8 * db + j, vb), y[j]);
+  }
+};
+
+struct Frags {
+  bf16x8 a[4], b[kNJ];
+};
+
+__device__ __forceinline__ void read_frags(Frags& f, const char* stage, int ks, int wa, int wb, int lrow, int lhalf) {
+  const int c = 2 * ks + lhalf;
+  const char* cB = stage + 16384;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) f.a[i] = as_bf16x8(lds_read16(stage, ring_off(128 * wa + 32 * i + lrow, c)));
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) f.b[j] = as_bf16x8(lds_read16(cB, ring_off(64 * wb + 32 * j + lrow, c)));
+}
+
+__device__ __forceinline__ void mma_frags(const Frags& f, f32x16 (&acc)[4][kNJ]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = mfma32(f.a[i], f.b[j], acc[i][j]);
+}
+
+// Software pipeline (per iteration kt, stage kt in LDS buffer kt % 4):
+//   barrier                      -> stages <= kt+1 complete and visible; stage kt-1 no longer read
+//   [register loads for stage kt+2]; direct-to-LDS copies for stage kt+3
+//   read fragments (kt, k16 #1); MFMAs (kt, #0) on fragments read one step earlier
+//   read fragments (kt+1, #0);   MFMAs (kt, #1)
+//   [commit register stage kt+2]; wait: this wave's copies of stage kt+2 (and register loads) done
+// so LDS latency is always covered by a group of MFMAs, including across the barrier.
+template <class LA, class LB>
+__device__ __forceinline__ void gemm_ring(LA& la, LB& lb, int nk, char* lds, f32x16 (&acc)[4][kNJ]) {
+  constexpr int DMA = LA::kDma + LB::kDma;
+  constexpr bool REG = LA::kReg || LB::kReg;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int wa = w & 1, wb = w >> 1;
+  const int lrow = lane & 31, lhalf = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  auto stage = [&](int st) { return lds + (st & (kRing - 1)) * kStageBytes; };
+  if constexpr (REG) {
+    la.reg_load(0);
+    lb.reg_load(0);
+  }
+  for (int st = 0; st < kRing - 1; ++st) {
+    if (st < nk) {
+      la.dma(st, stage(st));
+      lb.dma(st, stage(st) + 16384);
+    }
+  }
+  if constexpr (REG) {
+    wait_vm<0, false>();
+    la.commit(stage(0));
+    lb.commit(stage(0) + 16384);
+    if (nk > 1) {
+      la.reg_load(1);
+      lb.reg_load(1);
+      wait_vm<0, false>();
+      la.commit(stage(1));
+      lb.commit(stage(1) + 16384);
+    }
+    wait_vm<0, true>();
+  } else {
+    if (nk > 2) wait_vm<DMA, true>();
+    else wait_vm<0, true>();
+  }
+  __builtin_amdgcn_s_barrier();
+  Frags f0, f1;
+  read_frags(f0, stage(0), 0, wa, wb, lrow, lhalf);
+
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt > 0) __builtin_amdgcn_s_barrier();
+    const bool reg_next = REG && (kt + 2 < nk);
+    if constexpr (REG) {
+      if (reg_next) {
+        la.reg_load(kt + 2);
+        lb.reg_load(kt + 2);
+      }
+    }
+    const bool dma_next = (kt + kRing - 1) < nk;
+    if (dma_next) {
+      la.dma(kt + kRing - 1, stage(kt + kRing - 1));
+      lb.dma(kt + kRing - 1, stage(kt + kRing - 1) + 16384);
+    }
+    read_frags(f1, stage(kt), 1, wa, wb, lrow, lhalf);
+    mma_frags(f0, acc);
+    if (kt + 1 < nk) read_frags(f0, stage(kt + 1), 0, wa, wb, lrow, lhalf);
+    mma_frags(f1, acc);
+    if constexpr (REG) {
+      if (reg_next) {
+        if (dma_next) wait_vm<DMA, false>();
+        else wait_vm<0, false>();
+        la.commit(stage(kt + 2));
+        lb.commit(stage(kt + 2) + 16384);
+      }
+    }
+    // Stage kt+2 must be complete before the next barrier; only stage kt+3's copies may remain.
+    if (dma_next) wait_vm<DMA, true>();
+    else wait_vm<0, true>();
+  }
+  __builtin_amdgcn_s_barrier();
+}
+
+// ------------------------------------------------------------------------------------------
+// Tile order for one-tile-per-workgroup launches. Workgroup g runs on XCD g % 8; each XCD gets a
+// contiguous range of the N-axis tiles and walks them in 4 (M) x 8 (N) groups, so the ~32
+// workgroups that run concurrently on one XCD share 4 A-operand and 8 B-operand slabs in its L2.
+// Returns false for the padding workgroups of the last XCD range.
+// ------------------------------------------------------------------------------------------
+__device__ __forceinline__ bool xcd_tile(int mtiles, int ntiles, int& m, int& n) {
+  const int xcd = blockIdx.x & 7;
+  const int i = blockIdx.x >> 3;
+  const int n_per = (ntiles + 7) / 8;
+  const int n_lo = xcd * n_per;
+  const int n_cnt = (ntiles - n_lo < n_per) ? ntiles - n_lo : n_per;
+  if (n_cnt <= 0 || i >= mtiles * n_cnt) return false;
+  const int group = i / (4 * n_cnt);
+  const int first_m = group * 4;
+  const int gm = (mtiles - first_m < 4) ? mtiles - first_m : 4;
+  const int j = i - group * 4 * n_cnt;
+  m = first_m + j % gm;
+  n = n_lo + j / gm;
+  return true;
 }
 
 // ------------------------------------------------------------------------------------------
@@ -276,22 +571,38 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
 
   for (int vt = vt_begin; vt < vt_end; ++vt) {
     const int v0 = vt * kTile;
+    const bool full = (v0 + kTile <= V) && (t0 + kTile <= N) && (D % kBK == 0);
     f32x16 acc[4][kNJ];
-    if constexpr (Q4) {
+    if (MTP_LCE_RING && full) {
+      DmaRowK rb;
+      rb.init(H + (long)t0 * D, D);
+      if constexpr (Q4) {
+        Q4RingRowK ra;
+        ra.wq = Wq + (long)v0 * (D >> 3);
+        ra.sc = Sc + (long)v0 * (D >> 6);
+        ra.bi = Bi + (long)v0 * (D >> 6);
+        ra.K = D;
+        gemm_ring(ra, rb, D / kRBK, lds, acc);
+      } else {
+        DmaRowK ra;
+        ra.init(W + (long)v0 * D, D);
+        gemm_ring(ra, rb, D / kRBK, lds, acc);
+      }
+    } else if constexpr (Q4) {
       Q4RowKLoader la;
       la.wq = Wq + (long)v0 * (D >> 3);
       la.sc = Sc + (long)v0 * (D >> 6);
       la.bi = Bi + (long)v0 * (D >> 6);
       la.nrows = V - v0;
       la.K = D;
-      gemm_256x256(la, lb, nk, lds, acc);
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     } else {
       RowKLoader la;
       la.base = W + (long)v0 * D;
       la.ld = D;
       la.nrows = V - v0;
       la.K = D;
-      gemm_256x256(la, lb, nk, lds, acc);
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     }
     const bool tail = (v0 + kTile) > V;
 #pragma unroll
@@ -434,13 +745,8 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
                       int N, int D, int V, int v_begin, int v_end, int vtiles, int ldg, bf16_t* __restrict__ G) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
-  const int total = rtiles * vtiles;
-  const int per_xcd = (total + 7) / 8;
-  const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (tile >= total) return;
-  const int vtl = tile / rtiles;
-  const int rt = tile % rtiles;
-
+  int rt, vtl;
+  if (!xcd_tile(rtiles, vtiles, rt, vtl)) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int wa = w & 1, wb = w >> 1;
@@ -449,8 +755,25 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   const int v0 = v_begin + vtl * kTile;
   const int nk = (D + kBK - 1) / kBK;
   const int vlim = v_end < V ? v_end : V;
+  const bool full = (v0 + kTile <= vlim) && (t0 + kTile <= N) && (D % kBK == 0);
 
   f32x16 acc[4][kNJ];
+  if (MTP_LCE_RING && full) {
+    DmaRowK rb;
+    rb.init(H + (long)t0 * D, D);
+    if constexpr (Q4) {
+      Q4RingRowK ra;
+      ra.wq = Wq + (long)v0 * (D >> 3);
+      ra.sc = Sc + (long)v0 * (D >> 6);
+      ra.bi = Bi + (long)v0 * (D >> 6);
+      ra.K = D;
+      gemm_ring(ra, rb, D / kRBK, lds, acc);
+    } else {
+      DmaRowK ra;
+      ra.init(W + (long)v0 * D, D);
+      gemm_ring(ra, rb, D / kRBK, lds, acc);
+    }
+  } else {
   RowKLoader lb;
   lb.base = H + (long)t0 * D;
   lb.ld = D;
@@ -463,16 +786,17 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
     la.bi = Bi + (long)v0 * (D >> 6);
     la.nrows = vlim - v0;
     la.K = D;
-    gemm_256x256(la, lb, nk, lds, acc);
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
   } else {
     RowKLoader la;
     la.base = W + (long)v0 * D;
     la.ld = D;
     la.nrows = vlim - v0;
     la.K = D;
-    gemm_256x256(la, lb, nk, lds, acc);
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
   }
 
+  }
   // Epilogue: stage the bf16 G tile as [token][vocab] (512 B rows, 16-byte chunks swizzled by
   // row & 31), then write it out with coalesced 16-byte stores.
 #pragma unroll
@@ -530,13 +854,8 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
-  const int total = rtiles * dtiles;
-  const int per_xcd = (total + 7) / 8;
-  const int tile = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (tile >= total) return;
-  const int rt = tile / dtiles;
-  const int dt = tile % dtiles;
-
+  int rt, dt;
+  if (!xcd_tile(rtiles, dtiles, rt, dt)) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int wa = w & 1, wb = w >> 1;
@@ -545,8 +864,27 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const int d0 = dt * kTile;
   const int vlim = v_end < V ? v_end : V;
   const int nk = kc / kBK;
+  const bool full = (t0 + kTile <= N) && (v_begin + kc <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
+  if (MTP_LCE_RING && full) {
+    DmaRowK ra;
+    ra.init(G + (long)t0 * ldg, ldg);
+    if constexpr (Q4) {
+      Q4TransRing rb;
+      rb.wq = Wq + (long)v_begin * (D >> 3);
+      rb.sc = Sc + (long)v_begin * (D >> 6);
+      rb.bi = Bi + (long)v_begin * (D >> 6);
+      rb.D = D;
+      rb.d0 = d0;
+      gemm_ring(ra, rb, kc / kRBK, lds, acc);
+    } else {
+      TransRing rb;
+      rb.w = W + (long)v_begin * D + d0;
+      rb.ld = D;
+      gemm_ring(ra, rb, kc / kRBK, lds, acc);
+    }
+  } else {
   RowKLoader la;
   la.base = G + (long)t0 * ldg;
   la.ld = ldg;
@@ -561,16 +899,17 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
     lb.d0 = d0;
     lb.kvalid = vlim - v_begin;
     lb.dvalid = D - d0;
-    gemm_256x256(la, lb, nk, lds, acc);
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
   } else {
     TransLoader lb;
     lb.w = W + (long)v_begin * D + d0;
     lb.ld = D;
     lb.kvalid = vlim - v_begin;
     lb.dvalid = D - d0;
-    gemm_256x256(la, lb, nk, lds, acc);
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
   }
 
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -647,8 +986,7 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     const int vb = c * chunk;
     const int ve = (vb + chunk < V) ? vb + chunk : V;
     const int ctiles = (ve - vb + kTile - 1) / kTile;
-    const int gtotal = rtiles * ctiles;
-    dim3 ggrid(((gtotal + 7) / 8) * 8);
+    dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
     if (h.q4) {
       hipLaunchKernelGGL(lce_bwd_g_kernel<1>, ggrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll,
                          ignore_index, N, D, V, vb, ve, ctiles, chunk, Gbuf);
@@ -663,8 +1001,7 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     else if (c == 0) mode = 0;
     else if (c == nchunks - 1) mode = 2;
     else mode = 1;
-    const int htotal = rtiles * dtiles;
-    dim3 hgrid(((htotal + 7) / 8) * 8);
+    dim3 hgrid(8 * rtiles * ((dtiles + 7) / 8));
     if (h.q4) {
       hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, chunk, ctiles * kTile, h.w, h.wq, h.sc,
                          h.bi, N, D, V, vb, ve, acc32, dH, mode);
