@@ -1,0 +1,202 @@
+"""`enable_flash_attention`: switch a torch causal-LM's attention onto `flash_attention`
+(the torch counterpart of src/mlx_train_perf/attention/wrapper.py:205-292).
+
+Two model shapes are served:
+
+- **Hugging Face transformers models** (Llama / Qwen2 / Qwen3 / Mistral-style decoders): the
+  attention implementation is registered in transformers' `AttentionInterface` (`IMPL_NAME`)
+  and selected on the model config. Every decoder layer keeps its own projections, rotary
+  embedding and (Qwen3) q/k norms; only the single attention call changes, exactly the seam the
+  reference swaps (wrapper.py:126-157). A packed batch passes its `PackedMask` as the
+  `mtp_segments=` keyword of the model call; transformers forwards it to every layer.
+- **mlx-lm-style modules**: layers whose `self_attn` has `q_proj/k_proj/v_proj/o_proj`, a `rope`
+  callable, `n_heads`, `n_kv_heads`, `scale` (and optionally `q_norm/k_norm`) are wrapped in
+  `FlashAttentionWrapper`, which holds the original submodules under their original names (so
+  LoRA injection by module path keeps working, wrapper.py:17-31) and reproduces the stock call.
+
+Refusals (`UnsupportedAttentionError`, at enable time): sliding-window or mixed `layer_types`,
+configured attention dropout, head_dim outside {64, 96, 128}, an unrecognised model shape.
+There is no rate calibration on MI355X, so `seq_len`/`batch_size`/`packed` only validate the
+launch plan up front (`plan/launch.py`); nothing is pre-warmed.
+"""
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+from torch import nn
+
+from mlx_train_perf.attention.api import flash_attention
+from mlx_train_perf.attention.segments import PackedMask
+from mlx_train_perf.errors import AttentionInputError, UnsupportedAttentionError
+from mlx_train_perf.plan import launch as _plan
+
+_KERNEL_HEAD_DIMS: tuple[int, ...] = (64, 96, 128)
+IMPL_NAME = "mtp_hip_attention"  # no "flash" in the name: transformers routes such names to its kernel hub
+
+
+def _resolve_mask(mask: Any) -> bool | PackedMask:
+    """Map a caller's mask onto `flash_attention` (wrapper.py:72-96): "causal"/None -> causal,
+    a PackedMask passes through, anything else (array / additive / sliding masks) is refused."""
+    if isinstance(mask, PackedMask):
+        return mask
+    if isinstance(mask, str):
+        if mask == "causal":
+            return True
+        raise AttentionInputError(
+            f"unsupported string mask {mask!r}; the flash-attention training path only supports the 'causal' mask"
+        )
+    if mask is None:
+        return True
+    raise AttentionInputError(
+        "array attention masks (sliding-window / additive) are not supported; the flash-attention training "
+        "path is causal-only -- enable it only on full-attention models"
+    )
+
+
+def _hf_flash_attention(module: nn.Module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
+                        attention_mask: Any, scaling: float, dropout: float = 0.0,
+                        mtp_segments: PackedMask | None = None, **kwargs: Any):
+    """transformers attention-interface function: q (B,Hq,S,D), k/v (B,Hkv,S,D) post-RoPE;
+    returns (output (B,S,Hq,D), None)."""
+    if dropout:
+        raise UnsupportedAttentionError("flash-attention training path does not support attention dropout")
+    if attention_mask is not None and mtp_segments is None:
+        # transformers builds no mask for a registered implementation; an explicit one means padding
+        # or a sliding window, which this causal-only path cannot honour.
+        raise AttentionInputError("explicit attention masks are not supported by the flash-attention path")
+    impl = getattr(module.config, "_mtp_flash_impl", "auto")
+    out = flash_attention(query, key, value, scale=float(scaling), causal=True, impl=impl, segments=mtp_segments)
+    return out.transpose(1, 2).contiguous(), None
+
+
+class FlashAttentionWrapper(nn.Module):
+    """Drop-in replacement for an mlx-lm-style attention module (wrapper.py:99-157): original
+    submodules held as direct attributes under their original names; only the attention call is
+    swapped for `flash_attention`."""
+
+    def __init__(self, original: nn.Module, *, impl: str) -> None:
+        super().__init__()
+        self.q_proj = original.q_proj
+        self.k_proj = original.k_proj
+        self.v_proj = original.v_proj
+        self.o_proj = original.o_proj
+        self.rope = original.rope
+        self._has_qk_norm = hasattr(original, "q_norm")
+        if self._has_qk_norm:
+            self.q_norm = original.q_norm
+            self.k_norm = original.k_norm
+        self.n_heads = original.n_heads
+        self.n_kv_heads = original.n_kv_heads
+        self.scale = original.scale
+        self._impl = impl
+
+    def forward(self, x: torch.Tensor, mask: Any = None, cache: Any = None) -> torch.Tensor:
+        if cache is not None:
+            raise AttentionInputError("FlashAttentionWrapper is a training-only path; a KV cache is not supported")
+        b, length, _ = x.shape
+        queries, keys, values = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        queries = queries.reshape(b, length, self.n_heads, -1)
+        keys = keys.reshape(b, length, self.n_kv_heads, -1)
+        if self._has_qk_norm:
+            queries = self.q_norm(queries)
+            keys = self.k_norm(keys)
+        queries = queries.transpose(1, 2)
+        keys = keys.transpose(1, 2)
+        values = values.reshape(b, length, self.n_kv_heads, -1).transpose(1, 2)
+        queries = self.rope(queries)
+        keys = self.rope(keys)
+        resolved = _resolve_mask(mask)
+        segments = resolved if isinstance(resolved, PackedMask) else None
+        out = flash_attention(queries, keys, values, scale=self.scale, causal=True, segments=segments,
+                              impl=self._impl)  # type: ignore[arg-type]
+        return self.o_proj(out.transpose(1, 2).reshape(b, length, -1))
+
+
+def _config_of(model: Any) -> Any:
+    return getattr(model, "config", None) or getattr(model, "args", None)
+
+
+def _head_dim(cfg: Any) -> int:
+    hd = getattr(cfg, "head_dim", None)
+    if hd:
+        return int(hd)
+    return int(cfg.hidden_size // cfg.num_attention_heads)
+
+
+def _refusals(cfg: Any, layers: Any) -> int:
+    layer_types = getattr(cfg, "layer_types", None)
+    if layer_types is not None:
+        offending = sorted({lt for lt in layer_types if lt != "full_attention"})
+        if offending:
+            raise UnsupportedAttentionError(
+                f"enable_flash_attention supports full-attention models only; model declares non-full-attention "
+                f"layer_types {offending} -- sliding-window / mixed attention is out of scope"
+            )
+    if getattr(cfg, "use_sliding_window", False) or any(getattr(layer, "use_sliding", False) for layer in layers):
+        raise UnsupportedAttentionError(
+            "enable_flash_attention supports full-attention models only; model has sliding-window attention"
+        )
+    dropout = getattr(cfg, "attention_dropout", 0.0)
+    if dropout:
+        raise UnsupportedAttentionError(
+            f"enable_flash_attention does not support attention dropout (attention_dropout={dropout}); it must be 0"
+        )
+    head_dim = _head_dim(cfg)
+    if head_dim not in _KERNEL_HEAD_DIMS:
+        raise UnsupportedAttentionError(
+            f"enable_flash_attention supports head_dim in {_KERNEL_HEAD_DIMS}; model has head_dim={head_dim}"
+        )
+    return head_dim
+
+
+def enable_flash_attention(model: Any, *, impl: str = "auto", seq_len: int | None = None, batch_size: int = 1,
+                           packed: bool = False) -> None:
+    """Enable the flash-attention training path on `model` in place (wrapper.py:205-292).
+
+    `impl`: forwarded to `flash_attention` per call ("auto"/"kernel" -> HIP kernels,
+    "reference" -> the materialized oracle, small shapes only). `seq_len`/`batch_size`: when given,
+    the launch plan for that shape is computed now so an unsupported shape fails at enable time."""
+    cfg = _config_of(model)
+    inner = getattr(model, "model", None)
+    layers = getattr(inner, "layers", None)
+    if cfg is None or layers is None:
+        raise UnsupportedAttentionError(
+            f"unsupported model architecture {type(model).__name__!r}: expected a causal LM with "
+            "`.model.layers` and a config"
+        )
+    _refusals(cfg, layers)
+    first = layers[0].self_attn
+    if hasattr(cfg, "_attn_implementation") and not hasattr(first, "rope"):
+        from transformers import AttentionInterface  # noqa: PLC0415 -- only for transformers models
+
+        AttentionInterface.register(IMPL_NAME, _hf_flash_attention)
+        try:
+            from transformers import AttentionMaskInterface  # noqa: PLC0415
+
+            AttentionMaskInterface.register(IMPL_NAME, lambda *a, **k: None)
+        except ImportError:
+            pass
+        cfg._mtp_flash_impl = impl
+        if hasattr(model, "set_attn_implementation"):
+            model.set_attn_implementation(IMPL_NAME)
+        else:
+            cfg._attn_implementation = IMPL_NAME
+    else:
+        for layer in layers:
+            if not isinstance(layer.self_attn, FlashAttentionWrapper):
+                layer.self_attn = FlashAttentionWrapper(layer.self_attn, impl=impl)
+    if seq_len is not None and impl in ("auto", "kernel"):
+        hq = int(cfg.num_attention_heads)
+        hkv = int(getattr(cfg, "num_key_value_heads", hq) or hq)
+        if hq % hkv:
+            raise UnsupportedAttentionError(f"Hq={hq} must be a multiple of Hkv={hkv}")
+        _plan.attn_plan(b=batch_size, hq=hq, hkv=hkv, s=seq_len)
+
+
+def is_enabled(model: Any) -> bool:
+    cfg = _config_of(model)
+    if cfg is not None and getattr(cfg, "_attn_implementation", None) == IMPL_NAME:
+        return True
+    layers = getattr(getattr(model, "model", None), "layers", None) or []
+    return bool(layers) and all(isinstance(layer.self_attn, FlashAttentionWrapper) for layer in layers)

@@ -1,0 +1,118 @@
+"""Memory planner for the hot path, sized for one MI355X (288 GB HBM3E).
+
+The reference fits empirical coefficients for a 32 GB unified-memory Mac (plan/estimate.py,
+calibration_data.json). Its hot-path terms are analytic and are kept here, re-derived for this
+build's kernels and workspaces:
+- loss layer (`_loss_bytes`, plan/estimate.py:252-271): kernel forward = the three fp32 outputs
+  plus the vocab-split partials; the backward adds the bf16 gradient chunk and (multi-chunk) the
+  fp32 dH accumulator; chunked = fp32 logits chunk x 3; naive = the full (N, V) fp32 logits plus
+  softmax intermediates;
+- flash-attention saved state (`_flash_saved_state_bytes`, plan/estimate.py:210-220): O in the
+  compute dtype plus the fp32 L per layer, and the backward's fp32 D vector.
+Whole-model terms (weights, optimizer, activations) are caller-supplied because they depend on the
+model, not on this path.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+from mlx_train_perf.errors import DoesNotFitError, PlanInputError
+from mlx_train_perf.plan import launch as _launch
+
+HBM_BYTES_MI355X = 288 * 10**9
+_DTYPE_BYTES = {"bf16": 2, "bfloat16": 2, "fp16": 2, "float16": 2, "fp32": 4, "float32": 4}
+
+
+def dtype_bytes(dtype: str) -> int:
+    try:
+        return _DTYPE_BYTES[dtype]
+    except KeyError:
+        raise PlanInputError(f"unknown dtype {dtype!r}; expected one of {sorted(_DTYPE_BYTES)}") from None
+
+
+@dataclass(frozen=True)
+class LossBytes:
+    forward_peak: int
+    backward_workspace: int
+
+
+def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf16", chunk: int | None = None,
+               bwd_budget: int | None = None) -> LossBytes:
+    """Loss-layer memory beyond its inputs: forward marginal peak and backward workspace.
+    The backward's returned dH (n*d*dtype) is the caller's gradient, not counted here."""
+    if n < 1 or d < 1 or v < 1:
+        raise PlanInputError("n, d, v must be >= 1")
+    eb = dtype_bytes(dtype)
+    if impl == "kernel":
+        fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)
+        c = chunk or _launch.lce_bwd_chunk(n, d, v, bwd_budget or _launch.lce_bwd_budget_bytes())
+        bwd = _launch.lce_bwd_workspace_bytes(n, d, v, c) + n * 4
+    elif impl == "chunked":
+        c = chunk or 8192
+        fwd = 3 * n * min(c, v) * 4 + 2 * n * 4
+        bwd = 3 * n * min(c, v) * 4 + n * d * 4 + n * min(c, v) * eb
+    elif impl == "naive":
+        fwd = 2 * n * v * 4 + n * v * eb
+        bwd = 2 * n * v * 4
+    else:
+        raise PlanInputError(f"unknown impl {impl!r}; expected 'naive', 'chunked', or 'kernel'")
+    return LossBytes(forward_peak=fwd, backward_workspace=bwd)
+
+
+def flash_saved_state_bytes(*, batch: int, seq_len: int, heads: int, head_dim: int, dtype: str = "bf16") -> int:
+    """Per attention layer: O (batch*heads*seq*head_dim, compute dtype) + L (batch*heads*seq fp32)."""
+    return batch * heads * seq_len * head_dim * dtype_bytes(dtype) + batch * heads * seq_len * 4
+
+
+def stock_attention_bytes(*, batch: int, seq_len: int, heads: int) -> int:
+    """One layer's materialized fp32 (S, S) scores + probabilities, what the flash path removes."""
+    return 2 * batch * heads * seq_len * seq_len * 4
+
+
+@dataclass
+class Plan:
+    components: dict[str, int] = field(default_factory=dict)
+
+    @property
+    def total(self) -> int:
+        return sum(self.components.values())
+
+
+def estimate_peak(*, n_layers: int, batch: int, seq_len: int, hidden: int, vocab: int, heads: int, kv_heads: int,
+                  head_dim: int, dtype: str = "bf16", attention: str = "flash", loss_impl: str = "kernel",
+                  weights_bytes: int = 0, optimizer_bytes: int = 0, activation_bytes: int = 0) -> Plan:
+    """Predicted peak bytes of a training step: hot-path terms computed here, model terms supplied."""
+    if heads % kv_heads:
+        raise PlanInputError(f"heads={heads} must be a multiple of kv_heads={kv_heads}")
+    n = batch * seq_len
+    lb = loss_bytes(n=n, d=hidden, v=vocab, impl=loss_impl, dtype=dtype)
+    if attention == "flash":
+        attn = n_layers * flash_saved_state_bytes(batch=batch, seq_len=seq_len, heads=heads, head_dim=head_dim,
+                                                  dtype=dtype) + batch * heads * seq_len * 4
+    elif attention == "stock":
+        attn = stock_attention_bytes(batch=batch, seq_len=seq_len, heads=heads)
+    else:
+        raise PlanInputError(f"unknown attention {attention!r}; expected 'stock' or 'flash'")
+    return Plan(components={
+        "weights": weights_bytes, "optimizer": optimizer_bytes, "activations": activation_bytes,
+        "attention": attn, "loss": max(lb.forward_peak, lb.backward_workspace),
+    })
+
+
+def plan_fit(plan: Plan, *, budget_bytes: int | None = None, headroom: float = 0.05) -> int:
+    """Return the planned peak, raising DoesNotFitError above (1 - headroom) * budget (default:
+    the free memory of the current GPU when one is visible, else 288 GB)."""
+    if budget_bytes is None:
+        budget_bytes = HBM_BYTES_MI355X
+        try:
+            import torch  # noqa: PLC0415
+
+            if torch.cuda.is_available():
+                budget_bytes = torch.cuda.mem_get_info()[0]
+        except Exception:  # noqa: BLE001 -- a planner must work without a GPU
+            pass
+    limit = int(budget_bytes * (1 - headroom))
+    if plan.total > limit:
+        raise DoesNotFitError(f"predicted peak {plan.total / 1e9:.2f} GB exceeds {limit / 1e9:.2f} GB "
+                              f"({', '.join(f'{k}={v / 1e9:.2f}' for k, v in plan.components.items())})")
+    return plan.total

@@ -58,3 +58,23 @@ def test_attention_plan():
     assert p.fwd_workgroups == (8192 // 32) * 8
     assert p.dkv_workgroups == 64 * 8
     assert plan.attn_heads_per_workgroup(6, 3) == 2 and plan.attn_heads_per_workgroup(3, 1) == 1
+
+
+def test_memory_planner_terms():
+    from mlx_train_perf.errors import DoesNotFitError, PlanInputError
+    from mlx_train_perf.plan import estimate as est
+
+    lb = est.loss_bytes(n=8192, d=4096, v=151936, impl="kernel")
+    assert lb.forward_peak == 3 * 8192 * 4 + plan.lce_fwd_workspace_bytes(8192, 151936) < 0.01e9
+    assert est.loss_bytes(n=8192, d=4096, v=151936, impl="naive").forward_peak > 4.9e9
+    assert est.flash_saved_state_bytes(batch=1, seq_len=8192, heads=32, head_dim=128) == 8192 * 32 * 128 * 2 + 8192 * 32 * 4
+    p = est.estimate_peak(n_layers=32, batch=1, seq_len=8192, hidden=4096, vocab=151936, heads=32, kv_heads=8,
+                          head_dim=128, weights_bytes=16 * 10**9)
+    assert est.plan_fit(p, budget_bytes=288 * 10**9) == p.total
+    with pytest.raises(DoesNotFitError):
+        est.plan_fit(p, budget_bytes=10 * 10**9)
+    stock = est.estimate_peak(n_layers=32, batch=1, seq_len=8192, hidden=4096, vocab=151936, heads=32, kv_heads=8,
+                              head_dim=128, attention="stock", loss_impl="naive")
+    assert stock.components["attention"] > p.components["attention"]
+    with pytest.raises(PlanInputError):
+        est.loss_bytes(n=1, d=1, v=1, impl="fast")
