@@ -29,6 +29,16 @@ namespace mtp {
 
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 
+// The dQ kernel stages one K/V tile in LDS (51 KiB at head_dim 128) and prefetches the next into
+// registers, so two workgroups (8 waves) share a CU; MTP_DQ_BUFS=2 double-buffers instead.
+#ifndef MTP_DQ_BUFS
+#define MTP_DQ_BUFS 1
+#endif
+// The dK/dV kernel processes each 64-query tile as two 32-query halves (fewer live registers).
+#ifndef MTP_DKV_HALVES
+#define MTP_DKV_HALVES 1
+#endif
+
 template <int DH>
 struct AttnCfg {
   static constexpr int kNatStride = DH * 2 + 16;
@@ -298,14 +308,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dvec_kernel(const bf16_t* __rest
 // Backward dQ (query-row owners; no atomics).
 // ------------------------------------------------------------------------------------------
 template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MTP_DQ_BUFS == 1 ? 2 : 1, MTP_DQ_BUFS == 1 ? 2 : 1)))
 void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                         const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
                         const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                         bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
   using C = AttnCfg<DH>;
   constexpr int kStage = 2 * C::kNatBytes + C::kTBytes + 256;  // K, V natural; K^T; key segment ids
-  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
+  constexpr int kBufs = MTP_DQ_BUFS;
+  __shared__ __attribute__((aligned(16))) char lds[kBufs * kStage];
 
   const int G = Hq / Hkv;
   const int hpw = heads_per_wg(G);
@@ -391,7 +402,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
   }
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const char* cur = lds + (t & 1) * kStage;
+    const char* cur = lds + (kBufs == 2 ? (t & 1) * kStage : 0);
     const int kv0 = kv_begin + t * kKT;
     const bool more = t + 1 < ntiles;
     if (more) load_tile(t + 1);
@@ -434,8 +445,16 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc[db] = mfma32(t_frag(kt, 32 * db + col, ks, hf), sf[ks], acc[db]);
     }
-    if (more) store_tile(lds + ((t + 1) & 1) * kStage);
-    __syncthreads();
+    if constexpr (kBufs == 2) {
+      if (more) store_tile(lds + ((t + 1) & 1) * kStage);
+      __syncthreads();
+    } else {
+      __syncthreads();
+      if (more) {
+        store_tile(lds);
+        __syncthreads();
+      }
+    }
   }
 
   if (qvalid) {
@@ -573,6 +592,55 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
       sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
     }
     if (!skip) {
+      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
+      const float* l2s = reinterpret_cast<const float*>(cur + 2 * C::kNatBytes + 2 * C::kTBytes);
+      const float* ds_ = l2s + 64;
+      const int* segs = reinterpret_cast<const int*>(l2s + 128);
+      const char* qt = cur + 2 * C::kNatBytes;
+      const char* dt = qt + C::kTBytes;
+#if MTP_DKV_HALVES
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x16 sacc, pacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[r] = 0.f;
+          pacc[r] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::kDK; ++ks) {
+          sacc = mfma32(nat_frag<DH>(cur, 32 * qb + col, ks, hf), kf[ks], sacc);
+          pacc = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * qb + col, ks, hf), vf[ks], pacc);
+        }
+        bf16x8 pf[2], sf[2];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * rq + u;
+            float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
+            if (need_mask) {
+              const int qq = q0 + ql0 + u;
+              bool ok = (kj <= qq) && (qq < S) && kvalid;
+              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
+              if (!ok) p = 0.f;
+            }
+            pf[r >> 3][r & 7] = (__bf16)p;
+            sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[u]));
+          }
+        }
+#pragma unroll
+        for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) {
+            dva[db] = mfma32(t_frag(dt, 32 * db + col, 2 * qb + kk, hf), pf[kk], dva[db]);
+            dka[db] = mfma32(t_frag(qt, 32 * db + col, 2 * qb + kk, hf), sf[kk], dka[db]);
+          }
+      }
+#else
       f32x16 sacc[2], pacc[2];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
@@ -587,10 +655,6 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
           pacc[qb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * qb + col, ks, hf), vf[ks], pacc[qb]);
         }
       }
-      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
-      const float* l2s = reinterpret_cast<const float*>(cur + 2 * C::kNatBytes + 2 * C::kTBytes);
-      const float* ds_ = l2s + 64;
-      const int* segs = reinterpret_cast<const int*>(l2s + 128);
       bf16x8 pf[4], sf[4];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb)
@@ -613,8 +677,6 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
             sf[2 * qb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[qb][r] - d4[u]));
           }
         }
-      const char* qt = cur + 2 * C::kNatBytes;
-      const char* dt = qt + C::kTBytes;
 #pragma unroll
       for (int db = 0; db < C::kDB; ++db)
 #pragma unroll
@@ -622,6 +684,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
           dva[db] = mfma32(t_frag(dt, 32 * db + col, ks, hf), pf[ks], dva[db]);
           dka[db] = mfma32(t_frag(qt, 32 * db + col, ks, hf), sf[ks], dka[db]);
         }
+#endif
     }
     if (more) store_tile(lds + ((it + 1) & 1) * kStage);
     __syncthreads();

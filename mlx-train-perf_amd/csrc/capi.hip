@@ -136,11 +136,12 @@ size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
 
 int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,
                 const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
-                const float* lse, const float* d_nll, void* d_hidden, int64_t chunk, void* workspace,
+                const float* lse, const float* d_nll, void* d_hidden, void* d_w, int64_t chunk, void* workspace,
                 size_t workspace_bytes, void* stream) {
   int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
   if (rc) return rc;
   if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
+  if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   const size_t need = mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk);
@@ -151,7 +152,8 @@ int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
   float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)n * (size_t)chunk * 2);
   hipError_t e = mtp::launch_lce_bwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
                                      targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
-                                     static_cast<mtp::bf16_t*>(d_hidden), gbuf, acc32, static_cast<hipStream_t>(stream));
+                                     static_cast<mtp::bf16_t*>(d_hidden), static_cast<mtp::bf16_t*>(d_w), gbuf, acc32,
+                                     static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -937,6 +937,55 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
 
 
 // ------------------------------------------------------------------------------------------
+// Backward step 3 (trainable dense head only): dW[v][d] = sum_t G[t][v] H[t][d] for the vocab rows
+// of one chunk, written once in bf16 (each output tile has a single owner: no atomics). Both
+// operands are read transposed (the contraction runs over tokens, the leading index of G and H).
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __restrict__ H, int N, int D, int V,
+                       int v_begin, int v_end, int ctiles, bf16_t* __restrict__ dW) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  const int dtiles = (D + kTile - 1) / kTile;
+  int vt, dt;
+  if (!xcd_tile(ctiles, dtiles, vt, dt)) return;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int wa = w & 1, wb = w >> 1;
+  const int lhalf = lane >> 5, lcol = lane & 31;
+  const int vlim = v_end < V ? v_end : V;
+  const int v0 = v_begin + vt * kTile;
+  const int d0 = dt * kTile;
+  const int nk = (N + kBK - 1) / kBK;
+  const bool full = (N % kBK == 0) && (v0 + kTile <= vlim) && (d0 + kTile <= D);
+
+  f32x16 acc[4][kNJ];
+  TransLoader la;
+  la.w = G + (v0 - v_begin);
+  la.ld = ldg;
+  la.kvalid = N;
+  la.dvalid = vlim - v0;
+  TransLoader lb;
+  lb.w = H + d0;
+  lb.ld = D;
+  lb.kvalid = N;
+  lb.dvalid = D - d0;
+  if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
+
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int v = v0 + 128 * wa + 32 * i + 8 * (r >> 2) + 4 * lhalf + (r & 3);
+      if (v >= vlim) continue;
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j) {
+        const int d = d0 + 64 * wb + 32 * j + lcol;
+        if (d < D) dW[(long)v * D + d] = __builtin_bit_cast(bf16_t, (__bf16)acc[i][j][r]);
+      }
+    }
+}
+
+// ------------------------------------------------------------------------------------------
 // Host-side launchers (called from the C-ABI after validation).
 // ------------------------------------------------------------------------------------------
 int lce_fwd_nsplit(long N, long V) {
@@ -977,7 +1026,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
-                          bf16_t* dH, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   const int nchunks = (V + chunk - 1) / chunk;
@@ -1011,6 +1060,12 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (dW != nullptr && !h.q4) {
+      dim3 wgrid(8 * ctiles * ((dtiles + 7) / 8));
+      hipLaunchKernelGGL(lce_bwd_dw_kernel, wgrid, block, 0, stream, Gbuf, chunk, H, N, D, V, vb, ve, ctiles, dW);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }

@@ -27,7 +27,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
-                          bf16_t* dH, bf16_t* Gbuf, float* acc32, hipStream_t stream);
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream);
 
 struct AttnShape {
   int b, hq, hkv, s, dh;

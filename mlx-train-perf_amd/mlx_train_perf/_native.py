@@ -58,7 +58,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64]),
     "mtp_lce_bwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
-                                   _i64, _c_void_p, _size, _c_void_p]),
+                                   _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
     "mtp_attn_fwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                     _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "mtp_attn_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),

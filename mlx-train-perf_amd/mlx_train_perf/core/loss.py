@@ -98,11 +98,6 @@ def _require_kernel_supported(*, head: HeadRef, dtype: torch.dtype) -> None:
             raise UnsupportedHeadError(
                 f"kernel impl requires the hidden dim to be a multiple of 8 (got d={d}); use impl='chunked'."
             )
-        if head.trainable:
-            raise UnsupportedHeadError(
-                "kernel impl on MI355X serves frozen heads (LoRA/QLoRA): dL/dW is not built; pass "
-                "DenseHead(weight=..., trainable=False) or use impl='chunked' for a trainable head."
-            )
 
 
 def resolve_impl(*, head: HeadRef, dtype: torch.dtype, n: int, impl: str = "auto",
@@ -213,7 +208,8 @@ VJP_CALLS: dict[str, int] = {}
 
 
 class _KernelLCE(torch.autograd.Function):
-    """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only."""
+    """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only; it also
+    returns dL/dW when the dense head is an input that requires grad (trainable head)."""
 
     @staticmethod
     def forward(ctx, hidden2, targets2, w, w_q, scales, biases, head_kind, ignore_index, bwd_chunk):
@@ -250,13 +246,14 @@ class _KernelLCE(torch.autograd.Function):
         ws_bytes = lib.mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
         d_hidden = torch.empty_like(hidden2)
+        d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
         ct = d_nll.to(torch.float32).contiguous()
         rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
                              _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ctx.ignore_index,
-                             lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(), chunk, ws.data_ptr(), ws_bytes,
-                             _native.stream_of(hidden2))
+                             lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(), _native.ptr(d_w), chunk,
+                             ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
-        return d_hidden, None, None, None, None, None, None, None, None
+        return d_hidden, None, d_w, None, None, None, None, None, None
 
 
 def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor, *, ignore_index: int = -100,
@@ -266,7 +263,10 @@ def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.T
     h = hidden2.contiguous()
     t = targets2.to(torch.int64).contiguous()
     if isinstance(head, DenseHead):
-        args = (head.weight.detach().contiguous(), None, None, None, _native.HEAD_DENSE)
+        w = head.weight if head.trainable else head.weight.detach()
+        if not w.is_contiguous():
+            raise UnsupportedHeadError("kernel impl needs a contiguous (V, D) head weight")
+        args = (w, None, None, None, _native.HEAD_DENSE)
     else:
         args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
     return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0))

@@ -88,6 +88,28 @@ def backward(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, lse: 
     return dh
 
 
+def backward_dw(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, lse: torch.Tensor,
+                cotangent: torch.Tensor, *, ignore_index: int = -100, round_g_bf16: bool = True, chunk: int = 8192,
+                dtype: torch.dtype = torch.float64) -> torch.Tensor:
+    """d_w (V,D) of a trainable head: per vocab chunk g.T @ hidden (core/chunked.py:87-90), with the
+    same g as `backward`."""
+    v = w.shape[0]
+    h = hidden.to(dtype)
+    y = targets.long()
+    ct = torch.where(y == ignore_index, torch.zeros_like(cotangent, dtype=dtype), cotangent.to(dtype))
+    out = torch.empty((v, hidden.shape[1]), dtype=dtype)
+    for v0 in range(0, v, chunk):
+        v1 = min(v0 + chunk, v)
+        wc = w[v0:v1].to(dtype)
+        p = torch.exp(h @ wc.T - lse.to(dtype)[:, None])
+        onehot = (torch.arange(v0, v1)[None, :] == y[:, None]).to(dtype)
+        g = (p - onehot) * ct[:, None]
+        if round_g_bf16:
+            g = _bf16_round(g)
+        out[v0:v1] = g.T @ h
+    return out
+
+
 def reduce_mean(nll: torch.Tensor, targets: torch.Tensor, ignore_index: int = -100) -> torch.Tensor:
     """Mean over non-ignored rows (the adapter's (nll * mask).sum() / ntoks, adapters/mlx_lm.py:212-216)."""
     valid = targets.long() != ignore_index

@@ -56,8 +56,6 @@ def test_kernel_gate_refusals_are_typed():
     bf = torch.bfloat16
     with pytest.raises(UnsupportedHeadError):  # fp32 hidden: the MI355X kernel is bf16
         resolve_impl(head=_dense(), dtype=torch.float32, n=8)
-    with pytest.raises(UnsupportedHeadError):  # trainable dense head: dL/dW not built
-        resolve_impl(head=_dense(trainable=True, dtype=bf), dtype=bf, n=8)
     wq, sc, bi = oq.quantize_affine(torch.randn(10, 64))
     with pytest.raises(UnsupportedHeadError):
         resolve_impl(head=QuantizedHead(w_q=wq, scales=sc, biases=bi, bits=8), dtype=bf, n=8)

@@ -66,10 +66,12 @@ def test_lce_refusals():
     assert _lce_fwd(ws_bytes=8) == _native.MTP_ERR_WORKSPACE
     assert "workspace" in _native.last_error()
     lib = _native.load()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, 100, FAKE, 1 << 20, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_INPUT and "multiple of 256" in _native.last_error()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, 256, FAKE, 16, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 16, None)
     assert rc == _native.MTP_ERR_WORKSPACE
+    rc = lib.mtp_lce_bwd(FAKE, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 1 << 20, None)
+    assert rc == _native.MTP_ERR_UNSUPPORTED and "frozen" in _native.last_error()
 
 
 def test_attention_refusals():

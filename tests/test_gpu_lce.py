@@ -129,3 +129,22 @@ def test_golden_fixtures():
     nll.backward(q["cotangent"].float().cuda())
     assert (nll.cpu().double() - q["nll"]).abs().max() <= 8e-3
     assert rel_l2(hd.grad.cpu(), q["d_hidden"]) <= 1e-2
+
+
+@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (300, 256, 3000, 1024), (512, 512, 5000, None)])
+def test_trainable_head_dw_parity(n, d, v, chunk):
+    from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
+
+    print(f"[lce dw] n={n} d={d} v={v} chunk={chunk}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=21 + n)
+    hd = h.cuda().requires_grad_(True)
+    wd = w.cuda().requires_grad_(True)
+    nll, lse, _ = kernel_forward_parts(hd, DenseHead(weight=wd, trainable=True), t.cuda(), ignore_index=IGN,
+                                       bwd_chunk=chunk)
+    ct = _cotangent(t)
+    nll.backward(ct.cuda())
+    _, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, dtype=torch.float64)
+    odw = olce.backward_dw(h, w, t, olse, ct, ignore_index=IGN)
+    assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+    assert rel_l2(wd.grad.cpu(), odw) <= 1e-2

@@ -117,3 +117,15 @@ def test_bf16_rounding_of_g_is_small():
     a = olce.backward(h, w, t, lse, ct, round_g_bf16=True, dtype=torch.float64)
     b = olce.backward(h, w, t, lse, ct, round_g_bf16=False, dtype=torch.float64)
     assert float((a - b).norm() / b.norm()) < 5e-3
+
+
+def test_dw_matches_autograd_of_naive():
+    h, w, t = lce_inputs(20, 16, 90, seed=11, ignore_frac=0.1)
+    ct = torch.rand(20, generator=torch.Generator().manual_seed(3)) + 0.5
+    _, lse, _ = olce.forward(h, w, t)
+    dw = olce.backward_dw(h, w, t, lse, ct, round_g_bf16=False, chunk=33)
+    ww = w.double().clone().requires_grad_(True)
+    safe = torch.where(t == -100, torch.zeros_like(t), t)
+    nll = olce.naive_linear_ce(h.double(), ww, safe, dtype=torch.float64)
+    (nll * torch.where(t == -100, 0.0, ct.double())).sum().backward()
+    assert torch.allclose(dw, ww.grad, atol=1e-12)
