@@ -59,6 +59,7 @@ mtp::LceHead make_head(const void* w, const uint32_t* w_q, const void* scales, c
   mtp::LceHead h;
   h.q4 = head_kind == MTP_HEAD_Q4;
   h.w = static_cast<const mtp::bf16_t*>(w);
+  h.wt = nullptr;
   h.wq = w_q;
   h.sc = static_cast<const mtp::bf16_t*>(scales);
   h.bi = static_cast<const mtp::bf16_t*>(biases);
@@ -115,11 +116,11 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) 
   if (n < 1 || d < 1 || v < 1) return 0;
   const int64_t vpad = round_up(v, kTile);
   // One chunk if the whole padded vocab fits the budget; otherwise the budget also carries the
-  // fp32 dH accumulator.
-  if ((size_t)n * (size_t)vpad * 2 <= budget_bytes) return vpad;
+  // fp32 dH accumulator. Gradient-tile rows are chunk + kGPitchPad elements apart.
+  if ((size_t)n * (size_t)(vpad + mtp::kGPitchPad) * 2 <= budget_bytes) return vpad;
   const size_t acc = (size_t)n * (size_t)d * 4;
   const size_t rest = budget_bytes > acc ? budget_bytes - acc : 0;
-  int64_t c = (int64_t)(rest / ((size_t)n * 2)) / kTile * kTile;
+  int64_t c = ((int64_t)(rest / ((size_t)n * 2)) - mtp::kGPitchPad) / kTile * kTile;
   if (c < kTile) c = kTile;
   if (c > vpad) c = vpad;
   return c;
@@ -129,17 +130,32 @@ size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
   (void)head_kind;
   if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
   const int64_t nchunks = (v + chunk - 1) / chunk;
-  size_t bytes = (size_t)n * (size_t)chunk * 2;
+  size_t bytes = (size_t)n * (size_t)(chunk + mtp::kGPitchPad) * 2;
   if (nchunks > 1) bytes += (size_t)n * (size_t)d * 4;
   return bytes;
 }
 
-int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,
-                const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
-                const float* lse, const float* d_nll, void* d_hidden, void* d_w, int64_t chunk, void* workspace,
-                size_t workspace_bytes, void* stream) {
+int64_t mtp_lce_head_t_ld(int64_t v) { return v < 1 ? 0 : (int64_t)mtp::lce_head_t_ld((long)v); }
+
+int mtp_lce_head_transpose(const void* w, int64_t v, int64_t d, void* w_t, void* stream) {
+  if (v < 1 || d < 1 || v > kMaxDim || d > kMaxDim) return fail(MTP_ERR_INPUT, "v, d must be in [1, 2^31) (got v=%lld d=%lld)", (long long)v, (long long)d);
+  if (!w || !w_t) return fail(MTP_ERR_INPUT, "w and w_t must be non-null");
+  if (!aligned16(w) || !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w and w_t must be 16-byte aligned");
+  if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "head transpose requires d %% 8 == 0 (got d=%lld)", (long long)d);
+  hipError_t e = mtp::launch_lce_head_transpose(static_cast<const mtp::bf16_t*>(w), (int)v, (int)d,
+                                                static_cast<mtp::bf16_t*>(w_t), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "head transpose launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32_t* w_q, const void* scales,
+                const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind,
+                int64_t ignore_index, const float* lse, const float* d_nll, void* d_hidden, void* d_w, int64_t chunk,
+                void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
   if (rc) return rc;
+  if (w_t && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_INPUT, "w_t is the transposed dense head: it must be null for a quantized head");
+  if (w_t && !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w_t must be 16-byte aligned");
   if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
   if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
@@ -149,8 +165,10 @@ int mtp_lce_bwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
     return fail(MTP_ERR_WORKSPACE, "lce backward needs a workspace of %zu bytes at chunk=%lld (got %zu)", need, (long long)chunk, workspace ? workspace_bytes : (size_t)0);
   if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
   mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
-  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)n * (size_t)chunk * 2);
-  hipError_t e = mtp::launch_lce_bwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
+  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)n * (size_t)(chunk + mtp::kGPitchPad) * 2);
+  mtp::LceHead head = make_head(w, w_q, scales, biases, head_kind);
+  head.wt = static_cast<const mtp::bf16_t*>(w_t);
+  hipError_t e = mtp::launch_lce_bwd(head, static_cast<const mtp::bf16_t*>(hidden),
                                      targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
                                      static_cast<mtp::bf16_t*>(d_hidden), static_cast<mtp::bf16_t*>(d_w), gbuf, acc32,
                                      static_cast<hipStream_t>(stream));

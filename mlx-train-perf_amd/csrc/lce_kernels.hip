@@ -12,9 +12,11 @@
 // the second product, chunked.py:84-86), and a second MFMA GEMM accumulates G . W_chunk into an
 // fp32 dH accumulator that is rounded to bf16 once, after the last chunk.
 //
-// All GEMM-shaped work uses one 256x256 workgroup tile (4 waves, each a 128x128 sub-tile of
-// 4x4 MFMA 32x32x16 blocks), BK = 64, double-buffered swizzled LDS (2 x 64 KiB) with a
-// global->register prefetch of the next K slab issued before the current slab's MFMAs.
+// All GEMM-shaped work uses one 256x256 workgroup tile: 8 waves (2 per SIMD), each a 128x64
+// sub-tile of 4x2 MFMA 32x32x16 blocks, BK = 64, two LDS stages of 64 KiB. The hot path feeds the
+// stages by direct global->LDS copies (gemm_dma); the register-staged core (gemm_256x256) serves
+// the 4-bit head, whose rows are dequantized in registers, and shapes whose contraction length is
+// not a multiple of 64.
 #include "mtp_common.hpp"
 #include "mtp_launch.hpp"
 
@@ -26,11 +28,6 @@ constexpr int kThreads = 512;          // 8 waves: 2 per SIMD
 constexpr int kNJ = 2;                 // 32-wide MFMA blocks per wave along the B rows
 constexpr int kLdsBytes = 4 * 32768;  // A0, B0, A1, B1 (each 256 rows x 128 B)
 
-// Interior tiles use the direct-to-LDS ring core when MTP_LCE_RING is 1, else the
-// register-staged double-buffered core.
-#ifndef MTP_LCE_RING
-#define MTP_LCE_RING 0
-#endif
 
 // ------------------------------------------------------------------------------------------
 // Operand loaders. Each produces a 256-row x 64-k bf16 tile in LDS (swizzled layout).
@@ -265,178 +262,196 @@ __device__ __forceinline__ void gemm_256x256(LA& la, LB& lb, int nk, char* lds, 
 }
 
 // ------------------------------------------------------------------------------------------
-// Interior-tile GEMM core: a 4-stage LDS ring, BK = 32 per stage (A 16 KiB + B 16 KiB).
-// Row-major bf16 operands are copied global -> LDS by the direct-to-LDS path
-// (global_load_lds_dwordx4, no staging registers) three stages ahead; operands that need
-// register work (4-bit dequant, W transpose) load one stage ahead into registers and are written
-// to LDS at the end of the iteration. Stage rows are 64 B (4 chunks), chunk c of row r stored at
-// slot c ^ ((r >> 1) & 3): conflict-free for the MFMA fragment reads (8 consecutive rows, one chunk).
-// Waits are explicit (s_waitcnt + s_barrier) so the direct-to-LDS copies stay in flight across
-// iterations.
+// DMA-fed GEMM core (the hot path). Both operand tiles are copied global -> LDS with
+// global_load_lds_dwordx4 (16 bytes per lane straight into LDS, no staging registers) in two
+// 64-deep stages of 64 KiB each (A tile at +0, B tile at +32 KiB). Per stage kt:
+//   k-steps 0..2: read the next k-step's fragments while the MFMAs of the current one run;
+//   then wait for this wave's fragment reads and for its copies of stage kt+1, s_barrier, issue
+//   the copies of stage kt+2 into the buffer just released, read stage kt+1's first fragments,
+//   and run k-step 3 on fragments that are already in registers.
+// The waits and the barrier are explicit so that the copies of one stage stay in flight while the
+// other stage is consumed. Requirements: every k-slab copied is in bounds and real (callers use
+// this core only when the contraction length is a multiple of 64); tile rows past the end of an
+// operand re-read its last row, and the epilogues discard those results.
 // ------------------------------------------------------------------------------------------
-constexpr int kRBK = 32;
-constexpr int kRing = 4;
-constexpr int kStageBytes = 32768;
+constexpr int kDmaStage = 65536;
 
-__device__ __forceinline__ int ring_off(int row, int c) { return row * 64 + ((c ^ ((row >> 1) & 3)) << 4); }
+__device__ __forceinline__ void raw_barrier() { asm volatile("s_barrier" ::: "memory"); }
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
-// s_waitcnt with vmcnt <= VM and lgkmcnt <= 0 (LGKM0) or unconstrained; expcnt unconstrained.
-template <int VM, bool LGKM0>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(VM >= 0 && VM < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((VM & 15) | (7 << 4) | ((LGKM0 ? 0 : 15) << 8) | ((VM >> 4) << 14));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// Buffer-resource copies global -> LDS (buffer_load_dwordx4 ... lds): an SGPR descriptor holds the
+// stage base and the readable byte count, each lane a 32-bit offset. Lanes whose offset falls
+// outside the readable range receive zeros instead of touching memory.
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t dma_rsrc(const char* base, long bytes) {
+  const int n = bytes <= 0 ? 0 : (bytes > 0x7fffffffL ? 0x7fffffff : (int)bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, char* dst) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voff, 0, 0, 0);
 }
 
-// Direct-to-LDS row-major operand: each wave copies rows 32w .. 32w+31 (two 1 KiB instructions).
-struct DmaRowK {
-  static constexpr int kDma = 2;
-  static constexpr bool kReg = false;
-  const bf16_t* base;  // row 0 of the tile, k = 0
-  int o0, o1;          // per-lane element offsets of the two instructions
-  __device__ __forceinline__ void init(const bf16_t* b, int ld) {
-    base = b;
-    const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
-    const int c = (l & 3) ^ ((l >> 3) & 3);
-    o0 = (32 * w + (l >> 2)) * ld + 8 * c;
-    o1 = o0 + 16 * ld;
-  }
-  __device__ __forceinline__ void dma(int kt, char* tile) const {
-    const int w = threadIdx.x >> 6;
-    const bf16_t* b = base + kt * kRBK;
-    __builtin_amdgcn_global_load_lds(b + o0, tile + 2048 * w, 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(b + o1, tile + 2048 * w + 1024, 16, 0, 0);
-  }
-  __device__ __forceinline__ void reg_load(int) {}
-  __device__ __forceinline__ void commit(char*) const {}
-};
+// K-contiguous operand: tile row r, k in [64 kt, 64 kt + 64) of a row-major [rows][ld] matrix.
+// LDS rows are 128 B with the swizzle of lds_off(); fragments are single ds_read_b128.
+struct DmaRowOp {
+  static constexpr int kReads = 1;
+  const char* base;    // tile row 0, k = 0
+  long bytes;          // readable bytes from base (the tile's nrows rows)
+  uint32_t voff[4];    // per-lane byte offsets of this wave's four 1 KiB copies
+  int lo[4], sx[4];    // per-lane fragment row offsets and swizzle (per 32-row block)
 
-// 4-bit rows: thread t dequantizes 16 values (two words) of row t >> 1 per stage.
-struct Q4RingRowK {
-  static constexpr int kDma = 0;
-  static constexpr bool kReg = true;
-  const uint32_t* wq;
-  const bf16_t* sc;
-  const bf16_t* bi;
-  int K;
-  u32x2 q;
-  float s, b;
-  __device__ __forceinline__ void dma(int, char*) const {}
-  __device__ __forceinline__ void reg_load(int kt) {
-    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
-    q = *reinterpret_cast<const u32x2*>(wq + (long)row * (K >> 3) + kt * 4 + 2 * half);
-    const long g = (long)row * (K >> 6) + (kt >> 1);
-    s = bf16_to_f32(sc[g]);
-    b = bf16_to_f32(bi[g]);
-  }
-  __device__ __forceinline__ void commit(char* tile) const {
-    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
-    lds_write16(tile, ring_off(row, 2 * half), dequant8(q[0], s, b));
-    lds_write16(tile, ring_off(row, 2 * half + 1), dequant8(q[1], s, b));
-  }
-};
-
-// Transposed dense operand (tile rows are columns d of W [v][d]; k runs over v): threads 0..127
-// each load an 8 (v) x 8 (d) block and transpose it in registers.
-struct TransRing {
-  static constexpr int kDma = 0;
-  static constexpr bool kReg = true;
-  const bf16_t* w;  // row v = chunk start, column d0
-  int ld;
-  u32x4 x[8];
-  __device__ __forceinline__ void dma(int, char*) const {}
-  __device__ __forceinline__ void reg_load(int kt) {
-    const int tid = threadIdx.x;
-    if (tid >= 128) return;
-    const int vb = tid & 3, db = tid >> 2;
-    const bf16_t* b = w + (long)kt * kRBK * ld;
-    const int o = 8 * vb * ld + 8 * db;
+  __device__ __forceinline__ void init(const bf16_t* b, int ld, int nrows) {
+    base = reinterpret_cast<const char*>(b);
+    bytes = 2L * nrows * ld;
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = *reinterpret_cast<const u32x4*>(b + o + i * ld);
-  }
-  __device__ __forceinline__ void commit(char* tile) const {
-    const int tid = threadIdx.x;
-    if (tid >= 128) return;
-    const int vb = tid & 3, db = tid >> 2;
-    u32x4 y[8];
-    transpose8x8(x, y);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) lds_write16(tile, ring_off(8 * db + j, vb), y[j]);
-  }
-};
-
-// Transposed 4-bit operand: threads 0..127 dequantize an 8 (v) x 8 (d) block and transpose it.
-struct Q4TransRing {
-  static constexpr int kDma = 0;
-  static constexpr bool kReg = true;
-  const uint32_t* wq;  // row v = chunk start
-  const bf16_t* sc;
-  const bf16_t* bi;
-  int D, d0;
-  uint32_t q[8];
-  float s[8], b[8];
-  __device__ __forceinline__ void dma(int, char*) const {}
-  __device__ __forceinline__ void reg_load(int kt) {
-    const int tid = threadIdx.x;
-    if (tid >= 128) return;
-    const int vb = tid & 3, db = tid >> 2;
-    const int word = (d0 >> 3) + db;
-    const int grp = (d0 + 8 * db) >> 6;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const long k = (long)kt * kRBK + 8 * vb + i;
-      q[i] = wq[k * (D >> 3) + word];
-      s[i] = bf16_to_f32(sc[k * (D >> 6) + grp]);
-      b[i] = bf16_to_f32(bi[k * (D >> 6) + grp]);
+    for (int i = 0; i < 4; ++i) {
+      const int row = 64 * i + 8 * w + (L >> 3);  // copy 8 i + w covers rows 8 (8 i + w) .. +7
+      const int c = (L & 7) ^ swz(row);
+      const int src = row < nrows ? row : nrows - 1;
+      voff[i] = 2u * (uint32_t)(src * ld + 8 * c);
     }
   }
-  __device__ __forceinline__ void commit(char* tile) const {
-    const int tid = threadIdx.x;
-    if (tid >= 128) return;
-    const int vb = tid & 3, db = tid >> 2;
-    u32x4 x[8], y[8];
+  __device__ __forceinline__ void issue(int kt, char* dst) const { issue_at(0, kt, dst); }
+  // Copy from the tile `shift` bytes further on with the same per-lane offsets (valid when both
+  // tiles are whole, i.e. no row was clamped).
+  __device__ __forceinline__ void issue_at(long shift, int kt, char* dst) const {
+    const int w = threadIdx.x >> 6;
+    const long o = shift + kt * (2 * kBK);
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, bytes - kt * (2 * kBK));
 #pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = dequant8(q[i], s[i], b[i]);
-    transpose8x8(x, y);
+    for (int i = 0; i < 4; ++i) dma16(r, voff[i], dst + 1024 * (8 * i + w));
+  }
+  template <int NB>
+  __device__ __forceinline__ void setup(int first_row) {
+    const int lane = threadIdx.x & 63;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) lds_write16(tile, ring_off(8 * db + j, vb), y[j]);
+    for (int b = 0; b < NB; ++b) {
+      const int row = first_row + 32 * b + (lane & 31);
+      lo[b] = row * 128;
+      sx[b] = swz(row) ^ (lane >> 5);
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
+    return as_bf16x8(lds_read16(st, lo[b] + (((2 * ks) ^ sx[b]) << 4)));
   }
 };
 
-struct Frags {
-  bf16x8 a[4], b[kNJ];
+// K-major operand: element (k, col) at base[k * ld + col]; the tile holds 64 k-rows x 256
+// columns per stage as 512 B LDS rows whose 16-byte slots are XOR-swizzled by 4 * (k & 3).
+// Fragments are two ds_read_b64_tr_b16 (gfx950 LDS transpose read): in each group of 16 lanes,
+// lane s reads 4 columns of k-row (s >> 2) and receives 4 consecutive k of one column, so the
+// pair yields the 8 consecutive k an MFMA operand lane needs. k-rows at or past kvalid re-read
+// row kvalid - 1; columns at or past ncols re-read the last 8 columns.
+struct DmaTransOp {
+  static constexpr int kReads = 2;
+  const char* base;    // k = 0, column 0 of the tile
+  long ldb;            // row pitch in bytes
+  int kvalid;
+  int rk[4];           // per-lane k-row (within a stage) of the four copies
+  uint32_t cofs[4];    // per-lane column byte offsets
+  int lo[4];           // per-lane fragment offsets (per 32-column block)
+
+  __device__ __forceinline__ void init(const bf16_t* b, int ld, int kvalid_, int ncols) {
+    base = reinterpret_cast<const char*>(b);
+    ldb = 2L * ld;
+    kvalid = kvalid_;
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = 2 * (8 * i + w) + (L >> 5);  // copy 8 i + w covers k-rows 2 (8 i + w), +1
+      const int slot = (L & 31) ^ (4 * (row & 3));
+      int col = 8 * slot;
+      if (col > ncols - 8) col = ncols - 8;
+      rk[i] = row;
+      cofs[i] = 2u * (uint32_t)col;
+    }
+  }
+  __device__ __forceinline__ void issue(int kt, char* dst) const {
+    const int w = threadIdx.x >> 6;
+    const int k0 = kt * kBK;
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + k0 * ldb, (long)(kvalid - k0) * ldb);
+    const int kmax = kvalid - 1 - k0;  // last readable k-row of this stage (may be negative)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int k = rk[i] < kmax ? rk[i] : kmax;  // rows past kvalid re-read the last row
+      dma16(r, (uint32_t)k * (uint32_t)ldb + cofs[i], dst + 1024 * (8 * i + w));
+    }
+  }
+  template <int NB>
+  __device__ __forceinline__ void setup(int first_col) {
+    const int l = threadIdx.x & 63;
+    const int kl = 8 * (l >> 5) + ((l >> 2) & 3);
+    const int kr = (l >> 2) & 3;
+    const int low = 2 * ((l >> 4) & 1) + ((l & 3) >> 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int jb = (first_col >> 5) + b;
+      lo[b] = kl * 512 + (((4 * jb) ^ (4 * kr)) + low) * 16 + 8 * (l & 1);
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
+    const lds_bf16x4* p = (const lds_bf16x4*)(st + lo[b] + ks * 16 * 512);
+    const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+    const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
+    return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  }
 };
 
-__device__ __forceinline__ void read_frags(Frags& f, const char* stage, int ks, int wa, int wb, int lrow, int lhalf) {
-  const int c = 2 * ks + lhalf;
-  const char* cB = stage + 16384;
+template <class OA, class OB>
+__device__ __forceinline__ void dma_read_frags(const OA& oa, const OB& ob, const char* st, int ks, bf16x8 (&fa)[4],
+                                               bf16x8 (&fb)[kNJ]) {
+  // Issue order = first use order of the i-major MFMA sequence below: b0, a0, b1, a1, a2, a3.
+  fb[0] = ob.read(st + 32768, 0, ks);
+  fa[0] = oa.read(st, 0, ks);
+  fb[1] = ob.read(st + 32768, 1, ks);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) f.a[i] = as_bf16x8(lds_read16(stage, ring_off(128 * wa + 32 * i + lrow, c)));
-#pragma unroll
-  for (int j = 0; j < kNJ; ++j) f.b[j] = as_bf16x8(lds_read16(cB, ring_off(64 * wb + 32 * j + lrow, c)));
+  for (int i = 1; i < 4; ++i) fa[i] = oa.read(st, i, ks);
 }
 
-__device__ __forceinline__ void mma_frags(const Frags& f, f32x16 (&acc)[4][kNJ]) {
+__device__ __forceinline__ void dma_mfma(const bf16x8 (&fa)[4], const bf16x8 (&fb)[kNJ], f32x16 (&acc)[4][kNJ]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < kNJ; ++j) acc[i][j] = mfma32(f.a[i], f.b[j], acc[i][j]);
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = mfma32(fa[i], fb[j], acc[i][j]);
 }
 
-// Software pipeline (per iteration kt, stage kt in LDS buffer kt % 4):
-//   barrier                      -> stages <= kt+1 complete and visible; stage kt-1 no longer read
-//   [register loads for stage kt+2]; direct-to-LDS copies for stage kt+3
-//   read fragments (kt, k16 #1); MFMAs (kt, #0) on fragments read one step earlier
-//   read fragments (kt+1, #0);   MFMAs (kt, #1)
-//   [commit register stage kt+2]; wait: this wave's copies of stage kt+2 (and register loads) done
-// so LDS latency is always covered by a group of MFMAs, including across the barrier.
-template <class LA, class LB>
-__device__ __forceinline__ void gemm_ring(LA& la, LB& lb, int nk, char* lds, f32x16 (&acc)[4][kNJ]) {
-  constexpr int DMA = LA::kDma + LB::kDma;
-  constexpr bool REG = LA::kReg || LB::kReg;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int wa = w & 1, wb = w >> 1;
-  const int lrow = lane & 31, lhalf = lane >> 5;
+// Interleave the 8 MFMAs of a k-step with the NR LDS reads of the next one. The reads are packed
+// into the first FRONT MFMAs so that they complete before the next k-step needs them.
+#ifndef MTP_DMA_FRONT
+#define MTP_DMA_FRONT 4
+#endif
+template <int NR, int S = 0>
+__device__ __forceinline__ void dma_sched() {
+  if constexpr (S < 8) {
+    constexpr int F = MTP_DMA_FRONT;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int r = S < F ? NR * (S + 1) / F - NR * S / F : 0;
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    dma_sched<NR, S + 1>();
+  }
+}
+
+// acc[i][j] (wave sub-tile 128 x 64: wave w covers A rows 128 (w & 1) .., B rows 64 (w >> 1) ..)
+// = A_tile . B_tile^T over nk 64-deep slabs. `pre`: stages 0 and 1 were already issued (by the
+// previous call's `next`). `next` (may be null-like: has_next false) issues the following tile's
+// stages 0 and 1 after the last barrier, when both buffers are free. Returns with no LDS reads
+// outstanding; the caller must barrier before writing LDS itself.
+template <class OA, class OB, class NEXT>
+__device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x16 (&acc)[4][kNJ], bool pre,
+                                         bool has_next, const NEXT& next) {
+  constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
+  const int w = threadIdx.x >> 6;
+  oa.template setup<4>(128 * (w & 1));
+  ob.template setup<kNJ>(64 * (w >> 1));
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -444,69 +459,49 @@ __device__ __forceinline__ void gemm_ring(LA& la, LB& lb, int nk, char* lds, f32
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  auto stage = [&](int st) { return lds + (st & (kRing - 1)) * kStageBytes; };
-  if constexpr (REG) {
-    la.reg_load(0);
-    lb.reg_load(0);
-  }
-  for (int st = 0; st < kRing - 1; ++st) {
-    if (st < nk) {
-      la.dma(st, stage(st));
-      lb.dma(st, stage(st) + 16384);
-    }
-  }
-  if constexpr (REG) {
-    wait_vm<0, false>();
-    la.commit(stage(0));
-    lb.commit(stage(0) + 16384);
+  if (!pre) {
+    oa.issue(0, lds);
+    ob.issue(0, lds + 32768);
     if (nk > 1) {
-      la.reg_load(1);
-      lb.reg_load(1);
-      wait_vm<0, false>();
-      la.commit(stage(1));
-      lb.commit(stage(1) + 16384);
+      oa.issue(1, lds + kDmaStage);
+      ob.issue(1, lds + kDmaStage + 32768);
     }
-    wait_vm<0, true>();
-  } else {
-    if (nk > 2) wait_vm<DMA, true>();
-    else wait_vm<0, true>();
   }
-  __builtin_amdgcn_s_barrier();
-  Frags f0, f1;
-  read_frags(f0, stage(0), 0, wa, wb, lrow, lhalf);
+  if (nk > 1 && !pre) wait_vmcnt<8>(); else wait_vmcnt<0>();
+  raw_barrier();
 
+  bf16x8 fa[4], fb[kNJ], ga[4], gb[kNJ];
+  dma_read_frags(oa, ob, lds, 0, fa, fb);
   for (int kt = 0; kt < nk; ++kt) {
-    if (kt > 0) __builtin_amdgcn_s_barrier();
-    const bool reg_next = REG && (kt + 2 < nk);
-    if constexpr (REG) {
-      if (reg_next) {
-        la.reg_load(kt + 2);
-        lb.reg_load(kt + 2);
-      }
+    char* cur = lds + ((kt & 1) ? kDmaStage : 0);
+    char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
+    dma_read_frags(oa, ob, cur, 1, ga, gb);
+    dma_mfma(fa, fb, acc);
+    dma_sched<NR>();
+    dma_read_frags(oa, ob, cur, 2, fa, fb);
+    dma_mfma(ga, gb, acc);
+    dma_sched<NR>();
+    dma_read_frags(oa, ob, cur, 3, ga, gb);
+    dma_mfma(fa, fb, acc);
+    dma_sched<NR>();
+    wait_lgkmcnt0();
+    wait_vmcnt<0>();
+    raw_barrier();
+    if (kt + 2 < nk) {
+      oa.issue(kt + 2, cur);
+      ob.issue(kt + 2, cur + 32768);
+    } else if (kt + 1 == nk && has_next) {
+      next();
     }
-    const bool dma_next = (kt + kRing - 1) < nk;
-    if (dma_next) {
-      la.dma(kt + kRing - 1, stage(kt + kRing - 1));
-      lb.dma(kt + kRing - 1, stage(kt + kRing - 1) + 16384);
-    }
-    read_frags(f1, stage(kt), 1, wa, wb, lrow, lhalf);
-    mma_frags(f0, acc);
-    if (kt + 1 < nk) read_frags(f0, stage(kt + 1), 0, wa, wb, lrow, lhalf);
-    mma_frags(f1, acc);
-    if constexpr (REG) {
-      if (reg_next) {
-        if (dma_next) wait_vm<DMA, false>();
-        else wait_vm<0, false>();
-        la.commit(stage(kt + 2));
-        lb.commit(stage(kt + 2) + 16384);
-      }
-    }
-    // Stage kt+2 must be complete before the next barrier; only stage kt+3's copies may remain.
-    if (dma_next) wait_vm<DMA, true>();
-    else wait_vm<0, true>();
+    if (kt + 1 < nk) dma_read_frags(oa, ob, nxt, 0, fa, fb);
+    dma_mfma(ga, gb, acc);
+    dma_sched<NR>();
   }
-  __builtin_amdgcn_s_barrier();
 }
+
+struct NoNext {
+  __device__ __forceinline__ void operator()() const {}
+};
 
 // ------------------------------------------------------------------------------------------
 // Tile order for one-tile-per-workgroup launches. Workgroup g runs on XCD g % 8; each XCD gets a
@@ -563,47 +558,8 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     s[j] = 0.f;
   }
 
-  RowKLoader lb;
-  lb.base = H + (long)t0 * D;
-  lb.ld = D;
-  lb.nrows = N - t0;
-  lb.K = D;
-
-  for (int vt = vt_begin; vt < vt_end; ++vt) {
-    const int v0 = vt * kTile;
-    const bool full = (v0 + kTile <= V) && (t0 + kTile <= N) && (D % kBK == 0);
-    f32x16 acc[4][kNJ];
-    if (MTP_LCE_RING && full) {
-      DmaRowK rb;
-      rb.init(H + (long)t0 * D, D);
-      if constexpr (Q4) {
-        Q4RingRowK ra;
-        ra.wq = Wq + (long)v0 * (D >> 3);
-        ra.sc = Sc + (long)v0 * (D >> 6);
-        ra.bi = Bi + (long)v0 * (D >> 6);
-        ra.K = D;
-        gemm_ring(ra, rb, D / kRBK, lds, acc);
-      } else {
-        DmaRowK ra;
-        ra.init(W + (long)v0 * D, D);
-        gemm_ring(ra, rb, D / kRBK, lds, acc);
-      }
-    } else if constexpr (Q4) {
-      Q4RowKLoader la;
-      la.wq = Wq + (long)v0 * (D >> 3);
-      la.sc = Sc + (long)v0 * (D >> 6);
-      la.bi = Bi + (long)v0 * (D >> 6);
-      la.nrows = V - v0;
-      la.K = D;
-      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-    } else {
-      RowKLoader la;
-      la.base = W + (long)v0 * D;
-      la.ld = D;
-      la.nrows = V - v0;
-      la.K = D;
-      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-    }
+  // Online (max, sum exp2) update of this lane's token columns with one 256-row vocab tile.
+  auto consume = [&](f32x16 (&acc)[4][kNJ], int v0) {
     const bool tail = (v0 + kTile) > V;
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) {
@@ -629,6 +585,73 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
         for (int r = 0; r < 16; ++r) sum += fast_exp2(acc[i][j][r] - base);
       s[j] = s[j] * fast_exp2(m[j] - base) + sum;
       m[j] = mn;
+    }
+  };
+
+  if (!Q4 && D % kBK == 0) {
+    // Hot path: DMA-fed core; the next vocab tile's first two stages are issued during the last
+    // k-step of the current one.
+    DmaRowOp ob;
+    ob.init(H + (long)t0 * D, D, N - t0);
+    DmaRowOp oa;
+    oa.init(W + (long)vt_begin * kTile * D, D, V - vt_begin * kTile);
+    const long tile_bytes = 2L * kTile * D;
+    bool pre = false;
+    for (int vt = vt_begin; vt < vt_end; ++vt) {
+      const int v0 = vt * kTile;
+      const bool has_next = vt + 1 < vt_end;
+      // Both this tile and the next are whole: the next one reuses this tile's lane offsets.
+      const bool next_whole = v0 + 2 * kTile <= V;
+      auto next = [&]() {
+        if (next_whole) {
+          oa.issue_at(tile_bytes, 0, lds);
+          if (nk > 1) oa.issue_at(tile_bytes, 1, lds + kDmaStage);
+        } else {
+          DmaRowOp na;
+          na.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
+          na.issue(0, lds);
+          if (nk > 1) na.issue(1, lds + kDmaStage);
+        }
+        ob.issue(0, lds + 32768);
+        if (nk > 1) ob.issue(1, lds + kDmaStage + 32768);
+      };
+      f32x16 acc[4][kNJ];
+      gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next);
+      pre = has_next;
+      if (has_next) {
+        if (next_whole) oa.base += tile_bytes;
+        else oa.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
+      }
+      consume(acc, v0);
+    }
+    raw_barrier();
+  } else {
+    RowKLoader lb;
+    lb.base = H + (long)t0 * D;
+    lb.ld = D;
+    lb.nrows = N - t0;
+    lb.K = D;
+    for (int vt = vt_begin; vt < vt_end; ++vt) {
+      const int v0 = vt * kTile;
+      const bool full = (v0 + kTile <= V) && (t0 + kTile <= N) && (D % kBK == 0);
+      f32x16 acc[4][kNJ];
+      if constexpr (Q4) {
+        Q4RowKLoader la;
+        la.wq = Wq + (long)v0 * (D >> 3);
+        la.sc = Sc + (long)v0 * (D >> 6);
+        la.bi = Bi + (long)v0 * (D >> 6);
+        la.nrows = V - v0;
+        la.K = D;
+        if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
+      } else {
+        RowKLoader la;
+        la.base = W + (long)v0 * D;
+        la.ld = D;
+        la.nrows = V - v0;
+        la.K = D;
+        if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
+      }
+      consume(acc, v0);
     }
   }
 
@@ -758,44 +781,34 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   const bool full = (v0 + kTile <= vlim) && (t0 + kTile <= N) && (D % kBK == 0);
 
   f32x16 acc[4][kNJ];
-  if (MTP_LCE_RING && full) {
-    DmaRowK rb;
-    rb.init(H + (long)t0 * D, D);
+  if (!Q4 && D % kBK == 0) {
+    DmaRowOp oa;
+    oa.init(W + (long)v0 * D, D, vlim - v0);
+    DmaRowOp ob;
+    ob.init(H + (long)t0 * D, D, N - t0);
+    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+  } else {
+    RowKLoader lb;
+    lb.base = H + (long)t0 * D;
+    lb.ld = D;
+    lb.nrows = N - t0;
+    lb.K = D;
     if constexpr (Q4) {
-      Q4RingRowK ra;
-      ra.wq = Wq + (long)v0 * (D >> 3);
-      ra.sc = Sc + (long)v0 * (D >> 6);
-      ra.bi = Bi + (long)v0 * (D >> 6);
-      ra.K = D;
-      gemm_ring(ra, rb, D / kRBK, lds, acc);
+      Q4RowKLoader la;
+      la.wq = Wq + (long)v0 * (D >> 3);
+      la.sc = Sc + (long)v0 * (D >> 6);
+      la.bi = Bi + (long)v0 * (D >> 6);
+      la.nrows = vlim - v0;
+      la.K = D;
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     } else {
-      DmaRowK ra;
-      ra.init(W + (long)v0 * D, D);
-      gemm_ring(ra, rb, D / kRBK, lds, acc);
+      RowKLoader la;
+      la.base = W + (long)v0 * D;
+      la.ld = D;
+      la.nrows = vlim - v0;
+      la.K = D;
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     }
-  } else {
-  RowKLoader lb;
-  lb.base = H + (long)t0 * D;
-  lb.ld = D;
-  lb.nrows = N - t0;
-  lb.K = D;
-  if constexpr (Q4) {
-    Q4RowKLoader la;
-    la.wq = Wq + (long)v0 * (D >> 3);
-    la.sc = Sc + (long)v0 * (D >> 6);
-    la.bi = Bi + (long)v0 * (D >> 6);
-    la.nrows = vlim - v0;
-    la.K = D;
-    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-  } else {
-    RowKLoader la;
-    la.base = W + (long)v0 * D;
-    la.ld = D;
-    la.nrows = vlim - v0;
-    la.K = D;
-    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-  }
-
   }
   // Epilogue: stage the bf16 G tile as [token][vocab] (512 B rows, 16-byte chunks swizzled by
   // row & 31), then write it out with coalesced 16-byte stores.
@@ -848,9 +861,9 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
 template <int Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16_t* __restrict__ W,
-                       const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
-                       const bf16_t* __restrict__ Bi, int N, int D, int V, int v_begin, int v_end,
-                       float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode) {
+                       const bf16_t* __restrict__ Wt, int ldt, const uint32_t* __restrict__ Wq,
+                       const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, int N, int D, int V,
+                       int v_begin, int v_end, float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
@@ -867,48 +880,45 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const bool full = (t0 + kTile <= N) && (v_begin + kc <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
-  if (MTP_LCE_RING && full) {
-    DmaRowK ra;
-    ra.init(G + (long)t0 * ldg, ldg);
+  if (!Q4 && D % kBK == 0 && Wt != nullptr) {
+    // Transposed head [D][ldt] (columns past V are zeros): both operands are K-contiguous rows.
+    DmaRowOp oa;
+    oa.init(G + (long)t0 * ldg, ldg, N - t0);
+    DmaRowOp ob;
+    ob.init(Wt + (long)d0 * ldt + v_begin, ldt, D - d0);
+    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+  } else if (!Q4 && D % kBK == 0) {
+    // G columns past the chunk's last vocab row are zeros, so the W rows they meet only need to
+    // be readable (kvalid clamps them to the last row of W).
+    DmaRowOp oa;
+    oa.init(G + (long)t0 * ldg, ldg, N - t0);
+    DmaTransOp ob;
+    ob.init(W + (long)v_begin * D + d0, D, V - v_begin, D - d0);
+    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+  } else {
+    RowKLoader la;
+    la.base = G + (long)t0 * ldg;
+    la.ld = ldg;
+    la.nrows = N - t0;
+    la.K = kc;
     if constexpr (Q4) {
-      Q4TransRing rb;
-      rb.wq = Wq + (long)v_begin * (D >> 3);
-      rb.sc = Sc + (long)v_begin * (D >> 6);
-      rb.bi = Bi + (long)v_begin * (D >> 6);
-      rb.D = D;
-      rb.d0 = d0;
-      gemm_ring(ra, rb, kc / kRBK, lds, acc);
+      Q4TransLoader lb;
+      lb.wq = Wq + (long)v_begin * (D >> 3);
+      lb.sc = Sc + (long)v_begin * (D >> 6);
+      lb.bi = Bi + (long)v_begin * (D >> 6);
+      lb.D = D;
+      lb.d0 = d0;
+      lb.kvalid = vlim - v_begin;
+      lb.dvalid = D - d0;
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     } else {
-      TransRing rb;
-      rb.w = W + (long)v_begin * D + d0;
-      rb.ld = D;
-      gemm_ring(ra, rb, kc / kRBK, lds, acc);
+      TransLoader lb;
+      lb.w = W + (long)v_begin * D + d0;
+      lb.ld = D;
+      lb.kvalid = vlim - v_begin;
+      lb.dvalid = D - d0;
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     }
-  } else {
-  RowKLoader la;
-  la.base = G + (long)t0 * ldg;
-  la.ld = ldg;
-  la.nrows = N - t0;
-  la.K = kc;
-  if constexpr (Q4) {
-    Q4TransLoader lb;
-    lb.wq = Wq + (long)v_begin * (D >> 3);
-    lb.sc = Sc + (long)v_begin * (D >> 6);
-    lb.bi = Bi + (long)v_begin * (D >> 6);
-    lb.D = D;
-    lb.d0 = d0;
-    lb.kvalid = vlim - v_begin;
-    lb.dvalid = D - d0;
-    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-  } else {
-    TransLoader lb;
-    lb.w = W + (long)v_begin * D + d0;
-    lb.ld = D;
-    lb.kvalid = vlim - v_begin;
-    lb.dvalid = D - d0;
-    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-  }
-
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -959,17 +969,27 @@ void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __re
   const bool full = (N % kBK == 0) && (v0 + kTile <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
-  TransLoader la;
-  la.w = G + (v0 - v_begin);
-  la.ld = ldg;
-  la.kvalid = N;
-  la.dvalid = vlim - v0;
-  TransLoader lb;
-  lb.w = H + d0;
-  lb.ld = D;
-  lb.kvalid = N;
-  lb.dvalid = D - d0;
-  if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
+  if (N % kBK == 0 && D % kBK == 0) {
+    // The vocab tile lies inside the chunk buffer (ctiles * 256 <= ldg), so all 256 G columns
+    // are readable; rows past the chunk's end are not stored below.
+    DmaTransOp oa;
+    oa.init(G + (v0 - v_begin), ldg, N, kTile);
+    DmaTransOp ob;
+    ob.init(H + d0, D, N, D - d0);
+    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+  } else {
+    TransLoader la;
+    la.w = G + (v0 - v_begin);
+    la.ld = ldg;
+    la.kvalid = N;
+    la.dvalid = vlim - v0;
+    TransLoader lb;
+    lb.w = H + d0;
+    lb.ld = D;
+    lb.kvalid = N;
+    lb.dvalid = D - d0;
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
+  }
 
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -983,6 +1003,53 @@ void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __re
         if (d < D) dW[(long)v * D + d] = __builtin_bit_cast(bf16_t, (__bf16)acc[i][j][r]);
       }
     }
+}
+
+// ------------------------------------------------------------------------------------------
+// Transposed dense head for the dH product: Wt[d][v] = W[v][d] for v < V, zeros for
+// V <= v < ldt (ldt = lce_head_t_ld(V)). 64 x 64 tiles through LDS; 16-byte loads and stores.
+// ------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* __restrict__ W, int V, int D, int ldt,
+                                                                 bf16_t* __restrict__ Wt) {
+  __shared__ uint16_t tile[64][64 + 2];
+  const int v0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int id = t + 256 * p;
+    const int r = id >> 3, c = id & 7;
+    const int v = v0 + r, d = d0 + 8 * c;
+    u32x4 x = zero4();
+    if (v < V && d < D) x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      tile[r][8 * c + 2 * e] = (uint16_t)(x[e] & 0xffffu);
+      tile[r][8 * c + 2 * e + 1] = (uint16_t)(x[e] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int p = 0; p < 2; ++p) {
+    const int id = t + 256 * p;
+    const int r = id >> 3, c = id & 7;
+    const int d = d0 + r, v = v0 + 8 * c;
+    if (d < D) {
+      u32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        y[e] = (uint32_t)tile[8 * c + 2 * e][r] | ((uint32_t)tile[8 * c + 2 * e + 1][r] << 16);
+      *reinterpret_cast<u32x4*>(Wt + (long)d * ldt + v) = y;
+    }
+  }
+}
+
+long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad; }
+
+hipError_t launch_lce_head_transpose(const bf16_t* W, int V, int D, bf16_t* Wt, hipStream_t stream) {
+  const int ldt = (int)lce_head_t_ld(V);
+  dim3 grid(ldt / 64, (D + 63) / 64), block(256);
+  hipLaunchKernelGGL(lce_head_transpose_kernel, grid, block, 0, stream, W, V, D, ldt, Wt);
+  return hipGetLastError();
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1030,6 +1097,8 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   const int nchunks = (V + chunk - 1) / chunk;
+  const int ldg = chunk + kGPitchPad;
+  const int ldt = (int)lce_head_t_ld(V);
   dim3 block(kThreads);
   for (int c = 0; c < nchunks; ++c) {
     const int vb = c * chunk;
@@ -1038,10 +1107,10 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
     if (h.q4) {
       hipLaunchKernelGGL(lce_bwd_g_kernel<1>, ggrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll,
-                         ignore_index, N, D, V, vb, ve, ctiles, chunk, Gbuf);
+                         ignore_index, N, D, V, vb, ve, ctiles, ldg, Gbuf);
     } else {
       hipLaunchKernelGGL(lce_bwd_g_kernel<0>, ggrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll,
-                         ignore_index, N, D, V, vb, ve, ctiles, chunk, Gbuf);
+                         ignore_index, N, D, V, vb, ve, ctiles, ldg, Gbuf);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1052,17 +1121,17 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     else mode = 1;
     dim3 hgrid(8 * rtiles * ((dtiles + 7) / 8));
     if (h.q4) {
-      hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, chunk, ctiles * kTile, h.w, h.wq, h.sc,
-                         h.bi, N, D, V, vb, ve, acc32, dH, mode);
+      hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
+                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode);
     } else {
-      hipLaunchKernelGGL(lce_bwd_dh_kernel<0>, hgrid, block, 0, stream, Gbuf, chunk, ctiles * kTile, h.w, h.wq, h.sc,
-                         h.bi, N, D, V, vb, ve, acc32, dH, mode);
+      hipLaunchKernelGGL(lce_bwd_dh_kernel<0>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
+                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (dW != nullptr && !h.q4) {
       dim3 wgrid(8 * ctiles * ((dtiles + 7) / 8));
-      hipLaunchKernelGGL(lce_bwd_dw_kernel, wgrid, block, 0, stream, Gbuf, chunk, H, N, D, V, vb, ve, ctiles, dW);
+      hipLaunchKernelGGL(lce_bwd_dw_kernel, wgrid, block, 0, stream, Gbuf, ldg, H, N, D, V, vb, ve, ctiles, dW);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }

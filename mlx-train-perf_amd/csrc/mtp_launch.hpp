@@ -11,15 +11,24 @@ typedef uint16_t bf16_t;
 // shape so that results do not depend on the device a call lands on.
 constexpr int kNumCU = 256;
 
+// Row pitch of the backward's bf16 gradient-tile buffer is chunk + kGPitchPad elements: a pitch
+// that is a multiple of a large power of two (chunk is a multiple of 256) makes the 256 rows of
+// one operand tile fall on the same memory channels.
+constexpr int kGPitchPad = 64;
+
 struct LceHead {
   int q4;                 // 0: dense bf16 [V][D]; 1: 4-bit affine, group size 64
   const bf16_t* w;        // dense weight
+  const bf16_t* wt;       // optional transposed dense weight [D][lce_head_t_ld(V)] (or null)
   const uint32_t* wq;     // packed nibbles [V][D/8]
   const bf16_t* sc;       // scales [V][D/64]
   const bf16_t* bi;       // biases [V][D/64]
 };
 
 int lce_fwd_nsplit(long N, long V);
+long lce_head_t_ld(long V);
+
+hipError_t launch_lce_head_transpose(const bf16_t* W, int V, int D, bf16_t* Wt, hipStream_t stream);
 
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,

@@ -15,6 +15,8 @@ MI355X specifics:
 """
 from __future__ import annotations
 
+import os
+import weakref
 from dataclasses import dataclass
 from typing import Literal
 
@@ -206,13 +208,43 @@ def _chunked_nll(hidden2, head, targets2, ignore_index, chunk_size):
 
 VJP_CALLS: dict[str, int] = {}
 
+# Transposed copies of dense heads for the backward's dH product (mtp_lce_head_transpose), one per
+# device: (owner weakref, data_ptr, shape, version) -> bf16 [D][mtp_lce_head_t_ld(V)]. The owner is
+# the caller's weight tensor; an in-place update through it bumps its version and invalidates the
+# entry. A frozen head is therefore transposed once; a trainable one after every optimizer step.
+_HEAD_T_CACHE: dict[int, tuple[tuple, torch.Tensor]] = {}
+
+
+def clear_transposed_head_cache() -> None:
+    """Drop the cached transposed heads (e.g. after changing a head through `.data`, which does not
+    bump the tensor's version counter)."""
+    _HEAD_T_CACHE.clear()
+
+
+def _transposed_head(owner: torch.Tensor | None, w: torch.Tensor) -> torch.Tensor | None:
+    if owner is None or os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "1") == "0" or w.shape[1] % 64 != 0:
+        return None
+    dev = w.device.index if w.device.index is not None else torch.cuda.current_device()
+    key = (w.data_ptr(), tuple(w.shape), owner._version)
+    ent = _HEAD_T_CACHE.get(dev)
+    if ent is not None and ent[0][0]() is owner and ent[0][1:] == key:
+        return ent[1]
+    _HEAD_T_CACHE.pop(dev, None)
+    lib = _native.load()
+    v, d = w.shape
+    wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=w.device)
+    rc = lib.mtp_lce_head_transpose(w.data_ptr(), v, d, wt.data_ptr(), _native.stream_of(w))
+    _native.check(rc, domain="loss")
+    _HEAD_T_CACHE[dev] = ((weakref.ref(owner),) + key, wt)
+    return wt
+
 
 class _KernelLCE(torch.autograd.Function):
     """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only; it also
     returns dL/dW when the dense head is an input that requires grad (trainable head)."""
 
     @staticmethod
-    def forward(ctx, hidden2, targets2, w, w_q, scales, biases, head_kind, ignore_index, bwd_chunk):
+    def forward(ctx, hidden2, targets2, w, w_q, scales, biases, head_kind, ignore_index, bwd_chunk, owner=None):
         lib = _native.load()
         n, d = hidden2.shape
         v = w.shape[0] if head_kind == _native.HEAD_DENSE else w_q.shape[0]
@@ -231,6 +263,7 @@ class _KernelLCE(torch.autograd.Function):
         ctx.head = (w, w_q, scales, biases, head_kind, v)
         ctx.ignore_index = ignore_index
         ctx.bwd_chunk = bwd_chunk
+        ctx.owner = owner
         ctx.mark_non_differentiable(lse, tgt)
         return nll, lse, tgt
 
@@ -247,13 +280,14 @@ class _KernelLCE(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
         d_hidden = torch.empty_like(hidden2)
         d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
+        w_t = _transposed_head(ctx.owner, w) if head_kind == _native.HEAD_DENSE else None
         ct = d_nll.to(torch.float32).contiguous()
-        rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
-                             _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ctx.ignore_index,
-                             lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(), _native.ptr(d_w), chunk,
-                             ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
+        rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),
+                             _native.ptr(scales), _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind,
+                             ctx.ignore_index, lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(),
+                             _native.ptr(d_w), chunk, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
-        return d_hidden, None, d_w, None, None, None, None, None, None
+        return d_hidden, None, d_w, None, None, None, None, None, None, None
 
 
 def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor, *, ignore_index: int = -100,
@@ -266,9 +300,9 @@ def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.T
         w = head.weight if head.trainable else head.weight.detach()
         if not w.is_contiguous():
             raise UnsupportedHeadError("kernel impl needs a contiguous (V, D) head weight")
-        args = (w, None, None, None, _native.HEAD_DENSE)
-    else:
-        args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
+        return _KernelLCE.apply(h, t, w, None, None, None, _native.HEAD_DENSE, int(ignore_index), int(bwd_chunk or 0),
+                                head.weight)
+    args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
     return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0))
 
 

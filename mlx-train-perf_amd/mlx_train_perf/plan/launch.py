@@ -19,6 +19,11 @@ ATTN_TILE = 64      # attention key/query tile
 DEFAULT_LCE_BWD_BUDGET = 1 << 30  # bytes of backward workspace (bf16 gradient chunk + fp32 dH)
 
 
+# Gradient-tile rows are chunk + 64 elements apart: a pitch that is a multiple of a large power of
+# two puts the rows of one operand tile on the same memory channels (csrc/mtp_launch.hpp).
+G_PITCH_PAD = 64
+
+
 def lce_bwd_budget_bytes() -> int:
     return int(os.environ.get("MTP_LCE_BWD_BUDGET", DEFAULT_LCE_BWD_BUDGET))
 
@@ -47,18 +52,20 @@ def lce_fwd_workspace_bytes(n: int, v: int) -> int:
 
 
 def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
+    """Vocab columns per backward chunk (multiple of 256) for a workspace budget in bytes."""
     vpad = -(-v // TILE) * TILE
-    if n * vpad * 2 <= budget:
+    if n * (vpad + G_PITCH_PAD) * 2 <= budget:
         return vpad
     acc = n * d * 4
     rest = max(budget - acc, 0)
-    c = (rest // (n * 2)) // TILE * TILE
+    c = (rest // (n * 2) - G_PITCH_PAD) // TILE * TILE
     return min(max(c, TILE), vpad)
 
 
 def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int) -> int:
+    """bf16 gradient tiles [n][chunk + G_PITCH_PAD] plus the fp32 dH accumulator when >1 chunk."""
     nchunks = -(-v // chunk)
-    return n * chunk * 2 + (n * d * 4 if nchunks > 1 else 0)
+    return n * (chunk + G_PITCH_PAD) * 2 + (n * d * 4 if nchunks > 1 else 0)
 
 
 @dataclass(frozen=True)

@@ -66,12 +66,17 @@ def test_lce_refusals():
     assert _lce_fwd(ws_bytes=8) == _native.MTP_ERR_WORKSPACE
     assert "workspace" in _native.last_error()
     lib = _native.load()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100, FAKE, 1 << 20, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_INPUT and "multiple of 256" in _native.last_error()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 16, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 16, None)
     assert rc == _native.MTP_ERR_WORKSPACE
-    rc = lib.mtp_lce_bwd(FAKE, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 1 << 20, None)
+    rc = lib.mtp_lce_bwd(FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_UNSUPPORTED and "frozen" in _native.last_error()
+    rc = lib.mtp_lce_bwd(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 1 << 20, None)
+    assert rc == _native.MTP_ERR_INPUT and "w_t" in _native.last_error()
+    assert lib.mtp_lce_head_t_ld(151936) == 152064 + 64 and lib.mtp_lce_head_t_ld(1) == 256 + 64
+    assert lib.mtp_lce_head_transpose(FAKE, 100, 36, FAKE, None) == _native.MTP_ERR_UNSUPPORTED
+    assert lib.mtp_lce_head_transpose(None, 100, 64, FAKE, None) == _native.MTP_ERR_INPUT
 
 
 def test_attention_refusals():

@@ -148,3 +148,50 @@ def test_trainable_head_dw_parity(n, d, v, chunk):
     odw = olce.backward_dw(h, w, t, olse, ct, ignore_index=IGN)
     assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
     assert rel_l2(wd.grad.cpu(), odw) <= 1e-2
+
+
+@pytest.mark.parametrize(("v", "d"), [(1027, 192), (300, 64), (5000, 512)])
+def test_head_transpose_exact(v, d):
+    """mtp_lce_head_transpose: w_t[:, :v] == w.T bitwise, zero padding up to the row pitch."""
+    from mlx_train_perf import _native
+
+    print(f"[lce head transpose] v={v} d={d}", flush=True)
+    lib = _native.load()
+    w = torch.randn(v, d, generator=torch.Generator().manual_seed(v)).to(torch.bfloat16).cuda()
+    ld = lib.mtp_lce_head_t_ld(v)
+    wt = torch.full((d, ld), 7.0, dtype=torch.bfloat16, device="cuda")
+    _native.check(lib.mtp_lce_head_transpose(w.data_ptr(), v, d, wt.data_ptr(), None), domain="loss")
+    torch.cuda.synchronize()
+    assert torch.equal(wt[:, :v].cpu(), w.cpu().T)
+    assert not wt[:, v:].any()
+
+
+def test_transposed_head_cache_follows_in_place_updates(monkeypatch):
+    """The cached transposed head is rebuilt after an in-place update of the weight, and the
+    transposed-read path (cache disabled) gives the same dH."""
+    from mlx_train_perf.core import loss as L
+
+    print("[lce transposed-head cache]", flush=True)
+    n, d, v = 300, 256, 3000
+    h, w, t = lce_inputs(n, d, v, seed=77)
+    ct = _cotangent(t)
+    wd = w.cuda()
+    grads = []
+    for scale in (1.0, -0.5):
+        if scale != 1.0:
+            wd.mul_(scale)   # bumps the version counter: the cache entry must be replaced
+        hd = h.cuda().requires_grad_(True)
+        nll, _, _ = L.kernel_forward_parts(hd, L.DenseHead(weight=wd, trainable=False), t.cuda(), ignore_index=IGN,
+                                           bwd_chunk=1024)
+        nll.backward(ct.cuda())
+        wc = wd.cpu()
+        _, olse, _ = olce.forward(h, wc, t, ignore_index=IGN)
+        odh = olce.backward(h, wc, t, olse, ct, ignore_index=IGN, dtype=torch.float64)
+        assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+        grads.append(hd.grad.clone())
+    monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", "0")
+    hd = h.cuda().requires_grad_(True)
+    nll, _, _ = L.kernel_forward_parts(hd, L.DenseHead(weight=wd, trainable=False), t.cuda(), ignore_index=IGN,
+                                       bwd_chunk=1024)
+    nll.backward(ct.cuda())
+    assert rel_l2(hd.grad.float(), grads[1].float()) <= 2e-3

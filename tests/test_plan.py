@@ -48,8 +48,9 @@ def test_backward_chunk_fits_budget_when_possible(budget):
     assert c % 256 == 0
     if c > 256:
         assert ws <= budget
-    if budget >= n * (-(-v // 256) * 256) * 2:
-        assert -(-v // c) == 1 and ws == n * c * 2
+    if budget >= n * (-(-v // 256) * 256 + plan.G_PITCH_PAD) * 2:
+        # one chunk: only the bf16 gradient tiles (row pitch padded by 64 elements), no fp32 dH
+        assert -(-v // c) == 1 and ws == n * (c + 64) * 2
 
 
 def test_attention_plan():
