@@ -1055,10 +1055,14 @@ hipError_t launch_lce_head_transpose(const bf16_t* W, int V, int D, bf16_t* Wt, 
 // ------------------------------------------------------------------------------------------
 // Host-side launchers (called from the C-ABI after validation).
 // ------------------------------------------------------------------------------------------
+// Forward workgroups per CU (they run back to back; two per CU shortens the tail of the last
+// round and measured ~2% faster than one at the flagship shape).
+constexpr long kFwdWaves = 2;
+
 int lce_fwd_nsplit(long N, long V) {
   const long rtiles = (N + kTile - 1) / kTile;
   const long vtiles = (V + kTile - 1) / kTile;
-  long ns = (kNumCU + rtiles - 1) / rtiles;  // aim for >= one workgroup per CU
+  long ns = (kFwdWaves * kNumCU + rtiles - 1) / rtiles;  // aim for kFwdWaves workgroups per CU
   if (ns >= 8) ns = (ns + 7) / 8 * 8;        // one vocab split per XCD residue
   if (ns > vtiles) ns = vtiles;
   if (ns < 1) ns = 1;

@@ -38,10 +38,15 @@ def packed_pairs(lengths: list[int]) -> int:
     return sum(causal_pairs(n) for n in lengths)
 
 
+FWD_WGS_PER_CU = 2  # forward workgroups per CU (run back to back; csrc/lce_kernels.hip)
+
+
 def lce_fwd_splits(n: int, v: int) -> int:
+    """Vocab splits of the forward: about FWD_WGS_PER_CU workgroups per CU, a multiple of 8 (one
+    split per XCD residue) when >= 8, never more than the vocab tiles."""
     rtiles = -(-n // TILE)
     vtiles = -(-v // TILE)
-    ns = -(-NUM_CU // rtiles)
+    ns = -(-(FWD_WGS_PER_CU * NUM_CU) // rtiles)
     if ns >= 8:
         ns = -(-ns // 8) * 8
     return max(1, min(ns, vtiles))
