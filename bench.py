@@ -116,6 +116,38 @@ def bench_lce(steps, warmup, head_kind="dense"):
 
     sec = time_region(step, steps, warmup)
 
+    # Roofline kernel: the forward launch (lce_fwd_kernel + its finalize) through the C-ABI, timed with
+    # events on the stream it is launched on.
+    from mlx_train_perf import _native
+
+    lib = _native.load()
+    stream = torch.cuda.current_stream()
+    n_, d_, v_ = h.shape[0], h.shape[1], V
+    outs = [torch.empty(n_, dtype=torch.float32, device="cuda") for _ in range(3)]
+    kind = _native.HEAD_DENSE if head_kind == "dense" else _native.HEAD_Q4
+    ws_b = lib.mtp_lce_fwd_workspace_bytes(n_, d_, v_, kind)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    hw = h.contiguous()
+    tt = t.contiguous()
+    args = ((head.weight.data_ptr(), None, None, None) if head_kind == "dense" else
+            (None, head.w_q.data_ptr(), head.scales.data_ptr(), head.biases.data_ptr()))
+
+    def fwd_launch():
+        rc = lib.mtp_lce_fwd(hw.data_ptr(), *args, tt.data_ptr(), n_, d_, v_, kind, IGNORE, outs[0].data_ptr(),
+                             outs[1].data_ptr(), outs[2].data_ptr(), ws.data_ptr(), ws_b, stream.cuda_stream)
+        _native.check(rc, domain="loss")
+
+    fwd_launch()
+    kev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        kev[i][0].record(stream)
+        fwd_launch()
+        kev[i][1].record(stream)
+    torch.cuda.synchronize()
+    fwd_kernel_ms = sum(e[0].elapsed_time(e[1]) for e in kev) / steps
+    del ws
+
     # Live per-phase durations with events on the launch stream: [fwd][bwd] per step.
     stream = torch.cuda.current_stream()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
@@ -142,8 +174,12 @@ def bench_lce(steps, warmup, head_kind="dense"):
     fwd_peak = torch.cuda.max_memory_allocated() - before
     del nll
     p = plan.lce_plan(n=N, v=V, d=D)
-    return {"sec_per_step": sec, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_marginal_peak_gb": fwd_peak / 1e9,
-            "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks}
+    from mlx_train_perf.core import loss as _loss
+
+    head_t = sum(e[1].numel() * e[1].element_size() for e in _loss._HEAD_T_CACHE.values())
+    return {"sec_per_step": sec, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_kernel_ms": fwd_kernel_ms,
+            "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9,
+            "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks, "transposed_head_cache_gb": head_t / 1e9}
 
 
 def bench_attention(steps, warmup, packed=False):
@@ -200,7 +236,129 @@ def bench_attention(steps, warmup, packed=False):
     return out
 
 
-def cpu_baseline(budget_s: float = 20.0):
+# ------------------------------------------------------------------------------------------------
+# HBM traffic of the roofline kernel (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated against a
+# 1 GiB device copy). `--pmc-workload` is the program those passes profile; `--pmc-summary` turns
+# the two passes' csv output into the markdown committed under profiles/, whose json block
+# committed_traffic() reads back.
+# ------------------------------------------------------------------------------------------------
+PMC_COPY_BYTES = 1 << 30
+TRAFFIC_PROFILE = ROOT / "profiles" / "lce_attention_hbm_traffic_pmc.md"
+
+
+def committed_traffic(kernel: str):
+    try:
+        text = TRAFFIC_PROFILE.read_text()
+        blob = text.split("```json", 1)[1].split("```", 1)[0]
+        return json.loads(blob)["kernels"][kernel]["traffic_bytes"]
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
+
+
+def pmc_workload():
+    """One pass of each profiled workload (no timing): a 1 GiB device copy (the calibration),
+    the flagship LCE forward + backward, and causal attention forward + backward at S=8192."""
+    import torch
+
+    from mlx_train_perf.attention.api import kernel_backward, kernel_forward
+    from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
+
+    x = torch.empty(PMC_COPY_BYTES // 2, dtype=torch.int16, device="cuda").fill_(1)
+    y = torch.empty_like(x)
+    for _ in range(2):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    del x, y
+    h, w, t = lce_inputs_gpu(N, D, V)
+    hd = h.requires_grad_(True)
+    for _ in range(2):
+        nll, _, _ = kernel_forward_parts(hd, DenseHead(weight=w, trainable=False), t, ignore_index=IGNORE)
+        nll.backward(torch.ones_like(nll))
+    torch.cuda.synchronize()
+    del h, w, t, hd
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(1, 32, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
+    k = torch.randn(1, 8, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
+    v = torch.randn(1, 8, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
+    do = torch.randn_like(q)
+    for _ in range(2):
+        o, l = kernel_forward(q, k, v, scale=1 / math.sqrt(128))
+        kernel_backward(q, k, v, o, l, do, scale=1 / math.sqrt(128))
+    torch.cuda.synchronize()
+    print("pmc workload done", flush=True)
+
+
+def _pmc_means(root: str) -> dict:
+    """Per kernel, the mean over dispatches of each counter (summed over its dimension rows)."""
+    import collections
+    import csv
+    import glob
+    import re
+
+    acc = collections.defaultdict(lambda: collections.defaultdict(lambda: collections.defaultdict(float)))
+    for f in glob.glob(f"{root}/**/*counter_collection.csv", recursive=True):
+        with open(f) as fh:
+            for row in csv.DictReader(fh):
+                name = re.sub(r"\(.*", "", row["Kernel_Name"]).replace("void ", "").strip()
+                acc[name][row["Counter_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
+    return {k: {c: (sum(d.values()) / len(d), max(d.values()), len(d)) for c, d in cs.items()} for k, cs in acc.items()}
+
+
+def pmc_summary(fetch_dir: str, write_dir: str, command: str) -> str:
+    fetch, write = _pmc_means(fetch_dir), _pmc_means(write_dir)
+    copy = [k for k in fetch if "copyBuffer" in k or "copy" in k.lower()]
+    # calibration: the largest copy dispatch (the 1 GiB copy) in each pass, counters in KiB
+    cf = max(fetch[k]["FETCH_SIZE"][1] for k in copy if "FETCH_SIZE" in fetch[k])
+    cw = max(write[k]["WRITE_SIZE"][1] for k in copy if k in write and "WRITE_SIZE" in write[k])
+    f_fetch, f_write = PMC_COPY_BYTES / (cf * 1024.0), PMC_COPY_BYTES / (cw * 1024.0)
+    algorithmic = {  # bytes that must cross HBM at least once per launch
+        "lce_fwd_kernel<0>": 2.0 * (V * D + N * D),
+        "attn_fwd_kernel<128, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
+    }
+    kernels = {}
+    for k in sorted(fetch):
+        if not k.startswith("mtp::") or "FETCH_SIZE" not in fetch[k]:
+            continue
+        short = k[len("mtp::"):]
+        fb = fetch[k]["FETCH_SIZE"][0] * 1024.0 * f_fetch
+        wb = write.get(k, {}).get("WRITE_SIZE", (0.0,))[0] * 1024.0 * f_write
+        kernels[short] = {"fetch_bytes": fb, "write_bytes": wb, "traffic_bytes": fb + wb,
+                          "dispatches": fetch[k]["FETCH_SIZE"][2]}
+        if short in algorithmic:
+            kernels[short]["algorithmic_bytes"] = algorithmic[short]
+    lines = ["# HBM traffic per launch: LCE (N=8192 D=4096 V=151936) and causal attention (S=8192)", "",
+             "Commands (repository root on the GPU box; one rocprofv3 pass per counter):", "", "```", command, "```", "",
+             f"Calibration: a {PMC_COPY_BYTES} B device copy read FETCH_SIZE={cf:.0f} KiB and WRITE_SIZE={cw:.0f} KiB "
+             f"per dispatch, so bytes = KiB x 1024 x {f_fetch:.4f} (fetch) and x {f_write:.4f} (write).", "",
+             "| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB |", "|---|---:|---:|---:|---:|---:|"]
+    for k, r in kernels.items():
+        alg = r.get("algorithmic_bytes")
+        lines.append(f"| `{k}` | {r['dispatches']} | {r['fetch_bytes'] / 1e9:.3f} | {r['write_bytes'] / 1e9:.3f} | "
+                     f"{r['traffic_bytes'] / 1e9:.3f} | {'' if alg is None else f'{alg / 1e9:.3f}'} |")
+    blob = {"calibration": {"copy_bytes": PMC_COPY_BYTES, "fetch_kib": cf, "write_kib": cw,
+                            "fetch_factor": f_fetch, "write_factor": f_write}, "kernels": kernels}
+    lines += ["", "```json", json.dumps(blob, indent=1), "```", ""]
+    return "\n".join(lines)
+
+
+def trace_summary(stats_csv: str, title: str, command: str) -> str:
+    """Markdown table of this library's kernels from a rocprofv3 --kernel-trace --stats csv."""
+    import csv
+    import re
+
+    rows = [r for r in csv.DictReader(open(stats_csv)) if "mtp::" in r["Name"]]
+    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    out = [f"# {title}", "", "Command (repository root on the GPU box):", "", "```", command, "```", "",
+           "Per-kernel durations from `rocprofv3 --kernel-trace --stats` (kernel_stats.csv), microseconds.", "",
+           "| kernel | calls | avg us | min us | max us | total us |", "|---|---:|---:|---:|---:|---:|"]
+    for r in rows:
+        name = re.sub(r"\(.*", "", r["Name"]).replace("void ", "").strip()
+        out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+                   f"{float(r['MaxNs']) / 1e3:.1f} | {float(r['TotalDurationNs']) / 1e3:.1f} |")
+    return "\n".join(out) + "\n"
+
+
+def cpu_baseline(budget_s: float = 15.0):
     """The oracle (PyTorch-CPU fp32 restatement of the reference's naive path) on a bounded sample
     of the same workload: `rows` tokens of the flagship LCE fwd+bwd (full D, V)."""
     import torch
@@ -222,10 +380,10 @@ def cpu_baseline(budget_s: float = 20.0):
         return time.perf_counter() - t0
 
     run(8)  # warm-up outside the window
-    rows = 16
+    rows = 32
     dt = run(rows)
-    # scale the sample toward the budget (linear in rows), capped
-    rows = int(max(16, min(1024, rows * budget_s / max(dt, 1e-3) * 0.5)))
+    # scale the sample toward the budget (the work is linear in rows), capped
+    rows = int(max(32, min(4096, rows * budget_s / max(dt, 1e-3))))
     dt = run(rows)
     return {"value": rows / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"LCE fwd+bwd on {rows} of the {N} tokens (D={D}, V={V}), oracle/lce.py fp32, "
@@ -239,9 +397,20 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--pmc-workload", action="store_true", help="run the profiled workloads once (no timing)")
+    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "COMMAND"),
+                    help="summarize two rocprofv3 --pmc csv outputs into markdown")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("STATS_CSV", "TITLE", "COMMAND"),
+                    help="summarize a rocprofv3 --kernel-trace --stats csv into markdown")
     ap.add_argument("--parts", default="lce,qlora,attention",
                     help="comma list of lce, qlora, attention (lce is the headline line)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary))
+        return
+    if args.trace_summary:
+        print(trace_summary(*args.trace_summary), end="")
+        return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build runs on one GPU; "
               "see DESIGN.md for how the path would shard)", file=sys.stderr)
@@ -251,12 +420,15 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
+    if args.pmc_workload:
+        pmc_workload()
+        return
 
     lce = bench_lce(args.steps, args.warmup, "dense")
     sec = lce["sec_per_step"]
     flops_step = 6.0 * N * V * D
     fwd_flops = 2.0 * N * V * D
-    ach = fwd_flops / (lce["fwd_ms"] * 1e-3) / 1e12
+    ach = fwd_flops / (lce["fwd_kernel_ms"] * 1e-3) / 1e12
     result = {
         "metric": "fused-LCE fwd+bwd tokens/s @N8192 V151936 D4096 (bf16, frozen head)",
         "value": N / sec,
@@ -274,7 +446,7 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "kernel": "lce_fwd_kernel<0> (+ lce_fwd_finalize_kernel in the event window)",
                      "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
-                     "traffic": None},
+                     "traffic": committed_traffic("lce_fwd_kernel<0>")},
         "step_mfma_frac": flops_step / sec / 1e12 / PEAK_BF16_TFLOPS,
         "lce": {**lce, "step_tflops": flops_step / sec / 1e12},
     }
