@@ -27,6 +27,9 @@
 
 namespace mtp {
 
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 
 // The dQ kernel stages one K/V tile in LDS (51 KiB at head_dim 128) and prefetches the next into
@@ -708,6 +711,532 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------
+// Backward dK, dV for head_dim 128, DMA-fed. Same ownership and math as attn_bwd_dkv_kernel; the
+// 64-query Q and dO tiles are copied global -> LDS by buffer_load ... lds (16 bytes per lane, rows
+// past S read as zeros) into 256 B rows whose 16-byte chunks are XOR-swizzled by
+// sw(r) = 2 (r & 7) + ((r >> 3) & 1). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128;
+// the transposed operands of dV += dO^T P and dK += Q^T dS are ds_read_b64_tr_b16 of the same
+// tiles. The two reads of a transposed fragment start at query rows 4 hf and 4 hf + 8 of each
+// 16-row slab, which is the order of the probability / dS registers (MFMA accumulator rows), so
+// no permuted copy of the tiles is kept. Waits and the barrier are explicit: one barrier per
+// tile, the copies of the next tile stay in flight during the current one.
+// ------------------------------------------------------------------------------------------
+namespace dkv128 {
+constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
+constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
+constexpr int kScal = 3 * 256;             // lse*log2e, D, segment id of the 64 queries
+constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
+__device__ __forceinline__ int sw(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+}  // namespace dkv128
+
+template <bool PACKED>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                            const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
+                            const float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
+                            const int32_t* __restrict__ seg_start, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv,
+                            int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
+  using namespace dkv128;
+  constexpr int DH = 128;
+  constexpr int kDK = DH / 16, kDB = DH / 32;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+
+  const int G = Hq / Hkv;
+  const int nkv = B * Hkv;
+  const int g = blockIdx.x;
+  const int kvi = g % nkv;
+  const int ktile = g / nkv;  // earliest keys (most work under the causal mask) first
+  const int bidx = kvi / Hkv;
+  const int kvh = kvi % Hkv;
+  const int k0 = ktile * 128;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int kw0 = k0 + 32 * w;
+  const int kj = kw0 + col;
+  const bool kvalid = kj < S;
+  const bool wave_has = kw0 < S;
+
+  const long krow = (long)(bidx * Hkv + kvh) * S;
+  const bf16_t* kh = k + krow * DH;
+  const bf16_t* vh = v + krow * DH;
+  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  bf16x8 kf[kDK], vf[kDK];
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks) {
+    kf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(kh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+    vf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(vh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+  }
+  const int my_seg = (PACKED && kvalid) ? sid[kj] : -3;
+
+  const int q_begin = (k0 / kKT) * kKT;
+  int q_end = S;
+  if (PACKED) {
+    const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
+    q_end = upper_bound_i32(sst, S, klast);
+  }
+  const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
+  const int niter = G * ntq;
+
+  f32x16 dka[kDB], dva[kDB];
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      dka[db][r] = 0.f;
+      dva[db][r] = 0.f;
+    }
+
+  // Copy lanes: wave w issues 4 x 1 KiB per tile and operand (rows 4 (4 j + w) .. +3).
+  uint32_t coff[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int row = 4 * (4 * j + w) + (lane >> 4);
+    coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+  }
+  // Row-fragment lane offsets (per k16 step ks): row = 32 qb + col, chunk 2 ks + hf.
+  const int sw_r = sw(col & 15);
+  // Transposed-fragment lane offsets: read t covers rows 4 hf + 8 t + (s >> 2) of a 16-row slab,
+  // columns 32 db + 16 (g & 1) + 4 (s & 3) (g = lane >> 4, s = lane & 15).
+  int tro[2][kDB];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
+    const int swt = sw(rl);
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const int c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      tro[t][db] = rl * kRowB + ((c ^ swt) << 4) + 8 * (lane & 1);
+    }
+  }
+
+  auto issue = [&](int it, char* st) {
+    const int hh = it / ntq, tq = it % ntq;
+    const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
+    const int q0 = q_begin + tq * kKT;
+    const long rows_left = (long)(S - q0);
+    const char* qb_ = reinterpret_cast<const char*>(q + (qrow + q0) * DH);
+    const char* db_ = reinterpret_cast<const char*>(d_o + (qrow + q0) * DH);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, (int)(rows_left * kRowB), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, (int)(rows_left * kRowB), 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(st + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)(st + kTile + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
+    }
+  };
+  float l2_reg = 0.f, d_reg = 0.f;
+  int seg_reg = 0;
+  auto load_scal = [&](int it) {
+    if (tid < kKT) {
+      const int hh = it / ntq, tq = it % ntq;
+      const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
+      const int qq = q_begin + tq * kKT + tid;
+      const bool ok = qq < S;
+      l2_reg = ok ? lse[qrow + qq] * kLog2e : 0.f;
+      d_reg = ok ? dvec[qrow + qq] : 0.f;
+      if (PACKED) seg_reg = ok ? sid[qq] : -1;
+    }
+  };
+  auto store_scal = [&](char* st) {
+    if (tid < kKT) {
+      float* sc = reinterpret_cast<float*>(st + 2 * kTile);
+      sc[tid] = l2_reg;
+      sc[64 + tid] = d_reg;
+      reinterpret_cast<int*>(sc + 128)[tid] = seg_reg;
+    }
+  };
+
+  if (niter > 0) {
+    issue(0, lds);
+    load_scal(0);
+    store_scal(lds);  // waits for its own loads
+    if (niter > 1) {
+      issue(1, lds + kStage);
+      load_scal(1);
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (niter > 1) store_scal(lds + kStage);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+
+  for (int it = 0; it < niter; ++it) {
+    char* cur = lds + (it & 1) * kStage;
+    const int q0 = q_begin + (it % ntq) * kKT;
+    const bool more2 = it + 2 < niter;
+    if (more2) load_scal(it + 2);
+    bool skip = !wave_has || (q0 + kKT - 1 < kw0);
+    int sst_last = 0;
+    if (PACKED && !skip) {
+      skip = sst[q0] > kw0 + 31;
+      sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
+    }
+    if (!skip) {
+      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
+      const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
+      const float* ds_ = l2s + 64;
+      const int* segs = reinterpret_cast<const int*>(l2s + 128);
+      const char* qt = cur;
+      const char* dt = cur + kTile;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        f32x16 sacc, pacc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          sacc[r] = 0.f;
+          pacc[r] = 0.f;
+        }
+        const int rb = (32 * qb + col) * kRowB;
+#pragma unroll
+        for (int ks = 0; ks < kDK; ++ks) {
+          const int o = rb + (((2 * ks + hf) ^ sw_r) << 4);
+          sacc = mfma32(as_bf16x8(lds_read16(qt, o)), kf[ks], sacc);
+          pacc = mfma32(as_bf16x8(lds_read16(dt, o)), vf[ks], pacc);
+        }
+        bf16x8 pf[2], sf[2];
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * rq + u;
+            float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
+            if (need_mask) {
+              const int qq = q0 + ql0 + u;
+              bool ok = (kj <= qq) && (qq < S) && kvalid;
+              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
+              if (!ok) p = 0.f;
+            }
+            pf[r >> 3][r & 7] = (__bf16)p;
+            sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[u]));
+          }
+        }
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          const int slab = (32 * qb + 16 * kk) * kRowB;
+#pragma unroll
+          for (int db = 0; db < kDB; ++db) {
+            const lds_bf16x4* pd0 = (const lds_bf16x4*)(dt + slab + tro[0][db]);
+            const lds_bf16x4* pd1 = (const lds_bf16x4*)(dt + slab + tro[1][db]);
+            const lds_bf16x4* pq0 = (const lds_bf16x4*)(qt + slab + tro[0][db]);
+            const lds_bf16x4* pq1 = (const lds_bf16x4*)(qt + slab + tro[1][db]);
+            const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pd0);
+            const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pd1);
+            const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pq0);
+            const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pq1);
+            dva[db] = mfma32(bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, pf[kk], dva[db]);
+            dka[db] = mfma32(bf16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}, sf[kk], dka[db]);
+          }
+        }
+      }
+    }
+    // Next tile: this wave's copies of tile it+1 landed (issued one tile ago); after the barrier
+    // every wave is done with `cur`, which receives tile it+2.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (more2) {
+      issue(it + 2, cur);
+      store_scal(cur);
+    }
+  }
+
+  if (kvalid) {
+    bf16_t* ko = dk + (krow + kj) * DH;
+    bf16_t* vo = dv + (krow + kj) * DH;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        *reinterpret_cast<u32x2*>(ko + d) =
+            u32x2{pack_bf16x2(dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale),
+                  pack_bf16x2(dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale)};
+        *reinterpret_cast<u32x2*>(vo + d) = u32x2{pack_bf16x2(dva[db][4 * rq], dva[db][4 * rq + 1]),
+                                                  pack_bf16x2(dva[db][4 * rq + 2], dva[db][4 * rq + 3])};
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Forward and dQ for head_dim 128, DMA-fed. Same ownership and math as attn_fwd_kernel /
+// attn_bwd_dq_kernel. Each 64-key K and V tile is copied global -> LDS (rows past S read as
+// zeros) in the swizzled 256 B-row layout of the dK/dV kernel; S^T = K Q^T and dP^T = V dO^T read
+// row fragments, O^T += V^T P^T and dQ^T += K^T dS^T read transposed fragments of the same tiles.
+// Two LDS stages, one barrier per key tile.
+// ------------------------------------------------------------------------------------------
+namespace kv128 {
+constexpr int kRowB = 256;
+constexpr int kTile = kKT * kRowB;            // 16 KiB
+constexpr int kStage = 2 * kTile + 256;       // K, V, key segment ids
+__device__ __forceinline__ int sw(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+
+// Per-lane constants: copy offsets (4 per operand and wave), row-fragment swizzle, transposed
+// fragment offsets (read t of 32-row block db, relative to a 16-row slab).
+struct Lanes {
+  uint32_t coff[4];
+  int sw_r;
+  int tro[2][4];
+  __device__ __forceinline__ void init() {
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int hf = lane >> 5, col = lane & 31;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int row = 4 * (4 * j + w) + (lane >> 4);
+      coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+    }
+    sw_r = sw(col & 15);
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
+      const int swt = sw(rl);
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const int c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+        tro[t][db] = rl * kRowB + ((c ^ swt) << 4) + 8 * (lane & 1);
+      }
+    }
+  }
+  // Copy one 64-row tile (rows from `rows_left` on read as zeros) into `dst`.
+  __device__ __forceinline__ void copy(const bf16_t* src, int rows_left, char* dst) const {
+    const int w = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<bf16_t*>(src), (short)0, rows_left > 0 ? rows_left * kRowB : 0, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + 1024 * (4 * j + w)), 16,
+                                               coff[j], 0, 0, 0);
+  }
+  // Row fragment: tile row `row` (row & 15 == col & 15), k16 step ks, lane half hf.
+  __device__ __forceinline__ bf16x8 row_frag(const char* tile, int row, int ks, int hf) const {
+    return as_bf16x8(lds_read16(tile, row * kRowB + (((2 * ks + hf) ^ sw_r) << 4)));
+  }
+  // Transposed fragment: head_dim block db (32 columns), contraction over tile rows of the 16-row
+  // slab starting at `slab`, in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11).
+  __device__ __forceinline__ bf16x8 t_frag(const char* tile, int slab, int db) const {
+    const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + slab * kRowB + tro[0][db]));
+    const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + slab * kRowB + tro[1][db]));
+    return bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  }
+};
+}  // namespace kv128
+
+template <bool PACKED, bool DQ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                       const bf16_t* __restrict__ d_o, const float* __restrict__ lse_in,
+                       const float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
+                       const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
+                       int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
+  using namespace kv128;
+  constexpr int DH = 128;
+  constexpr int kDK = DH / 16, kDB = DH / 32;
+  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+
+  const int G = Hq / Hkv;
+  const int hpw = heads_per_wg(G);
+  const int P = 32 * (4 / hpw);
+  const int npb = (S + P - 1) / P;
+  const int hgb = Hq / hpw;
+  const int nhg = B * hgb;
+  const int g = blockIdx.x;
+  const int hg = g % nhg;
+  const int pb = npb - 1 - g / nhg;  // heaviest (latest) query blocks first
+  const int bidx = hg / hgb;
+  const int h0 = (hg % hgb) * hpw;
+  const int kvh = h0 / G;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int hf = lane >> 5, col = lane & 31;
+  const int head = h0 + (w % hpw);
+  const int qw0 = pb * P + 32 * (w / hpw);
+  const int qi = qw0 + col;
+  const bool qvalid = qi < S;
+  const bool wave_has = qw0 < S;
+  const int wq_last = wave_has ? ((qw0 + 31 < S) ? qw0 + 31 : S - 1) : 0;
+
+  const long qrow = (long)(bidx * Hq + head) * S;
+  const bf16_t* kh = k + (long)(bidx * Hkv + kvh) * S * DH;
+  const bf16_t* vh = v + (long)(bidx * Hkv + kvh) * S * DH;
+  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  bf16x8 qf[kDK], df[DQ ? kDK : 1];
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks)
+    qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(q + (qrow + qi) * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+  float l2q = 0.f, dq_row = 0.f;
+  if constexpr (DQ) {
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks)
+      df[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(d_o + (qrow + qi) * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+    l2q = qvalid ? lse_in[qrow + qi] * kLog2e : 0.f;
+    dq_row = qvalid ? dvec[qrow + qi] : 0.f;
+  }
+
+  const int wg_q0 = pb * P;
+  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  int kv_begin = 0;
+  if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
+  const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
+
+  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
+  if (PACKED) {
+    my_seg = qvalid ? sid[qi] : -2;
+    w_sst_first = wave_has ? sst[qw0] : 0;
+    w_sst_last = wave_has ? sst[wq_last] : 0;
+  }
+
+  float m = kNegInf, l = 0.f;
+  f32x16 acc[kDB];
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+  Lanes ln;
+  ln.init();
+  int seg_reg = 0;
+  auto issue = [&](int t, char* st) {
+    const int kv0 = kv_begin + t * kKT;
+    ln.copy(kh + (long)kv0 * DH, S - kv0, st);
+    ln.copy(vh + (long)kv0 * DH, S - kv0, st + kTile);
+    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
+  };
+  auto store_seg = [&](char* st) {
+    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + 2 * kTile)[tid] = seg_reg;
+  };
+
+  if (ntiles > 0) {
+    issue(0, lds);
+    store_seg(lds);
+    if (ntiles > 1) issue(1, lds + kStage);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (ntiles > 1) store_seg(lds + kStage);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  asm volatile("s_barrier" ::: "memory");
+
+  for (int t = 0; t < ntiles; ++t) {
+    const char* cur = lds + (t & 1) * kStage;
+    const int kv0 = kv_begin + t * kKT;
+    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    if (!skip) {
+      const char* kt = cur;
+      const char* vt = cur + kTile;
+      f32x16 sacc[2], pacc[DQ ? 2 : 1];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
+        if constexpr (DQ) {
+#pragma unroll
+          for (int r = 0; r < 16; ++r) pacc[kb][r] = 0.f;
+        }
+#pragma unroll
+        for (int ks = 0; ks < kDK; ++ks) {
+          sacc[kb] = mfma32(ln.row_frag(kt, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
+          if constexpr (DQ) pacc[kb] = mfma32(ln.row_frag(vt, 32 * kb + col, ks, hf), df[ks], pacc[kb]);
+        }
+      }
+      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int* segs = reinterpret_cast<const int*>(cur + 2 * kTile);
+      bf16x8 pf[4];
+      if constexpr (DQ) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float p = fast_exp2(sacc[kb][r] * scale_log2 - l2q);
+            if (need_mask) {
+              const int j = kv0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+              bool ok = (j <= qi) && (j < S) && qvalid;
+              if (PACKED) ok = ok && (segs[j - kv0] == my_seg);
+              if (!ok) p = 0.f;
+            }
+            pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
+          }
+      } else {
+        float mt = kNegInf;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            float x = sacc[kb][r] * scale_log2;
+            if (need_mask) {
+              const int j = kv0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
+              bool ok = (j <= qi) && (j < S) && qvalid;
+              if (PACKED) ok = ok && (segs[j - kv0] == my_seg);
+              if (!ok) x = kNegInf;
+            }
+            sacc[kb][r] = x;
+            mt = fmaxf(mt, x);
+          }
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mn = fmaxf(m, mt);
+        const float base = (mn == kNegInf) ? 0.f : mn;
+        const float alpha = fast_exp2(m - base);
+        m = mn;
+        l *= alpha;
+#pragma unroll
+        for (int db = 0; db < kDB; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+        float ls = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const float p = fast_exp2(sacc[kb][r] - base);
+            ls += p;
+            pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
+          }
+        l += ls;
+      }
+      // O^T += V^T P^T (forward) or dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
+      const char* at = DQ ? kt : vt;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(ln.t_frag(at, 16 * ks, db), pf[ks], acc[db]);
+    }
+    // This wave's copies of tile t+1 landed; after the barrier nobody reads `cur`, which takes t+2.
+    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    asm volatile("s_barrier" ::: "memory");
+    if (t + 2 < ntiles) {
+      issue(t + 2, const_cast<char*>(cur));
+      store_seg(const_cast<char*>(cur));
+    }
+  }
+
+  float mul = scale, lt = 0.f;
+  if constexpr (!DQ) {
+    lt = l + __shfl_xor(l, 32, 64);
+    mul = (lt > 0.f) ? 1.f / lt : 0.f;
+  }
+  if (qvalid) {
+    bf16_t* oh = out + (qrow + qi) * DH;
+    if constexpr (!DQ) {
+      if (hf == 0) lse_out[qrow + qi] = (m + fast_log2(lt)) * kLn2;
+    }
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        *reinterpret_cast<u32x2*>(oh + d) = u32x2{pack_bf16x2(acc[db][4 * rq] * mul, acc[db][4 * rq + 1] * mul),
+                                                  pack_bf16x2(acc[db][4 * rq + 2] * mul, acc[db][4 * rq + 3] * mul)};
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Launchers
 // ------------------------------------------------------------------------------------------
 namespace {
@@ -723,6 +1252,11 @@ hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
                   const int32_t* sst, bf16_t* o, float* lse, hipStream_t st) {
   const float sl2 = sh.scale * kLog2e;
   dim3 grid(fwd_grid(sh)), block(256);
+  if constexpr (DH == 128) {
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    return hipGetLastError();
+  }
   if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
   else hipLaunchKernelGGL((attn_fwd_kernel<DH, false>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
   return hipGetLastError();
@@ -739,11 +1273,21 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   if (e != hipSuccess) return e;
   const float sl2 = sh.scale * kLog2e;
   dim3 qgrid(fwd_grid(sh));
+  if constexpr (DH == 128) {
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  } else {
   if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
   else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
+  if constexpr (DH == 128) {
+    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_kernel<true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_bwd_dkv128_kernel<false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    return hipGetLastError();
+  }
   if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
   else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
   return hipGetLastError();

@@ -24,6 +24,7 @@ SHAPES = [  # (b, hq, hkv, s, d)
     (1, 4, 1, 130, 96),
     (1, 8, 2, 300, 128),
     (1, 6, 2, 200, 128),
+    (1, 8, 2, 1100, 128),   # 18 key tiles: the two-stage copy rotation over many tiles
 ]
 
 
