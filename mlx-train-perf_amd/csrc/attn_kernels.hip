@@ -29,6 +29,7 @@ namespace mtp {
 
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 
@@ -870,20 +871,17 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
     const bool more2 = it + 2 < niter;
     if (more2) load_scal(it + 2);
     bool skip = !wave_has || (q0 + kKT - 1 < kw0);
-    int sst_last = 0;
-    if (PACKED && !skip) {
-      skip = sst[q0] > kw0 + 31;
-      sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
-    }
+    if (PACKED && !skip) skip = sst[q0] > kw0 + 31;
     if (!skip) {
-      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
       const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
       const float* ds_ = l2s + 64;
       const int* segs = reinterpret_cast<const int*>(l2s + 128);
       const char* qt = cur;
       const char* dt = cur + kTile;
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
+      // Per 32-query half: S and dP (MFMA), probabilities and dS (VALU), dV and dK (MFMA). The
+      // body is branch-free; tiles away from the diagonal and the tail skip the element masks.
+      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || PACKED;
+      auto half = [&](int qb, bool masked) {
         f32x16 sacc, pacc;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -903,15 +901,17 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
           const int ql0 = 32 * qb + 8 * rq + 4 * hf;
           const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
           const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+          i32x4 s4 = {0, 0, 0, 0};
+          if (PACKED && masked) s4 = *reinterpret_cast<const i32x4*>(segs + ql0);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int r = 4 * rq + u;
             float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
-            if (need_mask) {
+            if (masked) {
               const int qq = q0 + ql0 + u;
               bool ok = (kj <= qq) && (qq < S) && kvalid;
-              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
-              if (!ok) p = 0.f;
+              if (PACKED) ok = ok && (s4[u] == my_seg);
+              p = ok ? p : 0.f;
             }
             pf[r >> 3][r & 7] = (__bf16)p;
             sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[u]));
@@ -922,18 +922,21 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
           const int slab = (32 * qb + 16 * kk) * kRowB;
 #pragma unroll
           for (int db = 0; db < kDB; ++db) {
-            const lds_bf16x4* pd0 = (const lds_bf16x4*)(dt + slab + tro[0][db]);
-            const lds_bf16x4* pd1 = (const lds_bf16x4*)(dt + slab + tro[1][db]);
-            const lds_bf16x4* pq0 = (const lds_bf16x4*)(qt + slab + tro[0][db]);
-            const lds_bf16x4* pq1 = (const lds_bf16x4*)(qt + slab + tro[1][db]);
-            const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pd0);
-            const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pd1);
-            const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pq0);
-            const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)pq1);
+            const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(dt + slab + tro[0][db]));
+            const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(dt + slab + tro[1][db]));
+            const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(qt + slab + tro[0][db]));
+            const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(qt + slab + tro[1][db]));
             dva[db] = mfma32(bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, pf[kk], dva[db]);
             dka[db] = mfma32(bf16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}, sf[kk], dka[db]);
           }
         }
+      };
+      if (need_mask) {
+        half(0, true);
+        half(1, true);
+      } else {
+        half(0, false);
+        half(1, false);
       }
     }
     // Next tile: this wave's copies of tile it+1 landed (issued one tile ago); after the barrier
