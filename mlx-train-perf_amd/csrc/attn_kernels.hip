@@ -715,7 +715,9 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 // Backward dK, dV for head_dim 128, DMA-fed. Same ownership and math as attn_bwd_dkv_kernel; the
 // 64-query Q and dO tiles are copied global -> LDS by buffer_load ... lds (16 bytes per lane, rows
 // past S read as zeros) into 256 B rows whose 16-byte chunks are XOR-swizzled by
-// sw(r) = 2 (r & 7) + ((r >> 3) & 1). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128;
+// sw(r) = 4 (r & 3) + ((r >> 2) & 3): a bijection over any 16 consecutive rows (row fragments, 16
+// lanes per LDS cycle) that also sends the aligned 4-chunk block of each of 4 consecutive rows to a
+// different quarter of the banks (transposed fragments, 32 lanes x 8 bytes per LDS cycle). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128;
 // the transposed operands of dV += dO^T P and dK += Q^T dS are ds_read_b64_tr_b16 of the same
 // tiles. The two reads of a transposed fragment start at query rows 4 hf and 4 hf + 8 of each
 // 16-row slab, which is the order of the probability / dS registers (MFMA accumulator rows), so
@@ -727,7 +729,7 @@ constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
 constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
 constexpr int kScal = 3 * 256;             // lse*log2e, D, segment id of the 64 queries
 constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
-__device__ __forceinline__ int sw(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 }  // namespace dkv128
 
 template <bool PACKED>
@@ -977,7 +979,7 @@ namespace kv128 {
 constexpr int kRowB = 256;
 constexpr int kTile = kKT * kRowB;            // 16 KiB
 constexpr int kStage = 2 * kTile + 256;       // K, V, key segment ids
-__device__ __forceinline__ int sw(int r) { return ((r & 7) << 1) | ((r >> 3) & 1); }
+__device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // Per-lane constants: copy offsets (4 per operand and wave), row-fragment swizzle, transposed
 // fragment offsets (read t of 32-row block db, relative to a 16-row slab).
