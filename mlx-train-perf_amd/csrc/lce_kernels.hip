@@ -320,13 +320,14 @@ struct DmaRowOp {
       voff[i] = 2u * (uint32_t)(src * ld + 8 * c);
     }
   }
-  __device__ __forceinline__ void issue(int kt, char* dst) const { issue_at(0, kt, dst); }
+  __device__ __forceinline__ void issue(int kt, char* dst, bool live = true) const { issue_at(0, kt, dst, live); }
   // Copy from the tile `shift` bytes further on with the same per-lane offsets (valid when both
-  // tiles are whole, i.e. no row was clamped).
-  __device__ __forceinline__ void issue_at(long shift, int kt, char* dst) const {
+  // tiles are whole, i.e. no row was clamped). A copy that is not `live` gets a zero-byte range:
+  // it touches no memory and writes zeros.
+  __device__ __forceinline__ void issue_at(long shift, int kt, char* dst, bool live = true) const {
     const int w = threadIdx.x >> 6;
     const long o = shift + kt * (2 * kBK);
-    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, bytes - kt * (2 * kBK));
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, live ? bytes - kt * (2 * kBK) : 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(r, voff[i], dst + 1024 * (8 * i + w));
   }
@@ -375,10 +376,10 @@ struct DmaTransOp {
       cofs[i] = 2u * (uint32_t)col;
     }
   }
-  __device__ __forceinline__ void issue(int kt, char* dst) const {
+  __device__ __forceinline__ void issue(int kt, char* dst, bool live = true) const {
     const int w = threadIdx.x >> 6;
     const int k0 = kt * kBK;
-    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + k0 * ldb, (long)(kvalid - k0) * ldb);
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + k0 * ldb, live ? (long)(kvalid - k0) * ldb : 0);
     const int kmax = kvalid - 1 - k0;  // last readable k-row of this stage (may be negative)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -440,6 +441,19 @@ __device__ __forceinline__ void dma_sched() {
   }
 }
 
+// Last k-step of a stage: its 8 MFMAs interleaved with the 8 copies of the stage after next and
+// the NR reads of the next stage's first fragments.
+template <int NR, int S = 0>
+__device__ __forceinline__ void dma_sched_copy() {
+  if constexpr (S < 8) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    constexpr int r = NR * (S + 1) / 8 - NR * S / 8;
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    dma_sched_copy<NR, S + 1>();
+  }
+}
+
 // acc[i][j] (wave sub-tile 128 x 64: wave w covers A rows 128 (w & 1) .., B rows 64 (w >> 1) ..)
 // = A_tile . B_tile^T over nk 64-deep slabs. `pre`: stages 0 and 1 were already issued (by the
 // previous call's `next`). `next` (may be null-like: has_next false) issues the following tile's
@@ -472,7 +486,9 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
 
   bf16x8 fa[4], fb[kNJ], ga[4], gb[kNJ];
   dma_read_frags(oa, ob, lds, 0, fa, fb);
-  for (int kt = 0; kt < nk; ++kt) {
+  // All stages but the last: the body is branch-free (the copies of a stage past the end are not
+  // live), so the scheduler can interleave them with the last k-step's MFMAs.
+  for (int kt = 0; kt + 1 < nk; ++kt) {
     char* cur = lds + ((kt & 1) ? kDmaStage : 0);
     char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
     dma_read_frags(oa, ob, cur, 1, ga, gb);
@@ -487,13 +503,29 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     wait_lgkmcnt0();
     wait_vmcnt<0>();
     raw_barrier();
-    if (kt + 2 < nk) {
-      oa.issue(kt + 2, cur);
-      ob.issue(kt + 2, cur + 32768);
-    } else if (kt + 1 == nk && has_next) {
-      next();
-    }
-    if (kt + 1 < nk) dma_read_frags(oa, ob, nxt, 0, fa, fb);
+    const bool live = kt + 2 < nk;
+    oa.issue(kt + 2, cur, live);
+    ob.issue(kt + 2, cur + 32768, live);
+    dma_read_frags(oa, ob, nxt, 0, fa, fb);
+    dma_mfma(ga, gb, acc);
+    dma_sched_copy<NR>();
+  }
+  // Last stage.
+  {
+    char* cur = lds + (((nk - 1) & 1) ? kDmaStage : 0);
+    dma_read_frags(oa, ob, cur, 1, ga, gb);
+    dma_mfma(fa, fb, acc);
+    dma_sched<NR>();
+    dma_read_frags(oa, ob, cur, 2, fa, fb);
+    dma_mfma(ga, gb, acc);
+    dma_sched<NR>();
+    dma_read_frags(oa, ob, cur, 3, ga, gb);
+    dma_mfma(fa, fb, acc);
+    dma_sched<NR>();
+    wait_lgkmcnt0();
+    wait_vmcnt<0>();
+    raw_barrier();
+    if (has_next) next();
     dma_mfma(ga, gb, acc);
     dma_sched<NR>();
   }
