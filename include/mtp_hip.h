@@ -78,19 +78,21 @@ size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
 /* Row pitch (elements) of the transposed dense head used by mtp_lce_bwd: round_up(v, 256) + 64. */
 int64_t mtp_lce_head_t_ld(int64_t v);
 
-/* Transposed dense head for the backward: w_t[dd][vv] = w[vv][dd] for vv < v and 0 for
- * v <= vv < mtp_lce_head_t_ld(v); w_t is bf16 [d][mtp_lce_head_t_ld(v)], caller-allocated.
- * No reference counterpart (the reference reads w directly); a caller that keeps a frozen head
- * transposed once passes it to mtp_lce_bwd so the dH product reads both operands along the
- * contraction. */
-int mtp_lce_head_transpose(const void* w, int64_t v, int64_t d, void* w_t, void* stream);
+/* Transposed head for the backward: w_t[dd][vv] = W[vv][dd] for vv < v and 0 for
+ * v <= vv < mtp_lce_head_t_ld(v), bf16 [d][mtp_lce_head_t_ld(v)], caller-allocated. W is the dense
+ * head, or for head_kind Q4 its dequantization bf16(scale * q + bias) (the values the kernels use).
+ * No reference counterpart (the reference reads w directly and dequantizes chunk-wise in its
+ * vjp, core/loss.py:333-343); a caller that keeps a frozen head transposed once passes it to
+ * mtp_lce_bwd so the dH product reads both operands along the contraction. */
+int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scales, const void* biases,
+                           int64_t v, int64_t d, int32_t head_kind, void* w_t, void* stream);
 
 /* Backward: d_hidden[t] = sum_v g[t][v] w[v] with g[t][v] = bf16((exp(z[t][v] - lse[t]) - [v == targets[t]])
  * * coef[t]), coef[t] = d_nll[t] (0 for ignored rows); d_hidden is bf16 [n][d]. When d_w is non-null
  * (trainable dense head) it also writes d_w[v] = sum_t g[t][v] hidden[t], bf16 [v][d]; a quantized head
  * is frozen and must pass d_w = NULL. lse is the forward's saved output (no recompute of the forward).
- * w_t (optional, dense head only) is w transposed by mtp_lce_head_transpose; it must hold the same
- * values as w and only changes how the dH product reads the head (faster when given).
+ * w_t (optional) is the head transposed by mtp_lce_head_transpose; it must hold the values the
+ * kernels use for the head and only changes how the dH product reads it (faster when given).
  * Replaces: the kernel-path vjps _ce_vjp / _ce_frozen_vjp / quantized _ce_vjp
  * (core/loss.py:242-298,322-349) that call chunked_backward (core/chunked.py:52-90, d_w at :90);
  * design of the fused 2-GEMM backward K4 (core/kernel/source.py:475-611) and of the d_w kernel K5

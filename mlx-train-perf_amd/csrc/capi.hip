@@ -137,12 +137,22 @@ size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
 
 int64_t mtp_lce_head_t_ld(int64_t v) { return v < 1 ? 0 : (int64_t)mtp::lce_head_t_ld((long)v); }
 
-int mtp_lce_head_transpose(const void* w, int64_t v, int64_t d, void* w_t, void* stream) {
+int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scales, const void* biases, int64_t v,
+                           int64_t d, int32_t head_kind, void* w_t, void* stream) {
   if (v < 1 || d < 1 || v > kMaxDim || d > kMaxDim) return fail(MTP_ERR_INPUT, "v, d must be in [1, 2^31) (got v=%lld d=%lld)", (long long)v, (long long)d);
-  if (!w || !w_t) return fail(MTP_ERR_INPUT, "w and w_t must be non-null");
-  if (!aligned16(w) || !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w and w_t must be 16-byte aligned");
-  if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "head transpose requires d %% 8 == 0 (got d=%lld)", (long long)d);
-  hipError_t e = mtp::launch_lce_head_transpose(static_cast<const mtp::bf16_t*>(w), (int)v, (int)d,
+  if (!w_t) return fail(MTP_ERR_INPUT, "w_t must be non-null");
+  if (!aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w_t must be 16-byte aligned");
+  if (head_kind == MTP_HEAD_DENSE) {
+    if (!w) return fail(MTP_ERR_INPUT, "dense head: w must be non-null");
+    if (!aligned16(w)) return fail(MTP_ERR_UNSUPPORTED, "dense head: w must be 16-byte aligned");
+    if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "head transpose requires d %% 8 == 0 (got d=%lld)", (long long)d);
+  } else if (head_kind == MTP_HEAD_Q4) {
+    if (!w_q || !scales || !biases) return fail(MTP_ERR_INPUT, "quantized head: w_q, scales and biases must be non-null");
+    if (d % 64 != 0) return fail(MTP_ERR_UNSUPPORTED, "quantized head transpose requires d %% 64 == 0 (got d=%lld)", (long long)d);
+  } else {
+    return fail(MTP_ERR_UNSUPPORTED, "unknown head_kind %d", (int)head_kind);
+  }
+  hipError_t e = mtp::launch_lce_head_transpose(make_head(w, w_q, scales, biases, head_kind), (int)v, (int)d,
                                                 static_cast<mtp::bf16_t*>(w_t), static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "head transpose launch failed: %s", hipGetErrorString(e));
   return ok();
@@ -154,7 +164,6 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
                 void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
   if (rc) return rc;
-  if (w_t && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_INPUT, "w_t is the transposed dense head: it must be null for a quantized head");
   if (w_t && !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w_t must be 16-byte aligned");
   if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
   if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");

@@ -912,8 +912,9 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const bool full = (t0 + kTile <= N) && (v_begin + kc <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
-  if (!Q4 && D % kBK == 0 && Wt != nullptr) {
-    // Transposed head [D][ldt] (columns past V are zeros): both operands are K-contiguous rows.
+  if (D % kBK == 0 && Wt != nullptr) {
+    // Transposed (for the 4-bit head: dequantized) head [D][ldt], zeros past V: both operands
+    // are K-contiguous rows.
     DmaRowOp oa;
     oa.init(G + (long)t0 * ldg, ldg, N - t0);
     DmaRowOp ob;
@@ -1038,11 +1039,17 @@ void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __re
 }
 
 // ------------------------------------------------------------------------------------------
-// Transposed dense head for the dH product: Wt[d][v] = W[v][d] for v < V, zeros for
-// V <= v < ldt (ldt = lce_head_t_ld(V)). 64 x 64 tiles through LDS; 16-byte loads and stores.
+// Transposed head for the dH product: Wt[d][v] = W[v][d] for v < V, zeros for
+// V <= v < ldt (ldt = lce_head_t_ld(V)). For the 4-bit head W is its dequantization
+// bf16(scale * q + bias), computed exactly as the register loaders do. 64 x 64 tiles through LDS;
+// 16-byte loads and stores.
 // ------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* __restrict__ W, int V, int D, int ldt,
-                                                                 bf16_t* __restrict__ Wt) {
+template <int Q4>
+__global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* __restrict__ W,
+                                                                 const uint32_t* __restrict__ Wq,
+                                                                 const bf16_t* __restrict__ Sc,
+                                                                 const bf16_t* __restrict__ Bi, int V, int D,
+                                                                 int ldt, bf16_t* __restrict__ Wt) {
   __shared__ uint16_t tile[64][64 + 2];
   const int v0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
   const int t = threadIdx.x;
@@ -1052,7 +1059,14 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
     const int r = id >> 3, c = id & 7;
     const int v = v0 + r, d = d0 + 8 * c;
     u32x4 x = zero4();
-    if (v < V && d < D) x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
+    if (v < V && d < D) {
+      if constexpr (Q4) {
+        const long g = (long)v * (D >> 6) + (d >> 6);
+        x = dequant8(Wq[(long)v * (D >> 3) + (d >> 3)], bf16_to_f32(Sc[g]), bf16_to_f32(Bi[g]));
+      } else {
+        x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
+      }
+    }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       tile[r][8 * c + 2 * e] = (uint16_t)(x[e] & 0xffffu);
@@ -1077,10 +1091,11 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
 
 long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad; }
 
-hipError_t launch_lce_head_transpose(const bf16_t* W, int V, int D, bf16_t* Wt, hipStream_t stream) {
+hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream) {
   const int ldt = (int)lce_head_t_ld(V);
   dim3 grid(ldt / 64, (D + 63) / 64), block(256);
-  hipLaunchKernelGGL(lce_head_transpose_kernel, grid, block, 0, stream, W, V, D, ldt, Wt);
+  if (h.q4) hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
+  else hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
   return hipGetLastError();
 }
 

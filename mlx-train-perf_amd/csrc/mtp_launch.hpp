@@ -19,7 +19,7 @@ constexpr int kGPitchPad = 64;
 struct LceHead {
   int q4;                 // 0: dense bf16 [V][D]; 1: 4-bit affine, group size 64
   const bf16_t* w;        // dense weight
-  const bf16_t* wt;       // optional transposed dense weight [D][lce_head_t_ld(V)] (or null)
+  const bf16_t* wt;       // optional transposed (4-bit: dequantized) weight [D][lce_head_t_ld(V)], or null
   const uint32_t* wq;     // packed nibbles [V][D/8]
   const bf16_t* sc;       // scales [V][D/64]
   const bf16_t* bi;       // biases [V][D/64]
@@ -28,7 +28,7 @@ struct LceHead {
 int lce_fwd_nsplit(long N, long V);
 long lce_head_t_ld(long V);
 
-hipError_t launch_lce_head_transpose(const bf16_t* W, int V, int D, bf16_t* Wt, hipStream_t stream);
+hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream);
 
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,

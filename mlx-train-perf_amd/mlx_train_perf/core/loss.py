@@ -208,10 +208,11 @@ def _chunked_nll(hidden2, head, targets2, ignore_index, chunk_size):
 
 VJP_CALLS: dict[str, int] = {}
 
-# Transposed copies of dense heads for the backward's dH product (mtp_lce_head_transpose), one per
-# device: (owner weakref, data_ptr, shape, version) -> bf16 [D][mtp_lce_head_t_ld(V)]. The owner is
-# the caller's weight tensor; an in-place update through it bumps its version and invalidates the
-# entry. A frozen head is therefore transposed once; a trainable one after every optimizer step.
+# Transposed copies of heads for the backward's dH product (mtp_lce_head_transpose), one per device:
+# (owner weakref, data_ptr, shape, version) -> bf16 [D][mtp_lce_head_t_ld(V)]. The owner is the
+# caller's weight tensor (the packed w_q of a 4-bit head, whose copy holds the dequantized values);
+# an in-place update through it bumps its version and invalidates the entry. A frozen head is
+# therefore transposed once; a trainable one after every optimizer step.
 _HEAD_T_CACHE: dict[int, tuple[tuple, torch.Tensor]] = {}
 
 
@@ -221,19 +222,20 @@ def clear_transposed_head_cache() -> None:
     _HEAD_T_CACHE.clear()
 
 
-def _transposed_head(owner: torch.Tensor | None, w: torch.Tensor) -> torch.Tensor | None:
-    if owner is None or os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "1") == "0" or w.shape[1] % 64 != 0:
+def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_kind: int, v: int,
+                     d: int) -> torch.Tensor | None:
+    if owner is None or os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "1") == "0" or d % 64 != 0:
         return None
-    dev = w.device.index if w.device.index is not None else torch.cuda.current_device()
-    key = (w.data_ptr(), tuple(w.shape), owner._version)
+    dev = owner.device.index if owner.device.index is not None else torch.cuda.current_device()
+    key = (owner.data_ptr(), tuple(owner.shape), owner._version)
     ent = _HEAD_T_CACHE.get(dev)
     if ent is not None and ent[0][0]() is owner and ent[0][1:] == key:
         return ent[1]
     _HEAD_T_CACHE.pop(dev, None)
     lib = _native.load()
-    v, d = w.shape
-    wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=w.device)
-    rc = lib.mtp_lce_head_transpose(w.data_ptr(), v, d, wt.data_ptr(), _native.stream_of(w))
+    wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=owner.device)
+    rc = lib.mtp_lce_head_transpose(_native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases), v, d,
+                                    head_kind, wt.data_ptr(), _native.stream_of(owner))
     _native.check(rc, domain="loss")
     _HEAD_T_CACHE[dev] = ((weakref.ref(owner),) + key, wt)
     return wt
@@ -280,7 +282,7 @@ class _KernelLCE(torch.autograd.Function):
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
         d_hidden = torch.empty_like(hidden2)
         d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
-        w_t = _transposed_head(ctx.owner, w) if head_kind == _native.HEAD_DENSE else None
+        w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
         ct = d_nll.to(torch.float32).contiguous()
         rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),
                              _native.ptr(scales), _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind,
@@ -303,7 +305,7 @@ def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.T
         return _KernelLCE.apply(h, t, w, None, None, None, _native.HEAD_DENSE, int(ignore_index), int(bwd_chunk or 0),
                                 head.weight)
     args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
-    return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0))
+    return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0), head.w_q)
 
 
 def linear_cross_entropy(

@@ -72,11 +72,11 @@ def test_lce_refusals():
     assert rc == _native.MTP_ERR_WORKSPACE
     rc = lib.mtp_lce_bwd(FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_UNSUPPORTED and "frozen" in _native.last_error()
-    rc = lib.mtp_lce_bwd(FAKE, None, FAKE, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 1 << 20, None)
-    assert rc == _native.MTP_ERR_INPUT and "w_t" in _native.last_error()
     assert lib.mtp_lce_head_t_ld(151936) == 152064 + 64 and lib.mtp_lce_head_t_ld(1) == 256 + 64
-    assert lib.mtp_lce_head_transpose(FAKE, 100, 36, FAKE, None) == _native.MTP_ERR_UNSUPPORTED
-    assert lib.mtp_lce_head_transpose(None, 100, 64, FAKE, None) == _native.MTP_ERR_INPUT
+    assert lib.mtp_lce_head_transpose(FAKE, None, None, None, 100, 36, 0, FAKE, None) == _native.MTP_ERR_UNSUPPORTED
+    assert lib.mtp_lce_head_transpose(None, None, None, None, 100, 64, 0, FAKE, None) == _native.MTP_ERR_INPUT
+    assert lib.mtp_lce_head_transpose(None, FAKE, FAKE, FAKE, 100, 96, 1, FAKE, None) == _native.MTP_ERR_UNSUPPORTED
+    assert lib.mtp_lce_head_transpose(None, FAKE, None, FAKE, 100, 64, 1, FAKE, None) == _native.MTP_ERR_INPUT
 
 
 def test_attention_refusals():

@@ -160,10 +160,24 @@ def test_head_transpose_exact(v, d):
     w = torch.randn(v, d, generator=torch.Generator().manual_seed(v)).to(torch.bfloat16).cuda()
     ld = lib.mtp_lce_head_t_ld(v)
     wt = torch.full((d, ld), 7.0, dtype=torch.bfloat16, device="cuda")
-    _native.check(lib.mtp_lce_head_transpose(w.data_ptr(), v, d, wt.data_ptr(), None), domain="loss")
+    _native.check(lib.mtp_lce_head_transpose(w.data_ptr(), None, None, None, v, d, 0, wt.data_ptr(), None), domain="loss")
     torch.cuda.synchronize()
     assert torch.equal(wt[:, :v].cpu(), w.cpu().T)
     assert not wt[:, v:].any()
+    if d % 64 == 0:
+        # 4-bit head: the copy holds bf16(fp32(scale * q + bias)) with one fp32 rounding (an fma); the
+        # fp64 product and sum of bf16 scale/bias and a 4-bit code are exact, so rounding that to fp32
+        # and then to bf16 is the same value.
+        wq, sc, bi = oquant.quantize_affine(w.cpu().float())
+        q = oquant.unpack_nibbles(wq).double()
+        deq = (sc.double().repeat_interleave(64, dim=1) * q + bi.double().repeat_interleave(64, dim=1)).float().to(torch.bfloat16)
+        wt.fill_(7.0)
+        wqd, scd, bid = wq.cuda(), sc.cuda(), bi.cuda()   # kept alive until the launch has run
+        _native.check(lib.mtp_lce_head_transpose(None, wqd.data_ptr(), scd.data_ptr(), bid.data_ptr(), v, d, 1,
+                                                 wt.data_ptr(), None), domain="loss")
+        torch.cuda.synchronize()
+        assert torch.equal(wt[:, :v].cpu(), deq.T)
+        assert not wt[:, v:].any()
 
 
 def test_transposed_head_cache_follows_in_place_updates(monkeypatch):
