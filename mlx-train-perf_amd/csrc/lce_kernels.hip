@@ -303,6 +303,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, c
 // LDS rows are 128 B with the swizzle of lds_off(); fragments are single ds_read_b128.
 struct DmaRowOp {
   static constexpr int kReads = 1;
+  static constexpr bool kProduce = false;  // the copies land in the stage as they are
   const char* base;    // tile row 0, k = 0
   long bytes;          // readable bytes from base (the tile's nrows rows)
   uint32_t voff[4];    // per-lane byte offsets of this wave's four 1 KiB copies
@@ -344,6 +345,7 @@ struct DmaRowOp {
   __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
     return as_bf16x8(lds_read16(st, lo[b] + (((2 * ks) ^ sx[b]) << 4)));
   }
+  __device__ __forceinline__ void produce(int, char*) {}
 };
 
 // K-major operand: element (k, col) at base[k * ld + col]; the tile holds 64 k-rows x 256
@@ -354,6 +356,7 @@ struct DmaRowOp {
 // row kvalid - 1; columns at or past ncols re-read the last 8 columns.
 struct DmaTransOp {
   static constexpr int kReads = 2;
+  static constexpr bool kProduce = false;
   const char* base;    // k = 0, column 0 of the tile
   long ldb;            // row pitch in bytes
   int kvalid;
@@ -404,6 +407,67 @@ struct DmaTransOp {
     const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
     const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
     return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  }
+  __device__ __forceinline__ void produce(int, char*) {}
+};
+
+// 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16): the packed
+// words of each 64-deep slab are copied global -> a 2 x 8 KiB LDS staging area (rows of 32 B), and
+// `produce` dequantizes them, bf16(scale * q + bias) in fp32, into the stage's bf16 A tile (the
+// DmaRowOp layout, read the same way). Thread t produces half a row: row t >> 1, k 32 (t & 1) ..
+// +31; its scale and bias are loaded one slab ahead into registers.
+constexpr int kQ4Stage = 8192;
+struct DmaQ4Op : DmaRowOp {
+  static constexpr bool kProduce = true;
+  const char* qbase;   // packed words of tile row 0
+  long qbytes;         // readable bytes from qbase
+  const bf16_t* sc;    // scales / biases of tile row 0
+  const bf16_t* bi;
+  int D, nrows;
+  uint32_t qoff;       // lane byte offset of its 16-byte copy (row 32 w + L / 2, half L & 1)
+  char* stg;           // staging base (2 x kQ4Stage)
+  float s_n, b_n;      // scale / bias of this thread's row for the next slab to produce
+
+  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D_, int nrows_,
+                                       char* stg_) {
+    qbase = reinterpret_cast<const char*>(wq);
+    qbytes = 4L * nrows_ * (D_ >> 3);
+    sc = sc_;
+    bi = bi_;
+    D = D_;
+    nrows = nrows_;
+    stg = stg_;
+    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
+    const int row = 32 * w + (L >> 1);
+    const int src = row < nrows ? row : nrows - 1;
+    qoff = 4u * (uint32_t)(src * (D >> 3) + 4 * (L & 1));
+  }
+  // Next tile, `rows` further on, with the same lane offsets (both tiles whole).
+  __device__ __forceinline__ void advance(int rows) {
+    qbase += 4L * rows * (D >> 3);
+    sc += (long)rows * (D >> 6);
+    bi += (long)rows * (D >> 6);
+  }
+  __device__ __forceinline__ void issue(int kt, char*, bool live = true) const {
+    const int w = threadIdx.x >> 6;
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(qbase + kt * 32, live ? qbytes - kt * 32 : 0);
+    dma16(r, qoff, stg + (kt & 1) * kQ4Stage + 1024 * w);
+  }
+  __device__ __forceinline__ void load_sb(int kt) {
+    const int row = threadIdx.x >> 1;
+    const int last = (D >> 6) - 1;  // past the last slab: reload it (branch-free; unused)
+    const long g = (long)(row < nrows ? row : nrows - 1) * (D >> 6) + (kt < last ? kt : last);
+    s_n = bf16_to_f32(sc[g]);
+    b_n = bf16_to_f32(bi[g]);
+  }
+  // Dequantize slab kt (its copies have landed) into the A tile at `stage`, then fetch the next
+  // slab's scale and bias.
+  __device__ __forceinline__ void produce(int kt, char* stage) {
+    const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+    const u32x4 q = lds_read16(stg + (kt & 1) * kQ4Stage, row * 32 + 16 * h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) lds_write16(stage, lds_off(row, 4 * h + c), dequant8(q[c], s_n, b_n));
+    load_sb(kt + 1);
   }
 };
 
@@ -474,6 +538,7 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   if (!pre) {
+    if constexpr (OA::kProduce) oa.load_sb(0);
     oa.issue(0, lds);
     ob.issue(0, lds + 32768);
     if (nk > 1) {
@@ -481,7 +546,13 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       ob.issue(1, lds + kDmaStage + 32768);
     }
   }
-  if (nk > 1 && !pre) wait_vmcnt<8>(); else wait_vmcnt<0>();
+  if constexpr (OA::kProduce) {
+    wait_vmcnt<0>();
+    oa.produce(0, lds);
+    wait_lgkmcnt0();
+  } else {
+    if (nk > 1 && !pre) wait_vmcnt<8>(); else wait_vmcnt<0>();
+  }
   raw_barrier();
 
   bf16x8 fa[4], fb[kNJ], ga[4], gb[kNJ];
@@ -502,6 +573,10 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     dma_sched<NR>();
     wait_lgkmcnt0();
     wait_vmcnt<0>();
+    if constexpr (OA::kProduce) {
+      oa.produce(kt + 1, nxt);
+      wait_lgkmcnt0();
+    }
     raw_barrier();
     const bool live = kt + 2 < nk;
     oa.issue(kt + 2, cur, live);
@@ -568,7 +643,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                     const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
                     float* __restrict__ part_m, float* __restrict__ part_s) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
   const int g = blockIdx.x;
   const int split = g % nsplit;
   const int rt = g / nsplit;
@@ -654,6 +729,37 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
         if (next_whole) oa.base += tile_bytes;
         else oa.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
       }
+      consume(acc, v0);
+    }
+    raw_barrier();
+  } else if (Q4) {
+    // 4-bit head (D % 64 == 0): packed words copied to LDS and dequantized there (DmaQ4Op).
+    DmaRowOp ob;
+    ob.init(H + (long)t0 * D, D, N - t0);
+    DmaQ4Op oa;
+    const int vb0 = vt_begin * kTile;
+    oa.init(Wq + (long)vb0 * (D >> 3), Sc + (long)vb0 * (D >> 6), Bi + (long)vb0 * (D >> 6), D, V - vb0,
+            lds + kLdsBytes);
+    bool pre = false;
+    for (int vt = vt_begin; vt < vt_end; ++vt) {
+      const int v0 = vt * kTile;
+      const bool has_next = vt + 1 < vt_end;
+      // After the last barrier of this tile `oa` is only needed for the next tile: move it there
+      // and start its first two stages.
+      auto next = [&]() {
+        const int v1 = v0 + kTile;
+        if (v1 + kTile <= V) oa.advance(kTile);
+        else oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, V - v1,
+                     lds + kLdsBytes);
+        oa.load_sb(0);
+        oa.issue(0, lds);
+        if (nk > 1) oa.issue(1, lds);
+        ob.issue(0, lds + 32768);
+        if (nk > 1) ob.issue(1, lds + kDmaStage + 32768);
+      };
+      f32x16 acc[4][kNJ];
+      gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next);
+      pre = has_next;
       consume(acc, v0);
     }
     raw_barrier();
@@ -798,7 +904,7 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
                       const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
                       const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
                       int N, int D, int V, int v_begin, int v_end, int vtiles, int ldg, bf16_t* __restrict__ G) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   int rt, vtl;
   if (!xcd_tile(rtiles, vtiles, rt, vtl)) return;
@@ -816,6 +922,13 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   if (!Q4 && D % kBK == 0) {
     DmaRowOp oa;
     oa.init(W + (long)v0 * D, D, vlim - v0);
+    DmaRowOp ob;
+    ob.init(H + (long)t0 * D, D, N - t0);
+    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+  } else if (Q4) {
+    DmaQ4Op oa;
+    oa.init(Wq + (long)v0 * (D >> 3), Sc + (long)v0 * (D >> 6), Bi + (long)v0 * (D >> 6), D, vlim - v0,
+            lds + kLdsBytes);
     DmaRowOp ob;
     ob.init(H + (long)t0 * D, D, N - t0);
     gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
