@@ -632,6 +632,18 @@ __device__ __forceinline__ bool xcd_tile(int mtiles, int ntiles, int& m, int& n)
   return true;
 }
 
+// Row-grouped order for launches whose M-axis tiles divide into 8 groups: XCD x (workgroup g runs
+// on XCD g % 8) owns M tiles [x M/8, (x+1) M/8) for every N tile, walked N-major, so the ~32
+// workgroups resident on one XCD cover M/8 x 32/(M/8) tiles and each M-operand panel is fetched by
+// one XCD only. Returns false for padding workgroups and when M % 8 != 0 (use xcd_tile then).
+__device__ __forceinline__ bool xcd_rows_tile(int mtiles, int ntiles, int& m, int& n) {
+  if (mtiles % 8 != 0) return false;
+  const int rpx = mtiles / 8, slot = blockIdx.x >> 3;
+  m = (blockIdx.x & 7) * rpx + slot % rpx;
+  n = slot / rpx;
+  return n < ntiles;
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward: per (row tile, vocab split) workgroup, running per-token (max, sum exp2) partials.
 // A operand = head rows (vocab), B operand = hidden rows (tokens): every lane then owns whole
@@ -644,9 +656,21 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
                     float* __restrict__ part_m, float* __restrict__ part_s) {
   __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
+  // Workgroup g runs on XCD g % 8. When the row tiles divide into 8 groups, XCD x owns row tiles
+  // [x R/8, (x+1) R/8) for every split, walked split-major: the ~32 workgroups resident on one XCD
+  // then cover R/8 row tiles x 32/(R/8) splits (4 x 8 at the flagship), whose hidden and head
+  // slabs overlap in that XCD's L2 more than 16 row tiles x 2 splits would.
   const int g = blockIdx.x;
-  const int split = g % nsplit;
-  const int rt = g / nsplit;
+  const int rtiles = (N + kTile - 1) / kTile;
+  int split, rt;
+  if (rtiles % 8 == 0 && nsplit % 8 == 0) {
+    const int rpx = rtiles / 8, slot = g >> 3;
+    rt = (g & 7) * rpx + slot % rpx;
+    split = slot / rpx;
+  } else {
+    split = g % nsplit;
+    rt = g / nsplit;
+  }
   const int vtiles = (V + kTile - 1) / kTile;
   const int vt_begin = (int)(((long)split * vtiles) / nsplit);
   const int vt_end = (int)(((long)(split + 1) * vtiles) / nsplit);
@@ -1013,7 +1037,11 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   int rt, dt;
-  if (!xcd_tile(rtiles, dtiles, rt, dt)) return;
+  if (rtiles % 8 == 0) {
+    if (!xcd_rows_tile(rtiles, dtiles, rt, dt)) return;
+  } else if (!xcd_tile(rtiles, dtiles, rt, dt)) {
+    return;
+  }
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
   const int wa = w & 1, wb = w >> 1;
