@@ -17,6 +17,8 @@
 // stages by direct global->LDS copies (gemm_dma); the register-staged core (gemm_256x256) serves
 // the 4-bit head, whose rows are dequantized in registers, and shapes whose contraction length is
 // not a multiple of 64.
+#include <type_traits>
+
 #include "mtp_common.hpp"
 #include "mtp_launch.hpp"
 
@@ -75,40 +77,6 @@ struct RowKLoader {
       const int row = (tid >> 3) + 64 * p;
       lds_write16(lds, lds_off(row, c), r[p]);
     }
-  }
-};
-
-// Rows of a 4-bit affine group-quantized matrix: wq [rows][K/8] u32 (8 nibbles per word, low
-// nibble first), scales/biases [rows][K/64] bf16. K % 64 == 0; one group per 64-wide K slab.
-// Each thread owns one row of the tile and dequantizes it in registers before the LDS write.
-struct Q4RowKLoader {
-  const uint32_t* wq;
-  const bf16_t* sc;
-  const bf16_t* bi;
-  int nrows;
-  int K;
-  u32x4 q0;
-  float s, b;
-
-  // Thread t owns half a row: row t >> 1, words 4 * (t & 1) .. +3 (chunks of 8 values each).
-  template <bool FULL>
-  __device__ __forceinline__ void load(int kt) {
-    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
-    if (FULL || row < nrows) {
-      q0 = *reinterpret_cast<const u32x4*>(wq + (long)row * (K >> 3) + kt * 8 + 4 * half);
-      const long g = (long)row * (K >> 6) + kt;
-      s = bf16_to_f32(sc[g]);
-      b = bf16_to_f32(bi[g]);
-    } else {
-      q0 = zero4();
-      s = 0.f;
-      b = 0.f;
-    }
-  }
-  __device__ __forceinline__ void store(char* lds) const {
-    const int row = threadIdx.x >> 1, half = threadIdx.x & 1;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) lds_write16(lds, lds_off(row, 4 * half + c), dequant8(q0[c], s, b));
   }
 };
 
@@ -523,7 +491,9 @@ __device__ __forceinline__ void dma_sched_copy() {
 // previous call's `next`). `next` (may be null-like: has_next false) issues the following tile's
 // stages 0 and 1 after the last barrier, when both buffers are free. Returns with no LDS reads
 // outstanding; the caller must barrier before writing LDS itself.
-template <class OA, class OB, class NEXT>
+// PRE_VM: VMEM operations the caller issued after the prefetched stages (only with `pre`); the
+// first wait leaves them in flight.
+template <int PRE_VM = 0, class OA, class OB, class NEXT>
 __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x16 (&acc)[4][kNJ], bool pre,
                                          bool has_next, const NEXT& next) {
   constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
@@ -547,11 +517,13 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     }
   }
   if constexpr (OA::kProduce) {
-    wait_vmcnt<0>();
+    if (pre) wait_vmcnt<PRE_VM>(); else wait_vmcnt<0>();
     oa.produce(0, lds);
     wait_lgkmcnt0();
   } else {
-    if (nk > 1 && !pre) wait_vmcnt<8>(); else wait_vmcnt<0>();
+    if (pre) wait_vmcnt<PRE_VM>();
+    else if (nk > 1) wait_vmcnt<8>();
+    else wait_vmcnt<0>();
   }
   raw_barrier();
 
@@ -788,6 +760,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     }
     raw_barrier();
   } else {
+    // Dense head with D % 64 != 0: register-staged core (the 4-bit head requires D % 64 == 0).
     RowKLoader lb;
     lb.base = H + (long)t0 * D;
     lb.ld = D;
@@ -797,22 +770,12 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       const int v0 = vt * kTile;
       const bool full = (v0 + kTile <= V) && (t0 + kTile <= N) && (D % kBK == 0);
       f32x16 acc[4][kNJ];
-      if constexpr (Q4) {
-        Q4RowKLoader la;
-        la.wq = Wq + (long)v0 * (D >> 3);
-        la.sc = Sc + (long)v0 * (D >> 6);
-        la.bi = Bi + (long)v0 * (D >> 6);
-        la.nrows = V - v0;
-        la.K = D;
-        if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-      } else {
-        RowKLoader la;
-        la.base = W + (long)v0 * D;
-        la.ld = D;
-        la.nrows = V - v0;
-        la.K = D;
-        if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-      }
+      RowKLoader la;
+      la.base = W + (long)v0 * D;
+      la.ld = D;
+      la.nrows = V - v0;
+      la.K = D;
+      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
       consume(acc, v0);
     }
   }
@@ -917,18 +880,18 @@ __global__ __launch_bounds__(256) void lce_fwd_finalize_kernel(
 // ------------------------------------------------------------------------------------------
 // Backward step 1: G[t][v - v_begin] = bf16((exp(z_tv - lse_t) - [v == y_t]) * coef_t) for one
 // vocab chunk [v_begin, v_end). coef_t = d_nll_t, or 0 for ignored rows. Columns of the padded
-// chunk beyond v_end are written as zeros. Tiles are linearised vocab-tile-major and dealt out in
-// contiguous runs per XCD (workgroup id g runs on XCD g % 8), so concurrently running tiles on
-// one XCD share the same weight rows in L2.
+// chunk beyond v_end are written as zeros. This form (one tile per workgroup, register-staged
+// core) serves dense heads whose hidden dim is not a multiple of 64; the persistent form below
+// takes every other shape. Tiles are linearised vocab-tile-major and dealt out in contiguous runs
+// per XCD (workgroup id g runs on XCD g % 8), so concurrently running tiles on one XCD share the
+// same weight rows in L2.
 // ------------------------------------------------------------------------------------------
-template <int Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
-                      const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
-                      const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
-                      const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
-                      int N, int D, int V, int v_begin, int v_end, int vtiles, int ldg, bf16_t* __restrict__ G) {
-  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
+                      const int64_t* __restrict__ targets, const float* __restrict__ lse,
+                      const float* __restrict__ dnll, long long ignore_index, int N, int D, int V, int v_begin,
+                      int v_end, int vtiles, int ldg, bf16_t* __restrict__ G) {
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   int rt, vtl;
   if (!xcd_tile(rtiles, vtiles, rt, vtl)) return;
@@ -943,41 +906,18 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
   const bool full = (v0 + kTile <= vlim) && (t0 + kTile <= N) && (D % kBK == 0);
 
   f32x16 acc[4][kNJ];
-  if (!Q4 && D % kBK == 0) {
-    DmaRowOp oa;
-    oa.init(W + (long)v0 * D, D, vlim - v0);
-    DmaRowOp ob;
-    ob.init(H + (long)t0 * D, D, N - t0);
-    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
-  } else if (Q4) {
-    DmaQ4Op oa;
-    oa.init(Wq + (long)v0 * (D >> 3), Sc + (long)v0 * (D >> 6), Bi + (long)v0 * (D >> 6), D, vlim - v0,
-            lds + kLdsBytes);
-    DmaRowOp ob;
-    ob.init(H + (long)t0 * D, D, N - t0);
-    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
-  } else {
+  {
     RowKLoader lb;
     lb.base = H + (long)t0 * D;
     lb.ld = D;
     lb.nrows = N - t0;
     lb.K = D;
-    if constexpr (Q4) {
-      Q4RowKLoader la;
-      la.wq = Wq + (long)v0 * (D >> 3);
-      la.sc = Sc + (long)v0 * (D >> 6);
-      la.bi = Bi + (long)v0 * (D >> 6);
-      la.nrows = vlim - v0;
-      la.K = D;
-      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-    } else {
-      RowKLoader la;
-      la.base = W + (long)v0 * D;
-      la.ld = D;
-      la.nrows = vlim - v0;
-      la.K = D;
-      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-    }
+    RowKLoader la;
+    la.base = W + (long)v0 * D;
+    la.ld = D;
+    la.nrows = vlim - v0;
+    la.K = D;
+    if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
   }
   // Epilogue: stage the bf16 G tile as [token][vocab] (512 B rows, 16-byte chunks swizzled by
   // row & 31), then write it out with coalesced 16-byte stores.
@@ -1019,6 +959,155 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
     if (t < N) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(lds + row * 512 + ((c ^ (row & 31)) << 4));
       *reinterpret_cast<u32x4*>(G + (long)t * ldg + vtl * kTile + 8 * c) = v;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// Backward step 1, persistent form (hidden dim a multiple of 64). Workgroup (row tile, vocab
+// split) walks its split's vocab tiles of the chunk back to back on the DMA core, in the
+// forward's XCD-grouped order; the next tile's first two stages are issued during the current
+// tile's last k-step. Each lane stores its G values straight from the accumulator layout (8-byte
+// buffer stores of 4 columns; the write-back L2 merges a row's 16 segments into whole lines), so
+// the epilogue needs no barrier and its stores drain while the next tile's MFMAs run: every
+// thread issues exactly kGStores stores per tile and the next tile's first wait leaves those in
+// flight.
+// ------------------------------------------------------------------------------------------
+constexpr int kGStores = 4 * 4 * kNJ;
+
+template <int Q4>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
+                              const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
+                              const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
+                              const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
+                              int N, int D, int V, int v_begin, int v_end, int ctiles, int nsplit, int ldg,
+                              bf16_t* __restrict__ G) {
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
+
+  const int g = blockIdx.x;
+  const int rtiles = (N + kTile - 1) / kTile;
+  int split, rt;
+  if (rtiles % 8 == 0 && nsplit % 8 == 0) {
+    const int rpx = rtiles / 8, slot = g >> 3;
+    rt = (g & 7) * rpx + slot % rpx;
+    split = slot / rpx;
+  } else {
+    split = g % nsplit;
+    rt = g / nsplit;
+  }
+  const int vt_begin = (int)(((long)split * ctiles) / nsplit);
+  const int vt_end = (int)(((long)(split + 1) * ctiles) / nsplit);
+  if (vt_begin >= vt_end) return;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = tid >> 6;
+  const int wa = w & 1, wb = w >> 1;
+  const int lhalf = lane >> 5, lcol = lane & 31;
+  const int t0 = rt * kTile;
+  const int nk = D / kBK;
+  const int vlim = v_end < V ? v_end : V;
+  const int colb = 128 * wa + 4 * lhalf;  // this lane's first G column within a tile
+
+  // Per-thread token rows (fixed for the workgroup): coefficient, log2-domain lse, the target's
+  // column within the chunk (-1 when outside it or ignored) and the row's G byte offset.
+  float coef[kNJ], l2[kNJ];
+  int yrel[kNJ];
+  uint32_t gvo[kNJ];
+#pragma unroll
+  for (int j = 0; j < kNJ; ++j) {
+    const int r = 64 * wb + 32 * j + lcol;
+    const int t = t0 + r;
+    coef[j] = 0.f;
+    l2[j] = 0.f;
+    yrel[j] = -1;
+    gvo[j] = 2u * (uint32_t)(r * ldg + colb);
+    if (t < N) {
+      const long long y = targets[t];
+      const bool ign = y == ignore_index;
+      coef[j] = ign ? 0.f : dnll[t];
+      l2[j] = lse[t] * kLog2e;
+      yrel[j] = (!ign && y >= v_begin && y < vlim) ? (int)(y - v_begin) : -1;
+    }
+  }
+  // G rows of this row tile; stores to rows past N fall outside the range and are dropped.
+  const int grows = N - t0 < kTile ? N - t0 : kTile;
+  const __amdgpu_buffer_rsrc_t gr = dma_rsrc(reinterpret_cast<const char*>(G + (long)t0 * ldg), 2L * grows * ldg);
+
+  DmaRowOp ob;
+  ob.init(H + (long)t0 * D, D, N - t0);
+  typedef typename std::conditional<Q4 != 0, DmaQ4Op, DmaRowOp>::type OpA;
+  OpA oa;
+  auto init_a = [&](int v1) {
+    if constexpr (Q4) {
+      oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1,
+              lds + kLdsBytes);
+    } else {
+      oa.init(W + (long)v1 * D, D, vlim - v1);
+    }
+  };
+  init_a(v_begin + vt_begin * kTile);
+  const long tile_bytes = 2L * kTile * D;
+  bool pre = false;
+  for (int vt = vt_begin; vt < vt_end; ++vt) {
+    const int v0 = v_begin + vt * kTile;
+    const bool has_next = vt + 1 < vt_end;
+    const bool next_whole = v0 + 2 * kTile <= vlim;
+    auto next = [&]() {
+      if constexpr (Q4) {
+        const int v1 = v0 + kTile;
+        if (next_whole) oa.advance(kTile);
+        else init_a(v1);
+        oa.load_sb(0);
+        oa.issue(0, lds);
+        oa.issue(1, lds);
+      } else {
+        if (next_whole) {
+          oa.issue_at(tile_bytes, 0, lds);
+          oa.issue_at(tile_bytes, 1, lds + kDmaStage);
+        } else {
+          DmaRowOp na;
+          na.init(W + (long)(v0 + kTile) * D, D, vlim - v0 - kTile);
+          na.issue(0, lds);
+          na.issue(1, lds + kDmaStage);
+        }
+      }
+      ob.issue(0, lds + 32768);
+      ob.issue(1, lds + kDmaStage + 32768);
+    };
+    f32x16 acc[4][kNJ];
+    gemm_dma<kGStores>(oa, ob, nk, lds, acc, pre, has_next, next);
+    if constexpr (!Q4) {
+      if (has_next) {
+        if (next_whole) oa.base += tile_bytes;
+        else init_a(v0 + kTile);
+      }
+    }
+    pre = has_next;
+
+    // G = bf16((exp(z - lse) - onehot) * coef), zero in columns past the chunk's last vocab row.
+    // Tile column of acc[i][j][4q + u] is colb + 32 i + 8 q + u.
+    const int tl = v0 - v_begin;
+    const int lim = vlim - v0 - colb;
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+      const int yd = yrel[j] - tl - colb;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float gv[4];
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int idx = 32 * i + 8 * q + u;
+            // Branch-free: the columns past the chunk multiply a finite p (their head rows are
+            // clamped copies of a valid row) by zero.
+            const float p = fast_exp2(acc[i][j][4 * q + u] * kLog2e - l2[j]) - (idx == yd ? 1.f : 0.f);
+            gv[u] = p * (idx < lim ? coef[j] : 0.f);
+          }
+          const u32x2 val = u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
+          __builtin_amdgcn_raw_buffer_store_b64(val, gr, gvo[j] + 64 * i + 16 * q, 2 * tl, 0);
+        }
     }
   }
 }
@@ -1247,15 +1336,19 @@ hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt,
 // round and measured ~2% faster than one at the flagship shape).
 constexpr long kFwdWaves = 2;
 
-int lce_fwd_nsplit(long N, long V) {
+// Vocab splits for a persistent launch over N rows and V vocab columns: enough workgroups for
+// `per_cu` per compute unit, in a multiple of 8 when that many so every XCD residue holds a split.
+static int lce_nsplit(long N, long V, int per_cu) {
   const long rtiles = (N + kTile - 1) / kTile;
   const long vtiles = (V + kTile - 1) / kTile;
-  long ns = (kFwdWaves * kNumCU + rtiles - 1) / rtiles;  // aim for kFwdWaves workgroups per CU
-  if (ns >= 8) ns = (ns + 7) / 8 * 8;        // one vocab split per XCD residue
+  long ns = ((long)per_cu * kNumCU + rtiles - 1) / rtiles;
+  if (ns >= 8) ns = (ns + 7) / 8 * 8;
   if (ns > vtiles) ns = vtiles;
   if (ns < 1) ns = 1;
   return (int)ns;
 }
+
+int lce_fwd_nsplit(long N, long V) { return lce_nsplit(N, V, kFwdWaves); }
 
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,
@@ -1296,13 +1389,21 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     const int vb = c * chunk;
     const int ve = (vb + chunk < V) ? vb + chunk : V;
     const int ctiles = (ve - vb + kTile - 1) / kTile;
-    dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
-    if (h.q4) {
-      hipLaunchKernelGGL(lce_bwd_g_kernel<1>, ggrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll,
-                         ignore_index, N, D, V, vb, ve, ctiles, ldg, Gbuf);
+    if (D % kBK == 0) {
+      // One resident workgroup per CU (the stages take 128 KiB of LDS, 144 KiB for the 4-bit head).
+      const int ns = lce_nsplit(N, (long)ctiles * kTile, 1);
+      dim3 pgrid(rtiles * ns);
+      if (h.q4) {
+        hipLaunchKernelGGL(lce_bwd_g_persist_kernel<1>, pgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, Gbuf);
+      } else {
+        hipLaunchKernelGGL(lce_bwd_g_persist_kernel<0>, pgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, Gbuf);
+      }
     } else {
-      hipLaunchKernelGGL(lce_bwd_g_kernel<0>, ggrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll,
-                         ignore_index, N, D, V, vb, ve, ctiles, ldg, Gbuf);
+      dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
+      hipLaunchKernelGGL(lce_bwd_g_kernel, ggrid, block, 0, stream, H, h.w, targets, lse, dnll, ignore_index, N, D, V,
+                         vb, ve, ctiles, ldg, Gbuf);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

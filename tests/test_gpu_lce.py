@@ -38,8 +38,9 @@ def _cotangent(t, seed=5):
     return torch.rand(t.shape[0], generator=g) + 0.5  # non-uniform, like the adapter's masked mean
 
 
+# n=2048 gives 8 row tiles: the XCD-grouped workgroup order of the split-vocab kernels.
 @pytest.mark.parametrize(("n", "d", "v"), [(64, 64, 1024), (65, 192, 1027), (300, 512, 5000), (257, 128, 300),
-                                           (1024, 512, 32000)])
+                                           (1024, 512, 32000), (2048, 256, 32000), (130, 200, 3000)])
 def test_forward_parity_dense(n, d, v):
     print(f"[lce fwd dense] n={n} d={d} v={v}", flush=True)
     h, w, t = lce_inputs(n, d, v, seed=n + d + v)
@@ -56,7 +57,8 @@ def test_forward_parity_dense(n, d, v):
 
 @pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (65, 192, 1027, 256),
                                                     (300, 512, 5000, 1024), (257, 128, 300, 256),
-                                                    (1024, 512, 32000, None), (512, 256, 9000, 2048)])
+                                                    (1024, 512, 32000, None), (512, 256, 9000, 2048),
+                                                    (2048, 256, 32000, 8192), (130, 200, 3000, 1024)])
 def test_backward_parity_dense(n, d, v, chunk):
     print(f"[lce bwd dense] n={n} d={d} v={v} chunk={chunk}", flush=True)
     h, w, t = lce_inputs(n, d, v, seed=n * 7 + v)
@@ -72,7 +74,7 @@ def test_backward_parity_dense(n, d, v, chunk):
 
 
 @pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (65, 192, 1027, 256),
-                                                    (300, 512, 5000, 1024)])
+                                                    (300, 512, 5000, 1024), (2048, 128, 9000, 4096)])
 def test_quantized_parity(n, d, v, chunk):
     print(f"[lce q4] n={n} d={d} v={v} chunk={chunk}", flush=True)
     h, w, t = lce_inputs(n, d, v, seed=13 + n, w_std=0.05)
@@ -131,7 +133,9 @@ def test_golden_fixtures():
     assert rel_l2(hd.grad.cpu(), q["d_hidden"]) <= 1e-2
 
 
-@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (300, 256, 3000, 1024), (512, 512, 5000, None)])
+# d=200 (not a multiple of 64) runs the register-staged fallback kernels.
+@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (300, 256, 3000, 1024), (512, 512, 5000, None),
+                                                    (130, 200, 1500, None)])
 def test_trainable_head_dw_parity(n, d, v, chunk):
     from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
 
