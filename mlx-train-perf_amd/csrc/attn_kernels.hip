@@ -717,12 +717,24 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 // past S read as zeros) into 256 B rows whose 16-byte chunks are XOR-swizzled by
 // sw(r) = 4 (r & 3) + ((r >> 2) & 3): a bijection over any 16 consecutive rows (row fragments, 16
 // lanes per LDS cycle) that also sends the aligned 4-chunk block of each of 4 consecutive rows to a
-// different quarter of the banks (transposed fragments, 32 lanes x 8 bytes per LDS cycle). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128;
-// the transposed operands of dV += dO^T P and dK += Q^T dS are ds_read_b64_tr_b16 of the same
-// tiles. The two reads of a transposed fragment start at query rows 4 hf and 4 hf + 8 of each
-// 16-row slab, which is the order of the probability / dS registers (MFMA accumulator rows), so
-// no permuted copy of the tiles is kept. Waits and the barrier are explicit: one barrier per
-// tile, the copies of the next tile stay in flight during the current one.
+// different quarter of the banks (transposed fragments, 32 lanes x 8 bytes per LDS cycle). Row
+// fragments (S = Q K^T, dP = dO V^T) are ds_read_b128; the transposed operands of dV += dO^T P and
+// dK += Q^T dS are ds_read_b64_tr_b16 of the same tiles. The two reads of a transposed fragment
+// start at query rows 4 hf and 4 hf + 8 of each 16-row slab, which is the order of the
+// probability / dS registers (MFMA accumulator rows), so no permuted copy of the tiles is kept.
+//
+// One wave per SIMD, so the wave overlaps its own phases. A 64-query tile is two 32-query halves,
+// software-pipelined as
+//   P1: S, dP of half 0                     | row fragments of half 1, per-query scalars
+//   P2: S, dP of half 1                     | probabilities and dS of half 0, its transposed reads
+//   P3: dV, dK of half 0                    | probabilities and dS of half 1, its transposed reads
+//   (one barrier: the next tile's copies have landed, this tile's buffer is free)
+//   P4: dV, dK of half 1                    | row fragments of half 0 of the next tile
+// so the MFMA pipe always has independent work beside the VALU and LDS traffic. Masking is
+// branch-free (two compares against per-lane thresholds, plus the segment compare in packed
+// mode), keeping every MFMA of a tile in one basic block. Waits are compiler-visible builtins
+// (an inline-asm wait is opaque to the compiler's own wait insertion, which then keeps older
+// loads outstanding and waits for the in-flight copies of the next tile too).
 // ------------------------------------------------------------------------------------------
 namespace dkv128 {
 constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
@@ -730,6 +742,8 @@ constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
 constexpr int kScal = 3 * 256;             // lse*log2e, D, segment id of the 64 queries
 constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // vmcnt(0)
+__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
 }  // namespace dkv128
 
 template <bool PACKED>
@@ -759,7 +773,6 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   const int kw0 = k0 + 32 * w;
   const int kj = kw0 + col;
   const bool kvalid = kj < S;
-  const bool wave_has = kw0 < S;
 
   const long krow = (long)(bidx * Hkv + kvh) * S;
   const bf16_t* kh = k + krow * DH;
@@ -801,7 +814,9 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
     coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
   }
   // Row-fragment lane offsets (per k16 step ks): row = 32 qb + col, chunk 2 ks + hf.
-  const int sw_r = sw(col & 15);
+  int ro[kDK];
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks) ro[ks] = col * kRowB + (((2 * ks + hf) ^ sw(col & 15)) << 4);
   // Transposed-fragment lane offsets: read t covers rows 4 hf + 8 t + (s >> 2) of a 16-row slab,
   // columns 32 db + 16 (g & 1) + 4 (s & 3) (g = lane >> 4, s = lane & 15).
   int tro[2][kDB];
@@ -816,30 +831,34 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
     }
   }
 
-  auto issue = [&](int it, char* st) {
-    const int hh = it / ntq, tq = it % ntq;
+  // Copies of tile `it` into stage `st`; a copy that is not `live` gets a zero-byte range (no
+  // memory access) so the call needs no branch.
+  auto issue = [&](int it, char* st, bool live) {
+    const int itc = live ? it : 0;
+    const int hh = itc / ntq, tq = itc % ntq;
     const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
     const int q0 = q_begin + tq * kKT;
-    const long rows_left = (long)(S - q0);
+    const int bytes = live ? ((S - q0 < kKT) ? S - q0 : kKT) * kRowB : 0;
     const char* qb_ = reinterpret_cast<const char*>(q + (qrow + q0) * DH);
     const char* db_ = reinterpret_cast<const char*>(d_o + (qrow + q0) * DH);
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, (int)(rows_left * kRowB), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, (int)(rows_left * kRowB), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, bytes, 0x00020000);
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(st + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)(st + kTile + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
     }
   };
-  float l2_reg = 0.f, d_reg = 0.f;
-  int seg_reg = 0;
+  // Per-query scalars of a tile (wave 0): raw loads now, stored to the stage after the barrier.
+  float lse_reg = 0.f, d_reg = 0.f;
+  int seg_reg = -1;
   auto load_scal = [&](int it) {
     if (tid < kKT) {
       const int hh = it / ntq, tq = it % ntq;
       const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
       const int qq = q_begin + tq * kKT + tid;
       const bool ok = qq < S;
-      l2_reg = ok ? lse[qrow + qq] * kLog2e : 0.f;
+      lse_reg = ok ? lse[qrow + qq] : 0.f;
       d_reg = ok ? dvec[qrow + qq] : 0.f;
       if (PACKED) seg_reg = ok ? sid[qq] : -1;
     }
@@ -847,108 +866,144 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   auto store_scal = [&](char* st) {
     if (tid < kKT) {
       float* sc = reinterpret_cast<float*>(st + 2 * kTile);
-      sc[tid] = l2_reg;
+      sc[tid] = lse_reg * kLog2e;
       sc[64 + tid] = d_reg;
       reinterpret_cast<int*>(sc + 128)[tid] = seg_reg;
     }
   };
 
-  if (niter > 0) {
-    issue(0, lds);
+  if (niter <= 0) {
+    // No visible query: dK = dV = 0.
+  } else {
+    issue(0, lds, true);
     load_scal(0);
-    store_scal(lds);  // waits for its own loads
-    if (niter > 1) {
-      issue(1, lds + kStage);
-      load_scal(1);
-    }
+    store_scal(lds);
+    issue(1, lds + kStage, niter > 1);
+    if (niter > 1) load_scal(1);
+    vm_wait0();
+    if (niter > 1) store_scal(lds + kStage);
+    lgkm_wait0();
+    asm volatile("s_barrier" ::: "memory");
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  if (niter > 1) store_scal(lds + kStage);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  asm volatile("s_barrier" ::: "memory");
+  // The kernel-start K/V fragment loads are complete here (vmcnt(0) above): tell the compiler.
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(kf[ks]), "+v"(vf[ks]));
 
+  // Row fragments of half qb of the tile at `st`.
+  bf16x8 rqf[kDK], rdf[kDK];
+  auto read_rows = [&](const char* st, int qb, bf16x8 (&fq)[kDK], bf16x8 (&fd)[kDK]) {
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks) {
+      fq[ks] = as_bf16x8(lds_read16(st, 32 * qb * kRowB + ro[ks]));
+      fd[ks] = as_bf16x8(lds_read16(st + kTile, 32 * qb * kRowB + ro[ks]));
+    }
+  };
+  auto sdp = [&](const bf16x8 (&fq)[kDK], const bf16x8 (&fd)[kDK], f32x16& sacc, f32x16& pacc) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sacc[r] = 0.f;
+      pacc[r] = 0.f;
+    }
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks) {
+      sacc = mfma32(fq[ks], kf[ks], sacc);
+      pacc = mfma32(fd[ks], vf[ks], pacc);
+    }
+  };
+  // Transposed fragments of half qb: [kk][db] for dO^T (x) and Q^T (y).
+  auto read_tr = [&](const char* st, int qb, bf16x8 (&x)[2][kDB], bf16x8 (&y)[2][kDB]) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const int slab = (32 * qb + 16 * kk) * kRowB;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+        const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + kTile + slab + tro[0][db]));
+        const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + kTile + slab + tro[1][db]));
+        const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + slab + tro[0][db]));
+        const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + slab + tro[1][db]));
+        x[kk][db] = bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+        y[kk][db] = bf16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
+      }
+    }
+  };
+  auto dvdk = [&](const bf16x8 (&x)[2][kDB], const bf16x8 (&y)[2][kDB], const bf16x8 (&pf)[2], const bf16x8 (&sf)[2]) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+        dva[db] = mfma32(x[kk][db], pf[kk], dva[db]);
+        dka[db] = mfma32(y[kk][db], sf[kk], dka[db]);
+      }
+  };
+
+  if (niter > 0) read_rows(lds, 0, rqf, rdf);
   for (int it = 0; it < niter; ++it) {
     char* cur = lds + (it & 1) * kStage;
+    char* nxt = lds + ((it + 1) & 1) * kStage;
     const int q0 = q_begin + (it % ntq) * kKT;
     const bool more2 = it + 2 < niter;
     if (more2) load_scal(it + 2);
-    bool skip = !wave_has || (q0 + kKT - 1 < kw0);
-    if (PACKED && !skip) skip = sst[q0] > kw0 + 31;
-    if (!skip) {
-      const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
-      const float* ds_ = l2s + 64;
-      const int* segs = reinterpret_cast<const int*>(l2s + 128);
-      const char* qt = cur;
-      const char* dt = cur + kTile;
-      // Per 32-query half: S and dP (MFMA), probabilities and dS (VALU), dV and dK (MFMA). The
-      // body is branch-free; tiles away from the diagonal and the tail skip the element masks.
-      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || PACKED;
-      auto half = [&](int qb, bool masked) {
-        f32x16 sacc, pacc;
+    // Query row 32 qb + 8 rq + 4 hf + u of the tile is visible to this lane's key iff
+    // c = 32 qb + 8 rq + u satisfies thr <= c < lim (and, packed, the segments match).
+    const int thr = kvalid ? kj - q0 - 4 * hf : (1 << 20);
+    const int lim = S - q0 - 4 * hf;
+    const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
+    const float* ds_ = l2s + 64;
+    const int* segs = reinterpret_cast<const int*>(l2s + 128);
+    f32x4 l4[2][4], d4[2][4];
+    i32x4 s4[2][4];
+
+    auto probs = [&](int qb, const f32x16& sacc, const f32x16& pacc, bf16x8 (&pf)[2], bf16x8 (&sf)[2]) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[r] = 0.f;
-          pacc[r] = 0.f;
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int r = 4 * rq + u;
+          const int c = 32 * qb + 8 * rq + u;
+          float p = fast_exp2(sacc[r] * scale_log2 - l4[qb][rq][u]);
+          bool ok = (c >= thr) && (c < lim);
+          if (PACKED) ok = ok && (s4[qb][rq][u] == my_seg);
+          p = ok ? p : 0.f;
+          pf[r >> 3][r & 7] = (__bf16)p;
+          sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[qb][rq][u]));
         }
-        const int rb = (32 * qb + col) * kRowB;
+    };
+
+    // P1: S, dP of half 0 | row fragments of half 1, scalars.
+    f32x16 s0, p0, s1, p1;
+    bf16x8 rqf1[kDK], rdf1[kDK];
+    sdp(rqf, rdf, s0, p0);
+    read_rows(cur, 1, rqf1, rdf1);
 #pragma unroll
-        for (int ks = 0; ks < kDK; ++ks) {
-          const int o = rb + (((2 * ks + hf) ^ sw_r) << 4);
-          sacc = mfma32(as_bf16x8(lds_read16(qt, o)), kf[ks], sacc);
-          pacc = mfma32(as_bf16x8(lds_read16(dt, o)), vf[ks], pacc);
-        }
-        bf16x8 pf[2], sf[2];
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
-          i32x4 s4 = {0, 0, 0, 0};
-          if (PACKED && masked) s4 = *reinterpret_cast<const i32x4*>(segs + ql0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int r = 4 * rq + u;
-            float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
-            if (masked) {
-              const int qq = q0 + ql0 + u;
-              bool ok = (kj <= qq) && (qq < S) && kvalid;
-              if (PACKED) ok = ok && (s4[u] == my_seg);
-              p = ok ? p : 0.f;
-            }
-            pf[r >> 3][r & 7] = (__bf16)p;
-            sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[u]));
-          }
-        }
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
-          const int slab = (32 * qb + 16 * kk) * kRowB;
-#pragma unroll
-          for (int db = 0; db < kDB; ++db) {
-            const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(dt + slab + tro[0][db]));
-            const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(dt + slab + tro[1][db]));
-            const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(qt + slab + tro[0][db]));
-            const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(qt + slab + tro[1][db]));
-            dva[db] = mfma32(bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]}, pf[kk], dva[db]);
-            dka[db] = mfma32(bf16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]}, sf[kk], dka[db]);
-          }
-        }
-      };
-      if (need_mask) {
-        half(0, true);
-        half(1, true);
-      } else {
-        half(0, false);
-        half(1, false);
+      for (int rq = 0; rq < 4; ++rq) {
+        const int ql0 = 32 * qb + 8 * rq + 4 * hf;
+        l4[qb][rq] = *reinterpret_cast<const f32x4*>(l2s + ql0);
+        d4[qb][rq] = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+        if (PACKED) s4[qb][rq] = *reinterpret_cast<const i32x4*>(segs + ql0);
       }
-    }
-    // Next tile: this wave's copies of tile it+1 landed (issued one tile ago); after the barrier
-    // every wave is done with `cur`, which receives tile it+2.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    // P2: S, dP of half 1 | probabilities and dS of half 0, its transposed reads.
+    bf16x8 pf0[2], sf0[2], pf1[2], sf1[2];
+    bf16x8 x0[2][kDB], y0[2][kDB], x1[2][kDB], y1[2][kDB];
+    sdp(rqf1, rdf1, s1, p1);
+    probs(0, s0, p0, pf0, sf0);
+    read_tr(cur, 0, x0, y0);
+    // P3: dV, dK of half 0 | probabilities and dS of half 1, its transposed reads.
+    dvdk(x0, y0, pf0, sf0);
+    probs(1, s1, p1, pf1, sf1);
+    read_tr(cur, 1, x1, y1);
+    // Every read of `cur` has returned and this wave's copies of the next tile have landed;
+    // after the barrier `cur` receives the tile after next.
+    lgkm_wait0();
+    vm_wait0();
     asm volatile("s_barrier" ::: "memory");
-    if (more2) {
-      issue(it + 2, cur);
-      store_scal(cur);
-    }
+    issue(it + 2, cur, more2);
+    if (more2) store_scal(cur);
+    // P4: dV, dK of half 1 | row fragments of half 0 of the next tile (stale when there is none;
+    // never used then).
+    read_rows(nxt, 0, rqf, rdf);
+    dvdk(x1, y1, pf1, sf1);
   }
 
   if (kvalid) {
