@@ -33,6 +33,36 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 
+// Compiler-visible waits: an inline-asm s_waitcnt is opaque to the compiler's own wait insertion,
+// which then keeps earlier loads outstanding and waits for them again later (and for every copy
+// in flight with them).
+__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // vmcnt(0)
+__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
+
+__device__ __forceinline__ uint32_t lds_addr(const char* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+// ds_read_b64_tr_b16 (gfx950 LDS transpose read) of LDS byte address a + OFF, as inline asm. The
+// builtin form is treated by the compiler's wait insertion as a possible reader of every LDS DMA
+// in flight, so each tile would wait for the copies of the tile after next before its transposed
+// product; the asm form is invisible to it, and callers wait for the results (tr_wait) before use.
+template <int OFF>
+__device__ __forceinline__ u32x2 tr16_asm(uint32_t a) {
+  u32x2 r;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(r) : "v"(a), "i"(OFF));
+  return r;
+}
+__device__ __forceinline__ bf16x8 tr_pair(u32x2 lo, u32x2 hi) {
+  return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
+}
+// Waits for every LDS read issued so far and marks the 16 fragments as produced here.
+__device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(f[0][0]), "+v"(f[0][1]), "+v"(f[0][2]), "+v"(f[0][3]), "+v"(f[1][0]), "+v"(f[1][1]),
+                 "+v"(f[1][2]), "+v"(f[1][3]), "+v"(f[2][0]), "+v"(f[2][1]), "+v"(f[2][2]), "+v"(f[2][3]),
+                 "+v"(f[3][0]), "+v"(f[3][1]), "+v"(f[3][2]), "+v"(f[3][3]));
+}
+
 // The dQ kernel stages one K/V tile in LDS (51 KiB at head_dim 128) and prefetches the next into
 // registers, so two workgroups (8 waves) share a CU; MTP_DQ_BUFS=2 double-buffers instead.
 #ifndef MTP_DQ_BUFS
@@ -742,8 +772,6 @@ constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
 constexpr int kScal = 3 * 256;             // lse*log2e, D, segment id of the 64 queries
 constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
-__device__ __forceinline__ void vm_wait0() { __builtin_amdgcn_s_waitcnt(0x0F70); }    // vmcnt(0)
-__device__ __forceinline__ void lgkm_wait0() { __builtin_amdgcn_s_waitcnt(0xC07F); }  // lgkmcnt(0)
 }  // namespace dkv128
 
 template <bool PACKED>
@@ -1076,12 +1104,29 @@ struct Lanes {
   __device__ __forceinline__ bf16x8 row_frag(const char* tile, int row, int ks, int hf) const {
     return as_bf16x8(lds_read16(tile, row * kRowB + (((2 * ks + hf) ^ sw_r) << 4)));
   }
-  // Transposed fragment: head_dim block db (32 columns), contraction over tile rows of the 16-row
-  // slab starting at `slab`, in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11).
-  __device__ __forceinline__ bf16x8 t_frag(const char* tile, int slab, int db) const {
-    const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + slab * kRowB + tro[0][db]));
-    const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(tile + slab * kRowB + tro[1][db]));
-    return bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
+  // Transposed fragments f[ks][db] of the whole tile: head_dim block db (32 columns), contraction
+  // over the 16-row slab 16 ks, in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11). Asm reads:
+  // tr_wait(f) before use.
+  __device__ __forceinline__ void t_frags(const char* tile, bf16x8 (&f)[4][4]) const {
+    const uint32_t b = lds_addr(tile);
+    uint32_t a0[4], a1[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      a0[db] = b + tro[0][db];
+      a1[db] = b + tro[1][db];
+    }
+    t_slab<0>(a0, a1, f);
+    t_slab<1>(a0, a1, f);
+    t_slab<2>(a0, a1, f);
+    t_slab<3>(a0, a1, f);
+  }
+  template <int KS>
+  __device__ __forceinline__ static void t_slab(const uint32_t (&a0)[4], const uint32_t (&a1)[4], bf16x8 (&f)[4][4]) {
+    constexpr int off = KS * 16 * kRowB;
+    f[KS][0] = tr_pair(tr16_asm<off>(a0[0]), tr16_asm<off>(a1[0]));
+    f[KS][1] = tr_pair(tr16_asm<off>(a0[1]), tr16_asm<off>(a1[1]));
+    f[KS][2] = tr_pair(tr16_asm<off>(a0[2]), tr16_asm<off>(a1[2]));
+    f[KS][3] = tr_pair(tr16_asm<off>(a0[3]), tr16_asm<off>(a1[3]));
   }
 };
 }  // namespace kv128
@@ -1175,13 +1220,21 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 
   if (ntiles > 0) {
     issue(0, lds);
+    vm_wait0();
     store_seg(lds);
     if (ntiles > 1) issue(1, lds + kStage);
   }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  vm_wait0();
   if (ntiles > 1) store_seg(lds + kStage);
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  lgkm_wait0();
   asm volatile("s_barrier" ::: "memory");
+  // The kernel-start Q (and dO) fragment loads are complete here: tell the compiler.
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(qf[ks]));
+  if constexpr (DQ) {
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(df[ks]));
+  }
 
   for (int t = 0; t < ntiles; ++t) {
     const char* cur = lds + (t & 1) * kStage;
@@ -1190,23 +1243,52 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     if (!skip) {
       const char* kt = cur;
       const char* vt = cur + kTile;
+      // S^T = K Q^T (and dP^T = V dO^T): row fragments two k16 steps ahead, the two 32-key
+      // accumulator chains interleaved.
       f32x16 sacc[2], pacc[DQ ? 2 : 1];
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-        if constexpr (DQ) {
-#pragma unroll
-          for (int r = 0; r < 16; ++r) pacc[kb][r] = 0.f;
+        for (int r = 0; r < 16; ++r) {
+          sacc[kb][r] = 0.f;
+          if constexpr (DQ) pacc[kb][r] = 0.f;
         }
+      // Read-ahead distance in k16 steps (the dQ pass holds twice the fragments per step).
+      constexpr int RA = DQ ? 1 : 2;
+      bf16x8 rk[RA + 1][2], rv[DQ ? RA + 1 : 1][2];
+      auto rd = [&](int ks) {
 #pragma unroll
-        for (int ks = 0; ks < kDK; ++ks) {
-          sacc[kb] = mfma32(ln.row_frag(kt, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
-          if constexpr (DQ) pacc[kb] = mfma32(ln.row_frag(vt, 32 * kb + col, ks, hf), df[ks], pacc[kb]);
+        for (int kb = 0; kb < 2; ++kb) {
+          rk[ks % (RA + 1)][kb] = ln.row_frag(kt, 32 * kb + col, ks, hf);
+          if constexpr (DQ) rv[ks % (RA + 1)][kb] = ln.row_frag(vt, 32 * kb + col, ks, hf);
+        }
+      };
+#pragma unroll
+      for (int ks = 0; ks < RA; ++ks) rd(ks);
+#pragma unroll
+      for (int ks = 0; ks < kDK; ++ks) {
+        if (ks + RA < kDK) rd(ks + RA);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          sacc[kb] = mfma32(rk[ks % (RA + 1)][kb], qf[ks], sacc[kb]);
+          if constexpr (DQ) pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
         }
       }
+      // Transposed fragments of the second product's tile: in flight during the softmax (forward);
+      // the dQ pass issues them after dS, when the score registers are free.
+      bf16x8 tf[4][4];
+      if constexpr (!DQ) ln.t_frags(vt, tf);
+      // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
+      // c <= thr (causal and tail bounds), and, packed, the segments match.
       const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int thr = qvalid ? ((qi < S - 1 ? qi : S - 1) - kv0 - 4 * hf) : -1;
       const int* segs = reinterpret_cast<const int*>(cur + 2 * kTile);
+      auto visible = [&](int kb, int r) {
+        const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+        bool ok = c <= thr;
+        if (PACKED) ok = ok && (segs[c + 4 * hf] == my_seg);
+        return ok;
+      };
       bf16x8 pf[4];
       if constexpr (DQ) {
 #pragma unroll
@@ -1214,12 +1296,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             float p = fast_exp2(sacc[kb][r] * scale_log2 - l2q);
-            if (need_mask) {
-              const int j = kv0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-              bool ok = (j <= qi) && (j < S) && qvalid;
-              if (PACKED) ok = ok && (segs[j - kv0] == my_seg);
-              if (!ok) p = 0.f;
-            }
+            if (need_mask) p = visible(kb, r) ? p : 0.f;
             pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
           }
       } else {
@@ -1229,12 +1306,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
             float x = sacc[kb][r] * scale_log2;
-            if (need_mask) {
-              const int j = kv0 + 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-              bool ok = (j <= qi) && (j < S) && qvalid;
-              if (PACKED) ok = ok && (segs[j - kv0] == my_seg);
-              if (!ok) x = kNegInf;
-            }
+            if (need_mask) x = visible(kb, r) ? x : kNegInf;
             sacc[kb][r] = x;
             mt = fmaxf(mt, x);
           }
@@ -1260,14 +1332,16 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         l += ls;
       }
       // O^T += V^T P^T (forward) or dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
-      const char* at = DQ ? kt : vt;
+      if constexpr (DQ) ln.t_frags(kt, tf);
+      tr_wait(tf);
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(ln.t_frag(at, 16 * ks, db), pf[ks], acc[db]);
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
     }
     // This wave's copies of tile t+1 landed; after the barrier nobody reads `cur`, which takes t+2.
-    asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+    vm_wait0();
+    lgkm_wait0();
     asm volatile("s_barrier" ::: "memory");
     if (t + 2 < ntiles) {
       issue(t + 2, const_cast<char*>(cur));
