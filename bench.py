@@ -313,7 +313,7 @@ def pmc_summary(fetch_dir: str, write_dir: str, command: str) -> str:
     f_fetch, f_write = PMC_COPY_BYTES / (cf * 1024.0), PMC_COPY_BYTES / (cw * 1024.0)
     algorithmic = {  # bytes that must cross HBM at least once per launch
         "lce_fwd_kernel<0>": 2.0 * (V * D + N * D),
-        "attn_fwd_kernel<128, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
+        "attn_kv128_kernel<false, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
     }
     kernels = {}
     for k in sorted(fetch):
