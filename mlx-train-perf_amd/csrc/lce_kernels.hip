@@ -1332,9 +1332,9 @@ hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt,
 // ------------------------------------------------------------------------------------------
 // Host-side launchers (called from the C-ABI after validation).
 // ------------------------------------------------------------------------------------------
-// Forward workgroups per CU (they run back to back; two per CU shortens the tail of the last
-// round and measured ~2% faster than one at the flagship shape).
-constexpr long kFwdWaves = 2;
+// Forward workgroups per CU: one (a single resident round; with the XCD-grouped tile order this
+// measured ~1% faster at the flagship shape than two rounds of half the tiles each).
+constexpr long kFwdWaves = 1;
 
 // Vocab splits for a persistent launch over N rows and V vocab columns: enough workgroups for
 // `per_cu` per compute unit, in a multiple of 8 when that many so every XCD residue holds a split.

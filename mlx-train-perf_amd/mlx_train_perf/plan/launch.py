@@ -42,7 +42,7 @@ def packed_pairs(lengths: list[int]) -> int:
     return sum(causal_pairs(n) for n in lengths)
 
 
-FWD_WGS_PER_CU = 2  # forward workgroups per CU (run back to back; csrc/lce_kernels.hip)
+FWD_WGS_PER_CU = 1  # forward workgroups per CU (csrc/lce_kernels.hip)
 
 
 def lce_fwd_splits(n: int, v: int) -> int:

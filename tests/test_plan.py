@@ -37,7 +37,7 @@ def test_lce_forward_splits(n, v):
 def test_flagship_forward_workspace_under_10mb():
     p = plan.lce_plan(n=8192, v=151936, d=4096)
     assert p.fwd_workspace_bytes + 3 * 8192 * 4 < 0.01e9
-    assert p.fwd_splits == 16  # 32 row tiles x 16 splits = 2 workgroups per CU
+    assert p.fwd_splits == 8  # 32 row tiles x 8 splits = 1 workgroup per CU
 
 
 @pytest.mark.parametrize("budget", [1 << 20, 1 << 28, 1 << 30, 1 << 33])
