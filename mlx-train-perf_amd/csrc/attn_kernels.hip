@@ -22,6 +22,8 @@
 // "transposed" tiles keep head_dim rows x 64 positions in the 128-byte swizzled layout, with the
 // middle two 4-position quads of every 16-position group swapped so that one 16-byte read yields
 // the MFMA contraction slots that match the accumulator layout of the preceding product.
+#include <type_traits>
+
 #include "mtp_common.hpp"
 #include "mtp_launch.hpp"
 
@@ -32,6 +34,9 @@ typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
+// Online softmax: the running maximum (log2 domain) is raised, and O and l rescaled, only when a
+// tile's maximum exceeds it by more than this, so unnormalized probabilities stay <= 2^8.
+constexpr float kRescaleLog2 = 8.f;
 
 // Compiler-visible waits: an inline-asm s_waitcnt is opaque to the compiler's own wait insertion,
 // which then keeps earlier loads outstanding and waits for them again later (and for every copy
@@ -169,7 +174,9 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   const int kvh = h0 / G;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  // The wave index is read as a scalar so that every per-wave bound below (and the decisions built
+  // on them) is a scalar branch, not a per-lane select.
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int head = h0 + (w % hpw);
   const int qw0 = pb * P + 32 * (w / hpw);
@@ -199,8 +206,8 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
   int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
   if (PACKED) {
     my_seg = qvalid ? sid[qi] : -2;
-    w_sst_first = wave_has ? sst[qw0] : 0;
-    w_sst_last = wave_has ? sst[wq_last] : 0;
+    w_sst_first = __builtin_amdgcn_readfirstlane(wave_has ? sst[qw0] : 0);
+    w_sst_last = __builtin_amdgcn_readfirstlane(wave_has ? sst[wq_last] : 0);
   }
 
   float m = kNegInf, l = 0.f;
@@ -366,7 +373,9 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
   const int kvh = h0 / G;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  // The wave index is read as a scalar so that every per-wave bound below (and the decisions built
+  // on them) is a scalar branch, not a per-lane select.
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int head = h0 + (w % hpw);
   const int qw0 = pb * P + 32 * (w / hpw);
@@ -401,8 +410,8 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
   int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
   if (PACKED) {
     my_seg = qvalid ? sid[qi] : -2;
-    w_sst_first = wave_has ? sst[qw0] : 0;
-    w_sst_last = wave_has ? sst[wq_last] : 0;
+    w_sst_first = __builtin_amdgcn_readfirstlane(wave_has ? sst[qw0] : 0);
+    w_sst_last = __builtin_amdgcn_readfirstlane(wave_has ? sst[wq_last] : 0);
   }
 
   f32x16 acc[C::kDB];
@@ -760,18 +769,30 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 //   P3: dV, dK of half 0                    | probabilities and dS of half 1, its transposed reads
 //   (one barrier: the next tile's copies have landed, this tile's buffer is free)
 //   P4: dV, dK of half 1                    | row fragments of half 0 of the next tile
-// so the MFMA pipe always has independent work beside the VALU and LDS traffic. Masking is
-// branch-free (two compares against per-lane thresholds, plus the segment compare in packed
-// mode), keeping every MFMA of a tile in one basic block. Waits are compiler-visible builtins
-// (an inline-asm wait is opaque to the compiler's own wait insertion, which then keeps older
-// loads outstanding and waits for the in-flight copies of the next tile too).
+// so the MFMA pipe always has independent work beside the VALU and LDS traffic. Whether a tile
+// needs masking is decided per wave (scalar branches around two small blocks that set the hidden
+// scores of a half to -inf): only tiles that cross the wave's diagonal, the sequence end or (packed) the end of
+// a key's segment compare positions. Packed: with contiguous, gapless segments, query q shares key
+// k's segment and q >= k iff k <= q < seg_end(k), the first position whose seg_start exceeds k, so
+// the mask is a range test on a per-lane limit. Waits are compiler-visible builtins (an inline-asm
+// wait is opaque to the compiler's own wait insertion, which then keeps older loads outstanding and
+// waits for the in-flight copies of the next tile too).
 // ------------------------------------------------------------------------------------------
 namespace dkv128 {
 constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
 constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
-constexpr int kScal = 3 * 256;             // lse*log2e, D, segment id of the 64 queries
+constexpr int kScal = 2 * 256;             // lse*log2e and D of the 64 queries
 constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+// First index i in [lo, hi) with a[i] > x (hi if none); a is non-decreasing.
+__device__ __forceinline__ int first_above(const int32_t* a, int lo, int hi, int x) {
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (a[mid] > x) hi = mid;
+    else lo = mid + 1;
+  }
+  return lo;
+}
 }  // namespace dkv128
 
 template <bool PACKED>
@@ -784,7 +805,11 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   using namespace dkv128;
   constexpr int DH = 128;
   constexpr int kDK = DH / 16, kDB = DH / 32;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+  // The two stages are separate arrays and the tile loop is unrolled by two, so every LDS read
+  // names its stage statically: the compiler then knows the reads of one stage do not alias the
+  // copies in flight into the other, and inserts no wait for those copies before them.
+  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
 
   const int G = Hq / Hkv;
   const int nkv = B * Hkv;
@@ -796,7 +821,8 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   const int k0 = ktile * 128;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  // The wave index is read as a scalar so the per-wave masking decision is a scalar branch.
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int kw0 = k0 + 32 * w;
   const int kj = kw0 + col;
@@ -805,7 +831,6 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   const long krow = (long)(bidx * Hkv + kvh) * S;
   const bf16_t* kh = k + krow * DH;
   const bf16_t* vh = v + krow * DH;
-  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
   const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
 
   bf16x8 kf[kDK], vf[kDK];
@@ -814,13 +839,19 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
     kf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(kh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
     vf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(vh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
   }
-  const int my_seg = (PACKED && kvalid) ? sid[kj] : -3;
 
   const int q_begin = (k0 / kKT) * kKT;
   int q_end = S;
   if (PACKED) {
     const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
-    q_end = upper_bound_i32(sst, S, klast);
+    q_end = __builtin_amdgcn_readfirstlane(first_above(sst, 0, S, klast));
+  }
+  // Queries q with kj <= q < my_lim see key kj; w_lim is the wave's smallest limit (its first key's:
+  // segment ends do not decrease along the keys).
+  int my_lim = S, w_lim = S;
+  if (PACKED) {
+    my_lim = kvalid ? first_above(sst, kj, q_end, kj) : S;
+    w_lim = __builtin_amdgcn_readfirstlane(my_lim);
   }
   const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
   const int niter = G * ntq;
@@ -879,7 +910,6 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   };
   // Per-query scalars of a tile (wave 0): raw loads now, stored to the stage after the barrier.
   float lse_reg = 0.f, d_reg = 0.f;
-  int seg_reg = -1;
   auto load_scal = [&](int it) {
     if (tid < kKT) {
       const int hh = it / ntq, tq = it % ntq;
@@ -888,7 +918,6 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
       const bool ok = qq < S;
       lse_reg = ok ? lse[qrow + qq] : 0.f;
       d_reg = ok ? dvec[qrow + qq] : 0.f;
-      if (PACKED) seg_reg = ok ? sid[qq] : -1;
     }
   };
   auto store_scal = [&](char* st) {
@@ -896,20 +925,19 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
       float* sc = reinterpret_cast<float*>(st + 2 * kTile);
       sc[tid] = lse_reg * kLog2e;
       sc[64 + tid] = d_reg;
-      reinterpret_cast<int*>(sc + 128)[tid] = seg_reg;
     }
   };
 
   if (niter <= 0) {
     // No visible query: dK = dV = 0.
   } else {
-    issue(0, lds, true);
+    issue(0, lds0, true);
     load_scal(0);
-    store_scal(lds);
-    issue(1, lds + kStage, niter > 1);
+    store_scal(lds0);
+    issue(1, lds1, niter > 1);
     if (niter > 1) load_scal(1);
     vm_wait0();
-    if (niter > 1) store_scal(lds + kStage);
+    if (niter > 1) store_scal(lds1);
     lgkm_wait0();
     asm volatile("s_barrier" ::: "memory");
   }
@@ -964,74 +992,92 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
       }
   };
 
-  if (niter > 0) read_rows(lds, 0, rqf, rdf);
-  for (int it = 0; it < niter; ++it) {
-    char* cur = lds + (it & 1) * kStage;
-    char* nxt = lds + ((it + 1) & 1) * kStage;
+  if (niter > 0) read_rows(lds0, 0, rqf, rdf);
+  // Tile `it` runs on stage it & 1. An odd tile count gets one phantom tile at the end: its copy is
+  // zero bytes (Q and dO rows read as zeros) and every pair is hidden, so it adds exactly zero.
+  auto body = [&](auto stage, int it) {
+    char* cur = decltype(stage)::value ? lds1 : lds0;
+    char* nxt = decltype(stage)::value ? lds0 : lds1;
+    const bool phantom = it >= niter;
     const int q0 = q_begin + (it % ntq) * kKT;
     const bool more2 = it + 2 < niter;
     if (more2) load_scal(it + 2);
     // Query row 32 qb + 8 rq + 4 hf + u of the tile is visible to this lane's key iff
-    // c = 32 qb + 8 rq + u satisfies thr <= c < lim (and, packed, the segments match).
-    const int thr = kvalid ? kj - q0 - 4 * hf : (1 << 20);
-    const int lim = S - q0 - 4 * hf;
+    // c = 32 qb + 8 rq + u satisfies thr <= c < lim.
+    const int thr = (kvalid && !phantom) ? kj - q0 - 4 * hf : (1 << 20);
+    const int lim = my_lim - q0 - 4 * hf;
+    const bool need_mask = phantom || (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && q0 + kKT > w_lim);
     const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
     const float* ds_ = l2s + 64;
-    const int* segs = reinterpret_cast<const int*>(l2s + 128);
-    f32x4 l4[2][4], d4[2][4];
-    i32x4 s4[2][4];
 
-    auto probs = [&](int qb, const f32x16& sacc, const f32x16& pacc, bf16x8 (&pf)[2], bf16x8 (&sf)[2]) {
+    // Per-query L log2(e) and D of half qb, rows 8 rq + 4 hf + 0..3.
+    auto scal = [&](int qb, f32x4 (&l4)[4], f32x4 (&d4)[4]) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int ql0 = 32 * qb + 8 * rq + 4 * hf;
+        l4[rq] = *reinterpret_cast<const f32x4*>(l2s + ql0);
+        d4[rq] = *reinterpret_cast<const f32x4*>(ds_ + ql0);
+      }
+    };
+    // Scores of hidden pairs of half qb set to -inf, so that their probabilities are exp2(-inf) = 0.
+    auto mask = [&](int qb, f32x16& sacc) {
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int c = 32 * qb + 8 * rq + u;
+          sacc[4 * rq + u] = (c >= thr && c < lim) ? sacc[4 * rq + u] : kNegInf;
+        }
+    };
+    auto probs = [&](const f32x16& sacc, const f32x16& pacc, const f32x4 (&l4)[4], const f32x4 (&d4)[4],
+                     bf16x8 (&pf)[2], bf16x8 (&sf)[2]) {
 #pragma unroll
       for (int rq = 0; rq < 4; ++rq)
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
           const int r = 4 * rq + u;
-          const int c = 32 * qb + 8 * rq + u;
-          float p = fast_exp2(sacc[r] * scale_log2 - l4[qb][rq][u]);
-          bool ok = (c >= thr) && (c < lim);
-          if (PACKED) ok = ok && (s4[qb][rq][u] == my_seg);
-          p = ok ? p : 0.f;
+          const float p = fast_exp2(__builtin_fmaf(sacc[r], scale_log2, -l4[rq][u]));
           pf[r >> 3][r & 7] = (__bf16)p;
-          sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[qb][rq][u]));
+          sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[rq][u]));
         }
     };
 
-    // P1: S, dP of half 0 | row fragments of half 1, scalars.
+    // P1: S, dP of half 0 | row fragments of half 1, scalars of half 0.
     f32x16 s0, p0, s1, p1;
     bf16x8 rqf1[kDK], rdf1[kDK];
+    f32x4 la[4], da[4], lb[4], db4[4];
     sdp(rqf, rdf, s0, p0);
     read_rows(cur, 1, rqf1, rdf1);
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int ql0 = 32 * qb + 8 * rq + 4 * hf;
-        l4[qb][rq] = *reinterpret_cast<const f32x4*>(l2s + ql0);
-        d4[qb][rq] = *reinterpret_cast<const f32x4*>(ds_ + ql0);
-        if (PACKED) s4[qb][rq] = *reinterpret_cast<const i32x4*>(segs + ql0);
-      }
+    scal(0, la, da);
+    if (need_mask) mask(0, s0);
     // P2: S, dP of half 1 | probabilities and dS of half 0, its transposed reads.
     bf16x8 pf0[2], sf0[2], pf1[2], sf1[2];
     bf16x8 x0[2][kDB], y0[2][kDB], x1[2][kDB], y1[2][kDB];
     sdp(rqf1, rdf1, s1, p1);
-    probs(0, s0, p0, pf0, sf0);
+    probs(s0, p0, la, da, pf0, sf0);
     read_tr(cur, 0, x0, y0);
+    scal(1, lb, db4);
+    if (need_mask) mask(1, s1);
     // P3: dV, dK of half 0 | probabilities and dS of half 1, its transposed reads.
     dvdk(x0, y0, pf0, sf0);
-    probs(1, s1, p1, pf1, sf1);
+    probs(s1, p1, lb, db4, pf1, sf1);
     read_tr(cur, 1, x1, y1);
     // Every read of `cur` has returned and this wave's copies of the next tile have landed;
     // after the barrier `cur` receives the tile after next.
     lgkm_wait0();
     vm_wait0();
     asm volatile("s_barrier" ::: "memory");
-    issue(it + 2, cur, more2);
+    // Scalars first: a store after the copy into the same stage would wait for that copy.
     if (more2) store_scal(cur);
+    issue(it + 2, cur, more2);
     // P4: dV, dK of half 1 | row fragments of half 0 of the next tile (stale when there is none;
     // never used then).
     read_rows(nxt, 0, rqf, rdf);
     dvdk(x1, y1, pf1, sf1);
+  };
+  for (int it = 0; it < niter; it += 2) {
+    body(std::integral_constant<int, 0>{}, it);
+    body(std::integral_constant<int, 1>{}, it + 1);
   }
 
   if (kvalid) {
@@ -1052,6 +1098,308 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
 }
 
 // ------------------------------------------------------------------------------------------
+// Backward dK, dV for head_dim 128, operand-split: 8 waves per 128-key workgroup, two per SIMD.
+// Waves 0-3 ("P waves") own 32 keys each and hold K: S = Q K^T, P = exp2(S scale log2 e - L log2 e)
+// (hidden pairs 0), P handed to the partner wave through LDS, dV^T += dO^T P. Waves 4-7 ("dS waves")
+// own the same keys and hold V: dP = dO V^T, dS = P (dP - D) with the partner's P, dK^T += Q^T dS.
+// Each wave keeps one operand (32 registers) and one accumulator set (64), so a SIMD runs one wave
+// of each kind. The two are skewed by half a tile: between two barriers the P wave finishes tile t
+// (dV) and starts tile t+1 (S, P), the dS wave finishes tile t (dS, dK) and starts tile t+1 (dP),
+// so each has 32 products with its probability or dS arithmetic between them, and the SIMD
+// overlaps the arithmetic of one with the products of the other. Q and dO tiles are copied
+// global -> LDS exactly as in attn_bwd_dkv128_kernel (same swizzle and fragment reads) into a ring
+// of three stages, the copy of tile t+3 issued when tile t's stage is released; P goes through a
+// ring of three LDS buffers. The loop is unrolled by three so every stage is named statically.
+// ------------------------------------------------------------------------------------------
+namespace dkvab {
+constexpr int kStage = dkv128::kStage;          // Q, dO, L log2 e, D
+constexpr int kPBytes = kKT * 32 * 2;           // P of one key group (64 queries x 32 keys, bf16)
+constexpr int kPBuf = 4 * kPBytes;              // P of the workgroup's four key groups
+}  // namespace dkvab
+
+template <bool PACKED>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                               const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
+                               const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
+                               bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
+                               float scale_log2, float scale) {
+  using namespace dkv128;
+  constexpr int DH = 128;
+  constexpr int kDK = DH / 16, kDB = DH / 32;
+  __shared__ __attribute__((aligned(1024))) char st0[dkvab::kStage];
+  __shared__ __attribute__((aligned(1024))) char st1[dkvab::kStage];
+  __shared__ __attribute__((aligned(1024))) char st2[dkvab::kStage];
+  __shared__ __attribute__((aligned(1024))) char pb0[dkvab::kPBuf];
+  __shared__ __attribute__((aligned(1024))) char pb1[dkvab::kPBuf];
+  __shared__ __attribute__((aligned(1024))) char pb2[dkvab::kPBuf];
+
+  const int G = Hq / Hkv;
+  const int nkv = B * Hkv;
+  const int g = blockIdx.x;
+  const int kvi = g % nkv;
+  const int ktile = g / nkv;  // earliest keys (most work under the causal mask) first
+  const int bidx = kvi / Hkv;
+  const int kvh = kvi % Hkv;
+  const int k0 = ktile * 128;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = w & 3;             // key group: keys k0 + 32 grp .. + 31
+  const bool pwave = w < 4;          // P wave (K, dV) or dS wave (V, dK)
+  const int hf = lane >> 5, col = lane & 31;
+  const int kw0 = k0 + 32 * grp;
+  const int kj = kw0 + col;
+  const bool kvalid = kj < S;
+
+  const long krow = (long)(bidx * Hkv + kvh) * S;
+  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+
+  // This wave's operand of the first product: K (P wave) or V (dS wave) rows of its keys.
+  bf16x8 opf[kDK];
+  {
+    const bf16_t* src = (pwave ? k : v) + krow * DH;
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks)
+      opf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(src + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
+  }
+
+  const int q_begin = (k0 / kKT) * kKT;
+  int q_end = S;
+  if (PACKED) {
+    const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
+    q_end = __builtin_amdgcn_readfirstlane(first_above(sst, 0, S, klast));
+  }
+  // Queries q with kj <= q < my_lim see key kj (packed: my_lim is the end of kj's segment);
+  // w_lim is the wave's smallest limit, its first key's.
+  int my_lim = S, w_lim = S;
+  if (PACKED) {
+    my_lim = kvalid ? first_above(sst, kj, q_end, kj) : S;
+    w_lim = __builtin_amdgcn_readfirstlane(my_lim);
+  }
+  const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
+  const int niter = G * ntq;
+
+  f32x16 acc[kDB];  // dV^T (P wave) or dK^T (dS wave)
+#pragma unroll
+  for (int db = 0; db < kDB; ++db)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
+
+  // Copy lanes: wave w issues 2 x 1 KiB per tile and operand (rows 4 (8 j + w) .. +3).
+  uint32_t coff[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = 4 * (8 * j + w) + (lane >> 4);
+    coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+  }
+  int ro[kDK];
+#pragma unroll
+  for (int ks = 0; ks < kDK; ++ks) ro[ks] = col * kRowB + (((2 * ks + hf) ^ sw(col & 15)) << 4);
+  int tro[2][kDB];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
+    const int swt = sw(rl);
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const int c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      tro[t][db] = rl * kRowB + ((c ^ swt) << 4) + 8 * (lane & 1);
+    }
+  }
+  // The P wave reads Q rows and dO^T; the dS wave dO rows and Q^T.
+  const int row_src = pwave ? 0 : kTile;
+  const int tr_src = pwave ? kTile : 0;
+  const int pmine = grp * dkvab::kPBytes;
+
+  // Copies of tile `it` into stage `st` (zero bytes, no memory access, when not `live`).
+  auto issue = [&](int it, char* st, bool live) {
+    const int itc = live ? it : 0;
+    const int hh = itc / ntq, tq = itc % ntq;
+    const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
+    const int q0 = q_begin + tq * kKT;
+    const int bytes = live ? ((S - q0 < kKT) ? S - q0 : kKT) * kRowB : 0;
+    const char* qb_ = reinterpret_cast<const char*>(q + (qrow + q0) * DH);
+    const char* db_ = reinterpret_cast<const char*>(d_o + (qrow + q0) * DH);
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, bytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, bytes, 0x00020000);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(st + 1024 * (8 * j + w)), 16, coff[j], 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)(st + kTile + 1024 * (8 * j + w)), 16, coff[j], 0, 0, 0);
+    }
+  };
+  // Per-query scalars of tile `it` (wave 0): raw loads, then stored beside the tile.
+  float lse_reg = 0.f, d_reg = 0.f;
+  auto load_scal = [&](int it) {
+    if (tid < kKT) {
+      const int hh = it / ntq, tq = it % ntq;
+      const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
+      const int qq = q_begin + tq * kKT + tid;
+      const bool ok = qq < S;
+      lse_reg = ok ? lse[qrow + qq] : 0.f;
+      d_reg = ok ? dvec[qrow + qq] : 0.f;
+    }
+  };
+  auto store_scal = [&](char* st) {
+    if (tid < kKT) {
+      float* sc = reinterpret_cast<float*>(st + 2 * kTile);
+      sc[tid] = lse_reg * kLog2e;
+      sc[64 + tid] = d_reg;
+    }
+  };
+
+  // Start of tile `it` (stage `st`): the first product of both halves; the P wave then forms P
+  // (hidden pairs 0; a phantom tile past the last one is all hidden) and writes it to `pb`.
+  f32x16 a1[2];
+  auto start = [&](int it, const char* st, char* pb) {
+    {
+      bf16x8 rf[2][kDK];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int ks = 0; ks < kDK; ++ks) rf[h][ks] = as_bf16x8(lds_read16(st + row_src, 32 * h * kRowB + ro[ks]));
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a1[h][r] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < kDK; ++ks)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[h][ks], opf[ks], a1[h]);
+    }
+    if (pwave) {
+      const bool phantom = it >= niter;
+      const int q0 = q_begin + (it % ntq) * kKT;
+      // Query row 32 h + 8 rq + 4 hf + u is visible to key kj iff thr <= c < lim, c = 32 h + 8 rq + u.
+      const int thr = (kvalid && !phantom) ? kj - q0 - 4 * hf : (1 << 20);
+      const int lim = my_lim - q0 - 4 * hf;
+      const bool need_mask = phantom || (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && q0 + kKT > w_lim);
+      if (need_mask) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int c = 32 * h + 8 * (r >> 2) + (r & 3);
+            a1[h][r] = (c >= thr && c < lim) ? a1[h][r] : kNegInf;
+          }
+      }
+      const float* l2s = reinterpret_cast<const float*>(st + 2 * kTile);
+      bf16x8 pf[2][2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + 32 * h + 8 * rq + 4 * hf);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * rq + u;
+            pf[h][r >> 3][r & 7] = (__bf16)fast_exp2(__builtin_fmaf(a1[h][r], scale_log2, -l4[u]));
+          }
+        }
+      // Chunk j of every lane is one contiguous KiB of this key group's P.
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        *reinterpret_cast<u32x4*>(pb + pmine + 1024 * j + 16 * lane) = __builtin_bit_cast(u32x4, pf[j >> 1][j & 1]);
+    }
+  };
+  // Finish of tile `it` (stage `st`, P in `pb`): the second products, acc += X^T B over the tile's 64
+  // queries (X = dO for the P wave, Q for the dS wave, read transposed; B = P, or dS formed from the
+  // partner's P and this wave's dP).
+  auto finish = [&](const char* st, const char* pb) {
+    bf16x8 bo[2][2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bo[h][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(pb + pmine + 1024 * (2 * h + j) + 16 * lane));
+    if (!pwave) {
+      const float* ds_ = reinterpret_cast<const float*>(st + 2 * kTile) + 64;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + 32 * h + 8 * rq + 4 * hf);
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const int r = 4 * rq + u;
+            const float p = (float)bo[h][r >> 3][r & 7];
+            bo[h][r >> 3][r & 7] = (__bf16)(p * (a1[h][r] - d4[u]));
+          }
+        }
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        const int slab = (32 * h + 16 * kk) * kRowB;
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) {
+          const bf16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + tr_src + slab + tro[0][db]));
+          const bf16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + tr_src + slab + tro[1][db]));
+          acc[db] = mfma32(bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]}, bo[h][kk], acc[db]);
+        }
+      }
+  };
+  // Waits for this wave's LDS reads and copies, then the workgroup barrier.
+  auto sync = [&]() {
+    lgkm_wait0();
+    vm_wait0();
+    asm volatile("s_barrier" ::: "memory");
+  };
+
+  // Tiles run in groups of three (phantom tiles pad the count; they add exactly zero), tile t on
+  // stage t % 3 and P buffer t % 3.
+  const int nrun = (niter + 2) / 3 * 3;
+  if (nrun > 0) {
+    issue(0, st0, true);
+    issue(1, st1, niter > 1);
+    issue(2, st2, niter > 2);
+    load_scal(0);
+    store_scal(st0);
+    if (niter > 1) load_scal(1);
+    vm_wait0();
+    if (niter > 1) store_scal(st1);
+    if (niter > 2) load_scal(2);
+    vm_wait0();
+    if (niter > 2) store_scal(st2);
+    sync();
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(opf[ks]));
+    start(0, st0, pb0);
+    sync();
+  }
+  // Step t: finish tile t, start tile t+1, release tile t's stage to tile t+3.
+  auto step = [&](int t, char* sc, const char* pc, char* sn, char* pn) {
+    const bool more3 = t + 3 < niter;
+    if (more3) load_scal(t + 3);
+    finish(sc, pc);
+    start(t + 1, sn, pn);
+    sync();
+    if (more3) store_scal(sc);
+    issue(t + 3, sc, more3);
+  };
+  for (int t = 0; t < nrun; t += 3) {
+    step(t, st0, pb0, st1, pb1);
+    step(t + 1, st1, pb1, st2, pb2);
+    step(t + 2, st2, pb2, st0, pb0);
+  }
+
+  if (kvalid) {
+    bf16_t* o = (pwave ? dv : dk) + (krow + kj) * DH;
+    const float mul = pwave ? 1.f : scale;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        *reinterpret_cast<u32x2*>(o + d) = u32x2{pack_bf16x2(acc[db][4 * rq] * mul, acc[db][4 * rq + 1] * mul),
+                                                 pack_bf16x2(acc[db][4 * rq + 2] * mul, acc[db][4 * rq + 3] * mul)};
+      }
+  }
+}
+
+// ------------------------------------------------------------------------------------------
 // Forward and dQ for head_dim 128, DMA-fed. Same ownership and math as attn_fwd_kernel /
 // attn_bwd_dq_kernel. Each 64-key K and V tile is copied global -> LDS (rows past S read as
 // zeros) in the swizzled 256 B-row layout of the dK/dV kernel; S^T = K Q^T and dP^T = V dO^T read
@@ -1061,7 +1409,7 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
 namespace kv128 {
 constexpr int kRowB = 256;
 constexpr int kTile = kKT * kRowB;            // 16 KiB
-constexpr int kStage = 2 * kTile + 256;       // K, V, key segment ids
+constexpr int kStage = 2 * kTile;             // K, V
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
 // Per-lane constants: copy offsets (4 per operand and wave), row-fragment swizzle, transposed
@@ -1157,7 +1505,9 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   const int kvh = h0 / G;
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
+  // The wave index is read as a scalar so that every per-wave bound below (and the decisions built
+  // on them) is a scalar branch, not a per-lane select.
+  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int hf = lane >> 5, col = lane & 31;
   const int head = h0 + (w % hpw);
   const int qw0 = pb * P + 32 * (w / hpw);
@@ -1191,11 +1541,13 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
   const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
 
-  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
+  // Packed: with contiguous, gapless segments, key j shares query i's segment and j <= i iff
+  // seg_start[i] <= j <= i, so the mask is a range test on this lane's seg_start.
+  int my_sst = 0, w_sst_first = 0, w_sst_last = 0;
   if (PACKED) {
-    my_seg = qvalid ? sid[qi] : -2;
-    w_sst_first = wave_has ? sst[qw0] : 0;
-    w_sst_last = wave_has ? sst[wq_last] : 0;
+    my_sst = qvalid ? sst[qi] : S;
+    w_sst_first = __builtin_amdgcn_readfirstlane(wave_has ? sst[qw0] : 0);
+    w_sst_last = __builtin_amdgcn_readfirstlane(wave_has ? sst[wq_last] : 0);
   }
 
   float m = kNegInf, l = 0.f;
@@ -1207,25 +1559,17 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 
   Lanes ln;
   ln.init();
-  int seg_reg = 0;
   auto issue = [&](int t, char* st) {
     const int kv0 = kv_begin + t * kKT;
     ln.copy(kh + (long)kv0 * DH, S - kv0, st);
     ln.copy(vh + (long)kv0 * DH, S - kv0, st + kTile);
-    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
-  };
-  auto store_seg = [&](char* st) {
-    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + 2 * kTile)[tid] = seg_reg;
   };
 
   if (ntiles > 0) {
     issue(0, lds);
-    vm_wait0();
-    store_seg(lds);
     if (ntiles > 1) issue(1, lds + kStage);
   }
   vm_wait0();
-  if (ntiles > 1) store_seg(lds + kStage);
   lgkm_wait0();
   asm volatile("s_barrier" ::: "memory");
   // The kernel-start Q (and dO) fragment loads are complete here: tell the compiler.
@@ -1279,57 +1623,69 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
       bf16x8 tf[4][4];
       if constexpr (!DQ) ln.t_frags(vt, tf);
       // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
-      // c <= thr (causal and tail bounds), and, packed, the segments match.
+      // c <= thr (causal and tail bounds) and, packed, c >= lo (at or after the row's segment
+      // start). Only tiles that cross the wave's diagonal, the sequence end or (packed) a segment
+      // start are masked (scores of hidden keys set to -inf, so their probabilities are 0); the
+      // test is per wave, a scalar branch.
       const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
       const int thr = qvalid ? ((qi < S - 1 ? qi : S - 1) - kv0 - 4 * hf) : -1;
-      const int* segs = reinterpret_cast<const int*>(cur + 2 * kTile);
+      const int lo = my_sst - kv0 - 4 * hf;
       auto visible = [&](int kb, int r) {
         const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
         bool ok = c <= thr;
-        if (PACKED) ok = ok && (segs[c + 4 * hf] == my_seg);
+        if (PACKED) ok = ok && (c >= lo);
         return ok;
       };
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) sacc[kb][r] = visible(kb, r) ? sacc[kb][r] : kNegInf;
+      }
       bf16x8 pf[4];
       if constexpr (DQ) {
+        // dS = P (dP - D), P = exp2(scale log2(e) S - L log2(e)).
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int r = 0; r < 16; ++r) {
-            float p = fast_exp2(sacc[kb][r] * scale_log2 - l2q);
-            if (need_mask) p = visible(kb, r) ? p : 0.f;
+            const float p = fast_exp2(__builtin_fmaf(sacc[kb][r], scale_log2, -l2q));
             pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
           }
       } else {
-        float mt = kNegInf;
+        // Online softmax in the log2 domain against a reference maximum m that is raised only when
+        // some row of the wave exceeds it by more than kRescaleLog2: O and l are then rescaled
+        // together, otherwise probabilities up to 2^kRescaleLog2 accumulate against the old m.
+        // O / l and L = m + log2(l) are the same either way; most tiles skip the rescale.
+        {
+          float mx = kNegInf;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            float x = sacc[kb][r] * scale_log2;
-            if (need_mask) x = visible(kb, r) ? x : kNegInf;
-            sacc[kb][r] = x;
-            mt = fmaxf(mt, x);
+            for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, sacc[kb][r]), sacc[kb][r + 1]);
+          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          const float mt = mx * scale_log2;  // scale_log2 > 0: the max of the scaled scores
+          if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleLog2) != 0) {
+            const float mn = fmaxf(m, mt);
+            const float alpha = fast_exp2(m - ((mn == kNegInf) ? 0.f : mn));
+            m = mn;
+            l *= alpha;
+#pragma unroll
+            for (int db = 0; db < kDB; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
           }
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-        const float mn = fmaxf(m, mt);
-        const float base = (mn == kNegInf) ? 0.f : mn;
-        const float alpha = fast_exp2(m - base);
-        m = mn;
-        l *= alpha;
+          // m = -inf only while every key seen by this row is masked; then p = exp2(-inf) = 0.
+          const float nb = (m == kNegInf) ? 0.f : -m;
 #pragma unroll
-        for (int db = 0; db < kDB; ++db)
+          for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-        float ls = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = fast_exp2(sacc[kb][r] - base);
-            ls += p;
-            pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
-          }
-        l += ls;
+            for (int r = 0; r < 16; ++r) {
+              const float p = fast_exp2(__builtin_fmaf(sacc[kb][r], scale_log2, nb));
+              l += p;
+              pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
+            }
+        }
       }
       // O^T += V^T P^T (forward) or dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
       if constexpr (DQ) ln.t_frags(kt, tf);
@@ -1343,10 +1699,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     vm_wait0();
     lgkm_wait0();
     asm volatile("s_barrier" ::: "memory");
-    if (t + 2 < ntiles) {
-      issue(t + 2, const_cast<char*>(cur));
-      store_seg(const_cast<char*>(cur));
-    }
+    if (t + 2 < ntiles) issue(t + 2, const_cast<char*>(cur));
   }
 
   float mul = scale, lt = 0.f;
@@ -1374,6 +1727,15 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 // Launchers
 // ------------------------------------------------------------------------------------------
 namespace {
+// dK/dV at head_dim 128: the operand-split kernel (8 waves) unless MTP_DKV_SPLIT=0.
+bool dkv_split() {
+  static const bool on = [] {
+    const char* e = getenv("MTP_DKV_SPLIT");
+    return !(e && e[0] == '0');
+  }();
+  return on;
+}
+
 int fwd_grid(const AttnShape& sh) {
   const int G = sh.hq / sh.hkv;
   const int hpw = (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1);
@@ -1418,6 +1780,11 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   if (e != hipSuccess) return e;
   dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
   if constexpr (DH == 128) {
+    if (dkv_split()) {
+      if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+      else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+      return hipGetLastError();
+    }
     if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_kernel<true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
     else hipLaunchKernelGGL((attn_bwd_dkv128_kernel<false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
     return hipGetLastError();

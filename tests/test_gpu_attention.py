@@ -68,6 +68,21 @@ def test_causal_parity(shape):
     _check(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
 
 
+@pytest.mark.parametrize("shape", [(1, 8, 2, 1100, 128), (1, 4, 1, 130, 96), (1, 4, 2, 257, 64)])
+def test_causal_parity_rising_maxima(shape):
+    """Scores with a large spread whose row maxima keep rising along the keys, so the online
+    softmax's running maximum is raised (and O, l rescaled) on many tiles, not only the first."""
+    b, hq, hkv, s, d = shape
+    print(f"[attn causal rising maxima] {shape}", flush=True)
+    q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=7 * s + d)
+    u = torch.ones(d) / math.sqrt(d)
+    ramp = torch.linspace(0.0, 3.0, s)[:, None] * u * math.sqrt(d)  # key j's score grows with j
+    q = (q.float() * 4.0 + 2.0 * u * math.sqrt(d)).to(torch.bfloat16)
+    k = (k.float() + ramp).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+    _check(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
+
+
 @pytest.mark.parametrize(("lengths", "hq", "hkv", "d"), [
     ([3, 5, 56], 4, 2, 64),
     ([100, 37, 120], 4, 1, 128),
