@@ -1249,24 +1249,29 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     }
   };
 
-  // Start of tile `it` (stage `st`): the first product of both halves; the P wave then forms P
-  // (hidden pairs 0; a phantom tile past the last one is all hidden) and writes it to `pb`.
+  // Start of tile `it` (stage `st`): the first product of both halves into a1; the P wave then
+  // forms P (hidden pairs 0; a phantom tile past the last one is all hidden) and writes it to `pb`.
   f32x16 a1[2];
   auto start = [&](int it, const char* st, char* pb) {
     {
-      bf16x8 rf[2][kDK];
+      // Row fragments read two k16 steps ahead of their products.
+      bf16x8 rf[3][2];
+      auto rd = [&](int ks) {
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int ks = 0; ks < kDK; ++ks) rf[h][ks] = as_bf16x8(lds_read16(st + row_src, 32 * h * kRowB + ro[ks]));
+        for (int h = 0; h < 2; ++h) rf[ks % 3][h] = as_bf16x8(lds_read16(st + row_src, 32 * h * kRowB + ro[ks]));
+      };
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 16; ++r) a1[h][r] = 0.f;
+      rd(0);
+      rd(1);
 #pragma unroll
-      for (int ks = 0; ks < kDK; ++ks)
+      for (int ks = 0; ks < kDK; ++ks) {
+        if (ks + 2 < kDK) rd(ks + 2);
 #pragma unroll
-        for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[h][ks], opf[ks], a1[h]);
+        for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[ks % 3][h], opf[ks], a1[h]);
+      }
     }
     if (pwave) {
       const bool phantom = it >= niter;
@@ -1369,7 +1374,9 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     start(0, st0, pb0);
     sync();
   }
-  // Step t: finish tile t, start tile t+1, release tile t's stage to tile t+3.
+  // Step t: finish tile t (the dS wave uses its dP, still in a1), start tile t+1, then release
+  // tile t's stage to tile t+3. (Starting first, for the P wave's probabilities to overlap its own
+  // dV products, measured 6% slower.)
   auto step = [&](int t, char* sc, const char* pc, char* sn, char* pn) {
     const bool more3 = t + 3 < niter;
     if (more3) load_scal(t + 3);
