@@ -380,10 +380,10 @@ def cpu_baseline(budget_s: float = 15.0):
         return time.perf_counter() - t0
 
     run(8)  # warm-up outside the window
-    rows = 32
+    rows = 256  # a probe large enough that per-call overheads do not inflate the per-row cost
     dt = run(rows)
     # scale the sample toward the budget (the work is linear in rows), capped
-    rows = int(max(32, min(4096, rows * budget_s / max(dt, 1e-3))))
+    rows = int(max(64, min(8192, rows * budget_s / max(dt, 1e-3))))
     dt = run(rows)
     return {"value": rows / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"LCE fwd+bwd on {rows} of the {N} tokens (D={D}, V={V}), oracle/lce.py fp32, "

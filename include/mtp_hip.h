@@ -108,8 +108,12 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
  * k, v [b][hkv][s][dh], o like q, lse fp32 [b][hq][s] (natural log). GQA: query head h reads
  * kv head h / (hq / hkv) (attention/reference.py:37-39). dh in {64, 96, 128}.
  * Packed mode: seg_id and seg_start are int32 [b][s] (attention/segments.py:9-19); key j is
- * visible to query i iff seg_id[i] == seg_id[j] and j <= i (segments.py:22-29). Both NULL means
- * plain causal. causal must be 1 (the reference kernel serves causal only, api.py:109-113).
+ * visible to query i iff seg_id[i] == seg_id[j] and j <= i (segments.py:22-29). The layout
+ * contract of segments.py:9-19 applies: segment ids contiguous, ascending and gapless along each
+ * row, seg_start[i] the first position of i's segment. Under it the rule equals
+ * seg_start[i] <= j <= i, which the head_dim-128 kernels test (and all kernels use seg_start to
+ * bound their loops, as the reference does). Both NULL means plain causal. causal must be 1 (the
+ * reference kernel serves causal only, api.py:109-113).
  * ------------------------------------------------------------------------------------------- */
 
 /* Forward: o = softmax(scale * q k^T + mask) v, lse = row logsumexp of the masked scaled scores.
