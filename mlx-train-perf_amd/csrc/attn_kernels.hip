@@ -60,6 +60,12 @@ __device__ __forceinline__ u32x2 tr16_asm(uint32_t a) {
 __device__ __forceinline__ bf16x8 tr_pair(u32x2 lo, u32x2 hi) {
   return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
+// Waits until at most N LDS reads are outstanding and marks one slab's 4 fragments as produced here.
+template <int N>
+__device__ __forceinline__ void slab_wait(bf16x8 (&f)[4]) {
+  static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit field");
+  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) : "n"(N));
+}
 // Waits for every LDS read issued so far and marks the 16 fragments as produced here.
 __device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -1462,14 +1468,17 @@ struct Lanes {
   // Transposed fragments f[ks][db] of the whole tile: head_dim block db (32 columns), contraction
   // over the 16-row slab 16 ks, in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11). Asm reads:
   // tr_wait(f) before use.
-  __device__ __forceinline__ void t_frags(const char* tile, bf16x8 (&f)[4][4]) const {
+  __device__ __forceinline__ void t_addr(const char* tile, uint32_t (&a0)[4], uint32_t (&a1)[4]) const {
     const uint32_t b = lds_addr(tile);
-    uint32_t a0[4], a1[4];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       a0[db] = b + tro[0][db];
       a1[db] = b + tro[1][db];
     }
+  }
+  __device__ __forceinline__ void t_frags(const char* tile, bf16x8 (&f)[4][4]) const {
+    uint32_t a0[4], a1[4];
+    t_addr(tile, a0, a1);
     t_slab<0>(a0, a1, f);
     t_slab<1>(a0, a1, f);
     t_slab<2>(a0, a1, f);
@@ -1695,12 +1704,35 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         }
       }
       // O^T += V^T P^T (forward) or dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
-      if constexpr (DQ) ln.t_frags(kt, tf);
-      tr_wait(tf);
+      if constexpr (DQ) {
+        // The K^T fragments are read only now (the score registers are free after dS): slab by
+        // slab, each slab's products issued as soon as its reads have returned while the reads of
+        // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
+        uint32_t a0[4], a1[4];
+        ln.t_addr(kt, a0, a1);
+        Lanes::t_slab<0>(a0, a1, tf);
+        Lanes::t_slab<1>(a0, a1, tf);
+        slab_wait<8>(tf[0]);
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], pf[0], acc[db]);
+        Lanes::t_slab<2>(a0, a1, tf);
+        slab_wait<8>(tf[1]);
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], pf[1], acc[db]);
+        Lanes::t_slab<3>(a0, a1, tf);
+        slab_wait<8>(tf[2]);
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], pf[2], acc[db]);
+        slab_wait<0>(tf[3]);
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], pf[3], acc[db]);
+      } else {
+        tr_wait(tf);
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
+      }
     }
     // This wave's copies of tile t+1 landed; after the barrier nobody reads `cur`, which takes t+2.
     vm_wait0();
