@@ -38,6 +38,7 @@ constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 // tile's maximum exceeds it by more than this, so unnormalized probabilities stay <= 2^8.
 constexpr float kRescaleLog2 = 8.f;
 
+
 // Compiler-visible waits: an inline-asm s_waitcnt is opaque to the compiler's own wait insertion,
 // which then keeps earlier loads outstanding and waits for them again later (and for every copy
 // in flight with them).
@@ -1425,65 +1426,26 @@ constexpr int kTile = kKT * kRowB;            // 16 KiB
 constexpr int kStage = 2 * kTile;             // K, V
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
-// Per-lane constants: copy offsets (4 per operand and wave), row-fragment swizzle, transposed
-// fragment offsets (read t of 32-row block db, relative to a 16-row slab).
+// Per-lane constants: row-fragment swizzle and the transposed-read offsets tro[t] of read t (0, 1)
+// of head_dim block 0 within a 16-row slab (block db adds db << 6 by XOR: 4 db only touches chunk
+// bits 2-3 of the swizzled 16-byte chunk index).
 struct Lanes {
-  uint32_t coff[4];
   int sw_r;
-  int tro[2][4];
+  int tro[2];
   __device__ __forceinline__ void init() {
-    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     const int hf = lane >> 5, col = lane & 31;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int row = 4 * (4 * j + w) + (lane >> 4);
-      coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
-    }
     sw_r = sw(col & 15);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
-      const int swt = sw(rl);
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const int c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-        tro[t][db] = rl * kRowB + ((c ^ swt) << 4) + 8 * (lane & 1);
-      }
+      const int c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      tro[t] = rl * kRowB + ((c0 ^ sw(rl)) << 4) + 8 * (lane & 1);
     }
   }
-  // Copy one 64-row tile (rows from `rows_left` on read as zeros) into `dst`.
-  __device__ __forceinline__ void copy(const bf16_t* src, int rows_left, char* dst) const {
-    const int w = threadIdx.x >> 6;
-    const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<bf16_t*>(src), (short)0, rows_left > 0 ? rows_left * kRowB : 0, 0x00020000);
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)(dst + 1024 * (4 * j + w)), 16,
-                                               coff[j], 0, 0, 0);
-  }
-  // Row fragment: tile row `row` (row & 15 == col & 15), k16 step ks, lane half hf.
-  __device__ __forceinline__ bf16x8 row_frag(const char* tile, int row, int ks, int hf) const {
-    return as_bf16x8(lds_read16(tile, row * kRowB + (((2 * ks + hf) ^ sw_r) << 4)));
-  }
-  // Transposed fragments f[ks][db] of the whole tile: head_dim block db (32 columns), contraction
-  // over the 16-row slab 16 ks, in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11). Asm reads:
-  // tr_wait(f) before use.
-  __device__ __forceinline__ void t_addr(const char* tile, uint32_t (&a0)[4], uint32_t (&a1)[4]) const {
-    const uint32_t b = lds_addr(tile);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) {
-      a0[db] = b + tro[0][db];
-      a1[db] = b + tro[1][db];
-    }
-  }
-  __device__ __forceinline__ void t_frags(const char* tile, bf16x8 (&f)[4][4]) const {
-    uint32_t a0[4], a1[4];
-    t_addr(tile, a0, a1);
-    t_slab<0>(a0, a1, f);
-    t_slab<1>(a0, a1, f);
-    t_slab<2>(a0, a1, f);
-    t_slab<3>(a0, a1, f);
-  }
+  // Transposed fragments f[KS][db] of slab KS (tile rows 16 KS..): head_dim block db (32 columns),
+  // in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11), from the LDS addresses a0/a1[db] of
+  // reads 0 and 1. Asm reads: slab_wait before use.
   template <int KS>
   __device__ __forceinline__ static void t_slab(const uint32_t (&a0)[4], const uint32_t (&a1)[4], bf16x8 (&f)[4][4]) {
     constexpr int off = KS * 16 * kRowB;
@@ -1495,6 +1457,24 @@ struct Lanes {
 };
 }  // namespace kv128
 
+// max(x of lane l, x of lane l ^ 32): the two lane halves hold the two key halves of one query
+// column. v_permlane32_swap exchanges the upper half of one register with the lower half of the
+// other; started from two copies of x, each register then holds one half twice. A VALU operation,
+// so unlike a ds_bpermute exchange it does not wait behind LDS reads in flight. The s_nops cover
+// the VALU-write / permlane-read hazard, which the compiler does not see inside inline asm.
+__device__ __forceinline__ float max_xhalf(float x) {
+  float y = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+  return fmaxf(x, y);
+}
+
+// One LDS-DMA load: 16 bytes per lane from src + voff (lanes past `bytes` read zeros) to dst, a
+// wave-uniform LDS address.
+__device__ __forceinline__ void lds_copy16(const bf16_t* src, int bytes, char* dst, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(src), (short)0, bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+
 template <bool PACKED, bool DQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
@@ -1505,11 +1485,13 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   using namespace kv128;
   constexpr int DH = 128;
   constexpr int kDK = DH / 16, kDB = DH / 32;
-  __shared__ __attribute__((aligned(1024))) char lds[2 * kStage];
+  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
+  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
 
   const int G = Hq / Hkv;
   const int hpw = heads_per_wg(G);
-  const int P = 32 * (4 / hpw);
+  constexpr int NW = 4;
+  const int P = 32 * (NW / hpw);
   const int npb = (S + P - 1) / P;
   const int hgb = Hq / hpw;
   const int nhg = B * hgb;
@@ -1575,16 +1557,37 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 
   Lanes ln;
   ln.init();
-  auto issue = [&](int t, char* st) {
+  // Row-fragment offset of rows 32 kb + col, k16 step ks: 32 kb kRowB + (kbase ^ (ks << 5)) (the
+  // chunk index 2 ks + hf is XOR-swizzled with the row's pattern and 2 ks touches chunk bits 1-3
+  // only). Transposed-read offsets: tro[t][db] = tro[t][0] ^ (db << 6) (4 db touches chunk bits 2-3
+  // only). The bases pass through an empty asm in each tile, so the XORs are recomputed at each use
+  // instead of 32 offsets per lane (two stages) being held in registers across the loop.
+  const int kbase = col * kRowB + ((hf ^ ln.sw_r) << 4);
+  const int tbase0 = ln.tro[0], tbase1 = ln.tro[1];
+  // Copies of tile t into stage st: this wave's load j (0-3 K rows, 4-7 V rows); each wave copies
+  // kLd 1 KiB pieces of each 16 KiB tile, rows 4 (NW jj + w) .. +3 of piece jj. The copies of the
+  // next tile are issued during the current one, one per k16 step of its first product: a copy
+  // load holds its wave at issue while the CU's load path (~64 B/clk) serves the other waves'
+  // copies, and issued between products that wait overlaps MFMA work. Past the last tile the loads
+  // get an empty buffer range (no memory access; zeros into a stage nobody reads), so no branch
+  // splits the product loop.
+  constexpr int kLd = 16 / NW;
+  uint32_t coff[kLd];
+#pragma unroll
+  for (int jj = 0; jj < kLd; ++jj) {
+    const int row = 4 * (NW * jj + w) + (lane >> 4);
+    coff[jj] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+  }
+  auto issue_one = [&](int t, char* st, int j) __attribute__((always_inline)) {
+    const bool ok = t < ntiles;
     const int kv0 = kv_begin + t * kKT;
-    ln.copy(kh + (long)kv0 * DH, S - kv0, st);
-    ln.copy(vh + (long)kv0 * DH, S - kv0, st + kTile);
+    const int jj = j % kLd;
+    lds_copy16((j < kLd ? kh : vh) + (ok ? (long)kv0 * DH : 0), ok ? (S - kv0) * kRowB : 0,
+               st + (j < kLd ? 0 : kTile) + 1024 * (NW * jj + w), coff[jj]);
   };
 
-  if (ntiles > 0) {
-    issue(0, lds);
-    if (ntiles > 1) issue(1, lds + kStage);
-  }
+#pragma unroll
+  for (int j = 0; j < 2 * kLd; ++j) issue_one(0, lds0, j);
   vm_wait0();
   lgkm_wait0();
   asm volatile("s_barrier" ::: "memory");
@@ -1596,48 +1599,72 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(df[ks]));
   }
 
-  for (int t = 0; t < ntiles; ++t) {
-    const char* cur = lds + (t & 1) * kStage;
+  // Tile t from stage cur; the copies of tile t+1 go to stage nxt (free since the barrier that ended
+  // tile t-1).
+  auto body = [&](int t, const char* cur, char* nxt) __attribute__((always_inline)) {
     const int kv0 = kv_begin + t * kKT;
     const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
-    if (!skip) {
-      const char* kt = cur;
-      const char* vt = cur + kTile;
-      // S^T = K Q^T (and dP^T = V dO^T): row fragments two k16 steps ahead, the two 32-key
-      // accumulator chains interleaved.
-      f32x16 sacc[2], pacc[DQ ? 2 : 1];
+    const char* kt = cur;
+    const char* vt = cur + kTile;
+    int kb_ = kbase, t0_ = tbase0, t1_ = tbase1;
+    asm volatile("" : "+v"(kb_), "+v"(t0_), "+v"(t1_));
+    auto taddr = [&](const char* tile, uint32_t (&a0)[4], uint32_t (&a1)[4]) __attribute__((always_inline)) {
+      const uint32_t b = lds_addr(tile);
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[kb][r] = 0.f;
-          if constexpr (DQ) pacc[kb][r] = 0.f;
-        }
-      // Read-ahead distance in k16 steps (the dQ pass holds twice the fragments per step).
-      constexpr int RA = DQ ? 1 : 2;
-      bf16x8 rk[RA + 1][2], rv[DQ ? RA + 1 : 1][2];
-      auto rd = [&](int ks) {
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          rk[ks % (RA + 1)][kb] = ln.row_frag(kt, 32 * kb + col, ks, hf);
-          if constexpr (DQ) rv[ks % (RA + 1)][kb] = ln.row_frag(vt, 32 * kb + col, ks, hf);
-        }
-      };
-#pragma unroll
-      for (int ks = 0; ks < RA; ++ks) rd(ks);
-#pragma unroll
-      for (int ks = 0; ks < kDK; ++ks) {
-        if (ks + RA < kDK) rd(ks + RA);
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-          sacc[kb] = mfma32(rk[ks % (RA + 1)][kb], qf[ks], sacc[kb]);
-          if constexpr (DQ) pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
-        }
+      for (int db = 0; db < kDB; ++db) {
+        a0[db] = b + (uint32_t)(t0_ ^ (db << 6));
+        a1[db] = b + (uint32_t)(t1_ ^ (db << 6));
       }
+    };
+    // S^T = K Q^T (and dP^T = V dO^T): row fragments two k16 steps ahead, the two 32-key
+    // accumulator chains interleaved.
+    f32x16 sacc[2], pacc[DQ ? 2 : 1];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sacc[kb][r] = 0.f;
+        if constexpr (DQ) pacc[kb][r] = 0.f;
+      }
+    // Read-ahead distance in k16 steps (the dQ pass holds twice the fragments per step).
+    constexpr int RA = DQ ? 1 : 2;
+    bf16x8 rk[RA + 1][2], rv[DQ ? RA + 1 : 1][2];
+    auto rd = [&](int ks) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        rk[ks % (RA + 1)][kb] = as_bf16x8(lds_read16(kt, 32 * kb * kRowB + (kb_ ^ (ks << 5))));
+        if constexpr (DQ) rv[ks % (RA + 1)][kb] = as_bf16x8(lds_read16(vt, 32 * kb * kRowB + (kb_ ^ (ks << 5))));
+      }
+    };
+#pragma unroll
+    for (int ks = 0; ks < RA; ++ks) rd(ks);
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks) {
+      if (ks + RA < kDK) rd(ks + RA);
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sacc[kb] = mfma32(rk[ks % (RA + 1)][kb], qf[ks], sacc[kb]);
+        if constexpr (DQ) pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
+      }
+      if (ks < 2 * kLd) issue_one(t + 1, nxt, ks);
+      // Keep each k16 step's reads, products and copy load together (the scheduler would
+      // otherwise bunch the copies and hoist the transposed reads into this loop).
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // The products above run for every wave, as they carry the copies; the rest only for a wave
+    // with keys of this tile to attend to (the others meet them at the barrier either way).
+    if (!skip) {
       // Transposed fragments of the second product's tile: in flight during the softmax (forward);
       // the dQ pass issues them after dS, when the score registers are free.
       bf16x8 tf[4][4];
-      if constexpr (!DQ) ln.t_frags(vt, tf);
+      if constexpr (!DQ) {
+        uint32_t a0[4], a1[4];
+        taddr(vt, a0, a1);
+        Lanes::t_slab<0>(a0, a1, tf);
+        Lanes::t_slab<1>(a0, a1, tf);
+        Lanes::t_slab<2>(a0, a1, tf);
+        Lanes::t_slab<3>(a0, a1, tf);
+      }
       // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
       // c <= thr (causal and tail bounds) and, packed, c >= lo (at or after the row's segment
       // start). Only tiles that cross the wave's diagonal, the sequence end or (packed) a segment
@@ -1679,7 +1706,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
           for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
             for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, sacc[kb][r]), sacc[kb][r + 1]);
-          mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+          mx = max_xhalf(mx);
           const float mt = mx * scale_log2;  // scale_log2 > 0: the max of the scaled scores
           if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleLog2) != 0) {
             const float mn = fmaxf(m, mt);
@@ -1709,7 +1736,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         // slab, each slab's products issued as soon as its reads have returned while the reads of
         // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
         uint32_t a0[4], a1[4];
-        ln.t_addr(kt, a0, a1);
+        taddr(kt, a0, a1);
         Lanes::t_slab<0>(a0, a1, tf);
         Lanes::t_slab<1>(a0, a1, tf);
         slab_wait<8>(tf[0]);
@@ -1738,7 +1765,10 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     vm_wait0();
     lgkm_wait0();
     asm volatile("s_barrier" ::: "memory");
-    if (t + 2 < ntiles) issue(t + 2, const_cast<char*>(cur));
+  };
+  for (int t = 0; t < ntiles; t += 2) {
+    body(t, lds0, lds1);
+    if (t + 1 < ntiles) body(t + 1, lds1, lds0);
   }
 
   float mul = scale, lt = 0.f;
