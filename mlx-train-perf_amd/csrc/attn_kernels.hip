@@ -67,6 +67,29 @@ __device__ __forceinline__ void slab_wait(bf16x8 (&f)[4]) {
   static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit field");
   asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) : "n"(N));
 }
+// max(x of lane l, x of lane l ^ 32): the two lane halves hold the two key halves of one query
+// column. v_permlane32_swap exchanges the upper half of one register with the lower half of the
+// other; started from two copies of x, each register then holds one half twice. A VALU operation,
+// so unlike a ds_bpermute exchange it does not wait behind LDS reads in flight. The s_nops cover
+// the VALU-write / permlane-read hazard, which the compiler does not see inside inline asm.
+__device__ __forceinline__ float max_xhalf(float x) {
+  float y = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+  return fmaxf(x, y);
+}
+
+// One LDS-DMA load: 16 bytes per lane from src + voff (lanes past `bytes` read zeros) to dst, a
+// wave-uniform LDS address.
+__device__ __forceinline__ void lds_copy16(const bf16_t* src, int bytes, char* dst, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(src), (short)0, bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
+}
+// The same with 4 bytes per lane (lane i writes dst + 4 i).
+__device__ __forceinline__ void lds_copy4(const float* src, int bytes, char* dst, uint32_t voff) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(src), (short)0, bytes, 0x00020000);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, 0, 0, 0);
+}
+
 // Waits for every LDS read issued so far and marks the 16 fragments as produced here.
 __device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -788,7 +811,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 namespace dkv128 {
 constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
 constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
-constexpr int kScal = 2 * 256;             // lse*log2e and D of the 64 queries
+constexpr int kScal = 2 * 256;             // L and D of the 64 queries
 constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
 __device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 // First index i in [lo, hi) with a[i] > x (hi if none); a is non-decreasing.
@@ -1219,47 +1242,35 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   const int tr_src = pwave ? kTile : 0;
   const int pmine = grp * dkvab::kPBytes;
 
-  // Copies of tile `it` into stage `st` (zero bytes, no memory access, when not `live`).
-  auto issue = [&](int it, char* st, bool live) {
+  // Copies of tile `it` into stage `st`: this wave's load j (0-1 Q rows, 2-3 dO rows); zero bytes,
+  // no memory access (zeros into a free stage), when not `live`.
+  // The per-query scalars L and D of the tile's 64 queries go beside it (waves 0 and 4, one 4-byte
+  // load each).
+  struct CopySrc {
+    const bf16_t* qs;
+    const bf16_t* ds;
+    const float* scal;
+    int bytes, sbytes;
+  };
+  auto copy_src = [&](int it, bool live) __attribute__((always_inline)) {
     const int itc = live ? it : 0;
     const int hh = itc / ntq, tq = itc % ntq;
     const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
     const int q0 = q_begin + tq * kKT;
-    const int bytes = live ? ((S - q0 < kKT) ? S - q0 : kKT) * kRowB : 0;
-    const char* qb_ = reinterpret_cast<const char*>(q + (qrow + q0) * DH);
-    const char* db_ = reinterpret_cast<const char*>(d_o + (qrow + q0) * DH);
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, bytes, 0x00020000);
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(st + 1024 * (8 * j + w)), 16, coff[j], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)(st + kTile + 1024 * (8 * j + w)), 16, coff[j], 0, 0, 0);
-    }
+    const int rows = live ? ((S - q0 < kKT) ? S - q0 : kKT) : 0;
+    return CopySrc{q + (qrow + q0) * DH, d_o + (qrow + q0) * DH, (w < 4 ? lse : dvec) + qrow + q0, rows * kRowB, rows * 4};
   };
-  // Per-query scalars of tile `it` (wave 0): raw loads, then stored beside the tile.
-  float lse_reg = 0.f, d_reg = 0.f;
-  auto load_scal = [&](int it) {
-    if (tid < kKT) {
-      const int hh = it / ntq, tq = it % ntq;
-      const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
-      const int qq = q_begin + tq * kKT + tid;
-      const bool ok = qq < S;
-      lse_reg = ok ? lse[qrow + qq] : 0.f;
-      d_reg = ok ? dvec[qrow + qq] : 0.f;
-    }
+  auto issue_one = [&](const CopySrc& c, char* st, int j) __attribute__((always_inline)) {
+    lds_copy16(j < 2 ? c.qs : c.ds, c.bytes, st + (j < 2 ? 0 : kTile) + 1024 * (8 * (j & 1) + w), coff[j & 1]);
   };
-  auto store_scal = [&](char* st) {
-    if (tid < kKT) {
-      float* sc = reinterpret_cast<float*>(st + 2 * kTile);
-      sc[tid] = lse_reg * kLog2e;
-      sc[64 + tid] = d_reg;
-    }
+  auto issue_scal = [&](const CopySrc& c, char* st) __attribute__((always_inline)) {
+    if (grp == 0) lds_copy4(c.scal, c.sbytes, st + 2 * kTile + (pwave ? 0 : 256), (uint32_t)(4 * lane));
   };
 
   // Start of tile `it` (stage `st`): the first product of both halves into a1; the P wave then
   // forms P (hidden pairs 0; a phantom tile past the last one is all hidden) and writes it to `pb`.
   f32x16 a1[2];
-  auto start = [&](int it, const char* st, char* pb) {
+  auto start = [&](int it, const char* st, char* pb, const CopySrc& cx, char* sx) __attribute__((always_inline)) {
     {
       // Row fragments read two k16 steps ahead of their products.
       bf16x8 rf[3][2];
@@ -1271,6 +1282,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 16; ++r) a1[h][r] = 0.f;
+      issue_scal(cx, sx);
       rd(0);
       rd(1);
 #pragma unroll
@@ -1278,6 +1290,10 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
         if (ks + 2 < kDK) rd(ks + 2);
 #pragma unroll
         for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[ks % 3][h], opf[ks], a1[h]);
+        // The copy loads of the tile after next, one per two k16 steps, between products that
+        // wait: a copy load holds its wave at issue while the CU's load path serves the others.
+        if (ks & 1) issue_one(cx, sx, ks >> 1);
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
     if (pwave) {
@@ -1296,17 +1312,17 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
             a1[h][r] = (c >= thr && c < lim) ? a1[h][r] : kNegInf;
           }
       }
-      const float* l2s = reinterpret_cast<const float*>(st + 2 * kTile);
+      const float* ls = reinterpret_cast<const float*>(st + 2 * kTile);
       bf16x8 pf[2][2];
 #pragma unroll
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int rq = 0; rq < 4; ++rq) {
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + 32 * h + 8 * rq + 4 * hf);
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(ls + 32 * h + 8 * rq + 4 * hf);
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int r = 4 * rq + u;
-            pf[h][r >> 3][r & 7] = (__bf16)fast_exp2(__builtin_fmaf(a1[h][r], scale_log2, -l4[u]));
+            pf[h][r >> 3][r & 7] = (__bf16)fast_exp2(__builtin_fmaf(a1[h][r], scale_log2, -l4[u] * kLog2e));
           }
         }
       // Chunk j of every lane is one contiguous KiB of this key group's P.
@@ -1362,41 +1378,35 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
 
   // Tiles run in groups of three (phantom tiles pad the count; they add exactly zero), tile t on
   // stage t % 3 and P buffer t % 3.
+  // At the start of step t, tile t+1 sits in stage (t+1) % 3 and stage (t+2) % 3 is free (tile t-1
+  // was finished in step t-1): step t copies tile t+2 into it, spread over the products of
+  // start(t+1), and the sync that ends the step waits for those copies.
   const int nrun = (niter + 2) / 3 * 3;
   if (nrun > 0) {
-    issue(0, st0, true);
-    issue(1, st1, niter > 1);
-    issue(2, st2, niter > 2);
-    load_scal(0);
-    store_scal(st0);
-    if (niter > 1) load_scal(1);
-    vm_wait0();
-    if (niter > 1) store_scal(st1);
-    if (niter > 2) load_scal(2);
-    vm_wait0();
-    if (niter > 2) store_scal(st2);
+    {
+      const CopySrc c0 = copy_src(0, true);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) issue_one(c0, st0, j);
+      issue_scal(c0, st0);
+    }
     sync();
 #pragma unroll
     for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(opf[ks]));
-    start(0, st0, pb0);
+    start(0, st0, pb0, copy_src(1, niter > 1), st1);
     sync();
   }
-  // Step t: finish tile t (the dS wave uses its dP, still in a1), start tile t+1, then release
-  // tile t's stage to tile t+3. (Starting first, for the P wave's probabilities to overlap its own
-  // dV products, measured 6% slower.)
-  auto step = [&](int t, char* sc, const char* pc, char* sn, char* pn) {
-    const bool more3 = t + 3 < niter;
-    if (more3) load_scal(t + 3);
+  // Step t: finish tile t (the dS wave uses its dP, still in a1), start tile t+1 (carrying the
+  // copies of tile t+2 into stage sx), then the barrier. (Starting first, for the P wave's
+  // probabilities to overlap its own dV products, measured 6% slower.)
+  auto step = [&](int t, const char* sc, const char* pc, const char* sn, char* pn, char* sx) __attribute__((always_inline)) {
     finish(sc, pc);
-    start(t + 1, sn, pn);
+    start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
     sync();
-    if (more3) store_scal(sc);
-    issue(t + 3, sc, more3);
   };
   for (int t = 0; t < nrun; t += 3) {
-    step(t, st0, pb0, st1, pb1);
-    step(t + 1, st1, pb1, st2, pb2);
-    step(t + 2, st2, pb2, st0, pb0);
+    step(t, st0, pb0, st1, pb1, st2);
+    step(t + 1, st1, pb1, st2, pb2, st0);
+    step(t + 2, st2, pb2, st0, pb0, st1);
   }
 
   if (kvalid) {
@@ -1456,24 +1466,6 @@ struct Lanes {
   }
 };
 }  // namespace kv128
-
-// max(x of lane l, x of lane l ^ 32): the two lane halves hold the two key halves of one query
-// column. v_permlane32_swap exchanges the upper half of one register with the lower half of the
-// other; started from two copies of x, each register then holds one half twice. A VALU operation,
-// so unlike a ds_bpermute exchange it does not wait behind LDS reads in flight. The s_nops cover
-// the VALU-write / permlane-read hazard, which the compiler does not see inside inline asm.
-__device__ __forceinline__ float max_xhalf(float x) {
-  float y = x;
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
-  return fmaxf(x, y);
-}
-
-// One LDS-DMA load: 16 bytes per lane from src + voff (lanes past `bytes` read zeros) to dst, a
-// wave-uniform LDS address.
-__device__ __forceinline__ void lds_copy16(const bf16_t* src, int bytes, char* dst, uint32_t voff) {
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<bf16_t*>(src), (short)0, bytes, 0x00020000);
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16, voff, 0, 0, 0);
-}
 
 template <bool PACKED, bool DQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
