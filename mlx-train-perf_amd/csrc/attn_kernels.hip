@@ -90,6 +90,17 @@ __device__ __forceinline__ void lds_copy4(const float* src, int bytes, char* dst
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, 0, 0, 0);
 }
 
+// Transposed fragments f[KS][db] of slab KS (rows 16 KS.. of a swizzled 256-byte-row tile): head_dim
+// block db (32 columns) in the MFMA accumulator-row order (4 hf + 0..3, 4 hf + 8..11), from the
+// LDS addresses a0/a1[db] of reads 0 and 1 (16-row slab 0). Asm reads: slab_wait before use.
+template <int KS>
+__device__ __forceinline__ void tr_slab(const uint32_t (&a0)[4], const uint32_t (&a1)[4], bf16x8 (&f)[4][4]) {
+  constexpr int off = KS * 16 * 256;
+  f[KS][0] = tr_pair(tr16_asm<off>(a0[0]), tr16_asm<off>(a1[0]));
+  f[KS][1] = tr_pair(tr16_asm<off>(a0[1]), tr16_asm<off>(a1[1]));
+  f[KS][2] = tr_pair(tr16_asm<off>(a0[2]), tr16_asm<off>(a1[2]));
+  f[KS][3] = tr_pair(tr16_asm<off>(a0[3]), tr16_asm<off>(a1[3]));
+}
 // Waits for every LDS read issued so far and marks the 16 fragments as produced here.
 __device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
   asm volatile("s_waitcnt lgkmcnt(0)"
@@ -1334,7 +1345,22 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   // Finish of tile `it` (stage `st`, P in `pb`): the second products, acc += X^T B over the tile's 64
   // queries (X = dO for the P wave, Q for the dS wave, read transposed; B = P, or dS formed from the
   // partner's P and this wave's dP).
-  auto finish = [&](const char* st, const char* pb) {
+  // The transposed reads of the first two 16-query slabs are issued first, in flight while P is read
+  // (and dS formed); each slab's products wait for its reads (lgkmcnt counts LDS reads in issue
+  // order) while the slab after next is read.
+  auto finish = [&](const char* st, const char* pb) __attribute__((always_inline)) {
+    uint32_t ta0[4], ta1[4];
+    {
+      const uint32_t b = lds_addr(st + tr_src);
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) {
+        ta0[db] = b + tro[0][db];
+        ta1[db] = b + tro[1][db];
+      }
+    }
+    bf16x8 tf[4][4];
+    tr_slab<0>(ta0, ta1, tf);
+    tr_slab<1>(ta0, ta1, tf);
     bf16x8 bo[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -1342,6 +1368,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       for (int j = 0; j < 2; ++j)
         bo[h][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(pb + pmine + 1024 * (2 * h + j) + 16 * lane));
     if (!pwave) {
+      // dS = P (dP - D).
       const float* ds_ = reinterpret_cast<const float*>(st + 2 * kTile) + 64;
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -1351,23 +1378,24 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
 #pragma unroll
           for (int u = 0; u < 4; ++u) {
             const int r = 4 * rq + u;
-            const float p = (float)bo[h][r >> 3][r & 7];
-            bo[h][r >> 3][r & 7] = (__bf16)(p * (a1[h][r] - d4[u]));
+            bo[h][r >> 3][r & 7] = (__bf16)((float)bo[h][r >> 3][r & 7] * (a1[h][r] - d4[u]));
           }
         }
     }
+    slab_wait<8>(tf[0]);
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], bo[0][0], acc[db]);
+    tr_slab<2>(ta0, ta1, tf);
+    slab_wait<8>(tf[1]);
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int slab = (32 * h + 16 * kk) * kRowB;
+    for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], bo[0][1], acc[db]);
+    tr_slab<3>(ta0, ta1, tf);
+    slab_wait<8>(tf[2]);
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) {
-          const bf16x4 t0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + tr_src + slab + tro[0][db]));
-          const bf16x4 t1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + tr_src + slab + tro[1][db]));
-          acc[db] = mfma32(bf16x8{t0[0], t0[1], t0[2], t0[3], t1[0], t1[1], t1[2], t1[3]}, bo[h][kk], acc[db]);
-        }
-      }
+    for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], bo[1][0], acc[db]);
+    slab_wait<0>(tf[3]);
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], bo[1][1], acc[db]);
   };
   // Waits for this wave's LDS reads and copies, then the workgroup barrier.
   auto sync = [&]() {
@@ -1452,17 +1480,6 @@ struct Lanes {
       const int c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
       tro[t] = rl * kRowB + ((c0 ^ sw(rl)) << 4) + 8 * (lane & 1);
     }
-  }
-  // Transposed fragments f[KS][db] of slab KS (tile rows 16 KS..): head_dim block db (32 columns),
-  // in the accumulator-row order (4 hf + 0..3, 4 hf + 8..11), from the LDS addresses a0/a1[db] of
-  // reads 0 and 1. Asm reads: slab_wait before use.
-  template <int KS>
-  __device__ __forceinline__ static void t_slab(const uint32_t (&a0)[4], const uint32_t (&a1)[4], bf16x8 (&f)[4][4]) {
-    constexpr int off = KS * 16 * kRowB;
-    f[KS][0] = tr_pair(tr16_asm<off>(a0[0]), tr16_asm<off>(a1[0]));
-    f[KS][1] = tr_pair(tr16_asm<off>(a0[1]), tr16_asm<off>(a1[1]));
-    f[KS][2] = tr_pair(tr16_asm<off>(a0[2]), tr16_asm<off>(a1[2]));
-    f[KS][3] = tr_pair(tr16_asm<off>(a0[3]), tr16_asm<off>(a1[3]));
   }
 };
 }  // namespace kv128
@@ -1652,10 +1669,10 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
       if constexpr (!DQ) {
         uint32_t a0[4], a1[4];
         taddr(vt, a0, a1);
-        Lanes::t_slab<0>(a0, a1, tf);
-        Lanes::t_slab<1>(a0, a1, tf);
-        Lanes::t_slab<2>(a0, a1, tf);
-        Lanes::t_slab<3>(a0, a1, tf);
+        tr_slab<0>(a0, a1, tf);
+        tr_slab<1>(a0, a1, tf);
+        tr_slab<2>(a0, a1, tf);
+        tr_slab<3>(a0, a1, tf);
       }
       // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
       // c <= thr (causal and tail bounds) and, packed, c >= lo (at or after the row's segment
@@ -1729,16 +1746,16 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
         uint32_t a0[4], a1[4];
         taddr(kt, a0, a1);
-        Lanes::t_slab<0>(a0, a1, tf);
-        Lanes::t_slab<1>(a0, a1, tf);
+        tr_slab<0>(a0, a1, tf);
+        tr_slab<1>(a0, a1, tf);
         slab_wait<8>(tf[0]);
 #pragma unroll
         for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], pf[0], acc[db]);
-        Lanes::t_slab<2>(a0, a1, tf);
+        tr_slab<2>(a0, a1, tf);
         slab_wait<8>(tf[1]);
 #pragma unroll
         for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], pf[1], acc[db]);
-        Lanes::t_slab<3>(a0, a1, tf);
+        tr_slab<3>(a0, a1, tf);
         slab_wait<8>(tf[2]);
 #pragma unroll
         for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], pf[2], acc[db]);
