@@ -272,14 +272,17 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, c
 struct DmaRowOp {
   static constexpr int kReads = 1;
   static constexpr bool kProduce = false;  // the copies land in the stage as they are
+  static constexpr bool kPartner = true;   // issue2 available
   const char* base;    // tile row 0, k = 0
   long bytes;          // readable bytes from base (the tile's nrows rows)
+  long row32;          // bytes of 32 rows
   uint32_t voff[4];    // per-lane byte offsets of this wave's four 1 KiB copies
   int lo[4], sx[4];    // per-lane fragment row offsets and swizzle (per 32-row block)
 
   __device__ __forceinline__ void init(const bf16_t* b, int ld, int nrows) {
     base = reinterpret_cast<const char*>(b);
     bytes = 2L * nrows * ld;
+    row32 = 64L * ld;
     const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -290,6 +293,21 @@ struct DmaRowOp {
     }
   }
   __device__ __forceinline__ void issue(int kt, char* dst, bool live = true) const { issue_at(0, kt, dst, live); }
+  // Waves 0-3 only: this wave's four copies and those of wave w + 4, whose rows are 32 further on.
+  // Their swizzle differs in chunk bit 2 (swz(r + 32) = swz(r) ^ 4 for r % 64 < 32), and with ld a
+  // multiple of 64 the chunk index sits in offset bits 4-6, so their lane offsets are voff ^ 64
+  // from a descriptor 32 rows further on. Rows past the operand's end read zeros (their results
+  // are discarded like those of the clamped rows).
+  __device__ __forceinline__ void issue2(int kt, char* dst, int w, bool live = true) const {
+    const long o = kt * (2 * kBK);
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, live ? bytes - o : 0);
+    const __amdgpu_buffer_rsrc_t r2 = dma_rsrc(base + o + row32, live ? bytes - o - row32 : 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dma16(r, voff[i], dst + 1024 * (8 * i + w));
+      dma16(r2, voff[i] ^ 64u, dst + 1024 * (8 * i + w + 4));
+    }
+  }
   // Copy from the tile `shift` bytes further on with the same per-lane offsets (valid when both
   // tiles are whole, i.e. no row was clamped). A copy that is not `live` gets a zero-byte range:
   // it touches no memory and writes zeros.
@@ -325,6 +343,7 @@ struct DmaRowOp {
 struct DmaTransOp {
   static constexpr int kReads = 2;
   static constexpr bool kProduce = false;
+  static constexpr bool kPartner = false;  // issue2 is never selected (kept so that calls compile)
   const char* base;    // k = 0, column 0 of the tile
   long ldb;            // row pitch in bytes
   int kvalid;
@@ -358,6 +377,7 @@ struct DmaTransOp {
       dma16(r, (uint32_t)k * (uint32_t)ldb + cofs[i], dst + 1024 * (8 * i + w));
     }
   }
+  __device__ __forceinline__ void issue2(int kt, char* dst, int, bool live = true) const { issue(kt, dst, live); }
   template <int NB>
   __device__ __forceinline__ void setup(int first_col) {
     const int l = threadIdx.x & 63;
@@ -387,6 +407,7 @@ struct DmaTransOp {
 constexpr int kQ4Stage = 8192;
 struct DmaQ4Op : DmaRowOp {
   static constexpr bool kProduce = true;
+  static constexpr bool kPartner = false;
   const char* qbase;   // packed words of tile row 0
   long qbytes;         // readable bytes from qbase
   const bf16_t* sc;    // scales / biases of tile row 0
@@ -474,6 +495,19 @@ __device__ __forceinline__ void dma_sched() {
   }
 }
 
+// 8 MFMAs of a k-step interleaved with NV copy loads and NR LDS reads, both spread evenly.
+template <int NR, int NV, int S = 0>
+__device__ __forceinline__ void dma_sched_mix() {
+  if constexpr (S < 8) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int v = NV * (S + 1) / 8 - NV * S / 8;
+    if constexpr (v > 0) __builtin_amdgcn_sched_group_barrier(0x020, v, 0);
+    constexpr int r = NR * (S + 1) / 8 - NR * S / 8;
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    dma_sched_mix<NR, NV, S + 1>();
+  }
+}
+
 // Last k-step of a stage: its 8 MFMAs interleaved with the 8 copies of the stage after next and
 // the NR reads of the next stage's first fragments.
 template <int NR, int S = 0>
@@ -499,6 +533,8 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
                                          bool has_next, const NEXT& next) {
   constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
   const int w = threadIdx.x >> 6;
+  constexpr bool kCopiers = OA::kPartner && OB::kPartner;
+  const int wsc = __builtin_amdgcn_readfirstlane(w);
   oa.template setup<4>(128 * (w & 1));
   ob.template setup<kNJ>(64 * (w >> 1));
 #pragma unroll
@@ -531,32 +567,57 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
   bf16x8 fa[4], fb[kNJ], ga[4], gb[kNJ];
   dma_read_frags(oa, ob, lds, 0, fa, fb);
   // All stages but the last: the body is branch-free (the copies of a stage past the end are not
-  // live), so the scheduler can interleave them with the last k-step's MFMAs.
-  for (int kt = 0; kt + 1 < nk; ++kt) {
-    char* cur = lds + ((kt & 1) ? kDmaStage : 0);
-    char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
-    dma_read_frags(oa, ob, cur, 1, ga, gb);
-    dma_mfma(fa, fb, acc);
-    dma_sched<NR>();
-    dma_read_frags(oa, ob, cur, 2, fa, fb);
-    dma_mfma(ga, gb, acc);
-    dma_sched<NR>();
-    dma_read_frags(oa, ob, cur, 3, ga, gb);
-    dma_mfma(fa, fb, acc);
-    dma_sched<NR>();
-    wait_lgkmcnt0();
-    wait_vmcnt<0>();
-    if constexpr (OA::kProduce) {
-      oa.produce(kt + 1, nxt);
+  // live), so the scheduler can interleave them with the last k-step's MFMAs. With kCopiers, one
+  // wave per SIMD (waves 0-3) issues the copies of its partner wave (w + 4) as well: while it waits
+  // at a copy's issue for the CU's load path, the SIMD's other wave keeps the MFMA pipe busy (with
+  // every wave copying, both stall at once). The two roles run separate copies of the loop, so no
+  // branch sits inside it.
+  auto stages = [&](auto role) __attribute__((always_inline)) {
+    constexpr int R = decltype(role)::value;  // 0: every wave copies; 1: copier; 2: non-copier
+    for (int kt = 0; kt + 1 < nk; ++kt) {
+      char* cur = lds + ((kt & 1) ? kDmaStage : 0);
+      char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
+      dma_read_frags(oa, ob, cur, 1, ga, gb);
+      dma_mfma(fa, fb, acc);
+      dma_sched<NR>();
+      dma_read_frags(oa, ob, cur, 2, fa, fb);
+      dma_mfma(ga, gb, acc);
+      dma_sched<NR>();
+      dma_read_frags(oa, ob, cur, 3, ga, gb);
+      dma_mfma(fa, fb, acc);
+      dma_sched<NR>();
       wait_lgkmcnt0();
+      wait_vmcnt<0>();
+      if constexpr (OA::kProduce) {
+        oa.produce(kt + 1, nxt);
+        wait_lgkmcnt0();
+      }
+      raw_barrier();
+      const bool live = kt + 2 < nk;
+      if constexpr (R == 0) {
+        oa.issue(kt + 2, cur, live);
+        ob.issue(kt + 2, cur + 32768, live);
+        dma_read_frags(oa, ob, nxt, 0, fa, fb);
+        dma_mfma(ga, gb, acc);
+        dma_sched_copy<NR>();
+      } else if constexpr (R == 1) {
+        oa.issue2(kt + 2, cur, wsc, live);
+        ob.issue2(kt + 2, cur + 32768, wsc, live);
+        dma_read_frags(oa, ob, nxt, 0, fa, fb);
+        dma_mfma(ga, gb, acc);
+        dma_sched_mix<NR, 16>();
+      } else {
+        dma_read_frags(oa, ob, nxt, 0, fa, fb);
+        dma_mfma(ga, gb, acc);
+        dma_sched_mix<NR, 0>();
+      }
     }
-    raw_barrier();
-    const bool live = kt + 2 < nk;
-    oa.issue(kt + 2, cur, live);
-    ob.issue(kt + 2, cur + 32768, live);
-    dma_read_frags(oa, ob, nxt, 0, fa, fb);
-    dma_mfma(ga, gb, acc);
-    dma_sched_copy<NR>();
+  };
+  if constexpr (kCopiers) {
+    if (wsc < 4) stages(std::integral_constant<int, 1>{});
+    else stages(std::integral_constant<int, 2>{});
+  } else {
+    stages(std::integral_constant<int, 0>{});
   }
   // Last stage.
   {
