@@ -1271,8 +1271,13 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     const int rows = live ? ((S - q0 < kKT) ? S - q0 : kKT) : 0;
     return CopySrc{q + (qrow + q0) * DH, d_o + (qrow + q0) * DH, (w < 4 ? lse : dvec) + qrow + q0, rows * kRowB, rows * 4};
   };
+  // The P waves copy for their dS partners too (the dS waves are the longer role): load j (0-7) of a
+  // P wave covers Q (j < 4) or dO rows, piece (j & 1) of wave w + 4 (j & 2), whose rows lie 16 on
+  // with the same swizzle (sw(r + 16) = sw(r)).
   auto issue_one = [&](const CopySrc& c, char* st, int j) __attribute__((always_inline)) {
-    lds_copy16(j < 2 ? c.qs : c.ds, c.bytes, st + (j < 2 ? 0 : kTile) + 1024 * (8 * (j & 1) + w), coff[j & 1]);
+    const int pw = w + ((j & 2) ? 4 : 0);
+    lds_copy16(j < 4 ? c.qs : c.ds, c.bytes, st + (j < 4 ? 0 : kTile) + 1024 * (8 * (j & 1) + pw),
+               coff[j & 1] + ((j & 2) ? 16u * kRowB : 0u));
   };
   auto issue_scal = [&](const CopySrc& c, char* st) __attribute__((always_inline)) {
     if (grp == 0) lds_copy4(c.scal, c.sbytes, st + 2 * kTile + (pwave ? 0 : 256), (uint32_t)(4 * lane));
@@ -1301,9 +1306,9 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
         if (ks + 2 < kDK) rd(ks + 2);
 #pragma unroll
         for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[ks % 3][h], opf[ks], a1[h]);
-        // The copy loads of the tile after next, one per two k16 steps, between products that
-        // wait: a copy load holds its wave at issue while the CU's load path serves the others.
-        if (ks & 1) issue_one(cx, sx, ks >> 1);
+        // The copy loads of the tile after next, one per k16 step of the P waves, between products
+        // that wait: a copy load holds its wave at issue while the CU's load path serves others.
+        if (pwave) issue_one(cx, sx, ks);
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -1411,12 +1416,12 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   // start(t+1), and the sync that ends the step waits for those copies.
   const int nrun = (niter + 2) / 3 * 3;
   if (nrun > 0) {
-    {
+    if (pwave) {
       const CopySrc c0 = copy_src(0, true);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) issue_one(c0, st0, j);
-      issue_scal(c0, st0);
+      for (int j = 0; j < 8; ++j) issue_one(c0, st0, j);
     }
+    issue_scal(copy_src(0, true), st0);
     sync();
 #pragma unroll
     for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(opf[ks]));
