@@ -1275,7 +1275,10 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
 // Backward step 3 (trainable dense head only): dW[v][d] = sum_t G[t][v] H[t][d] for the vocab rows
 // of one chunk, written once in bf16 (each output tile has a single owner: no atomics). Both
 // operands are read transposed (the contraction runs over tokens, the leading index of G and H).
+// DMA: the DMA-fed core (N and D multiples of 64); otherwise the register-staged core. The two are
+// separate instantiations (in one kernel the register-staged path's pressure spilled both).
 // ------------------------------------------------------------------------------------------
+template <bool DMA>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __restrict__ H, int N, int D, int V,
                        int v_begin, int v_end, int ctiles, bf16_t* __restrict__ dW) {
@@ -1294,7 +1297,7 @@ void lce_bwd_dw_kernel(const bf16_t* __restrict__ G, int ldg, const bf16_t* __re
   const bool full = (N % kBK == 0) && (v0 + kTile <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
-  if (N % kBK == 0 && D % kBK == 0) {
+  if constexpr (DMA) {
     // The vocab tile lies inside the chunk buffer (ctiles * 256 <= ldg), so all 256 G columns
     // are readable; rows past the chunk's end are not stored below.
     DmaTransOp oa;
@@ -1486,7 +1489,10 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     if (e != hipSuccess) return e;
     if (dW != nullptr && !h.q4) {
       dim3 wgrid(8 * ctiles * ((dtiles + 7) / 8));
-      hipLaunchKernelGGL(lce_bwd_dw_kernel, wgrid, block, 0, stream, Gbuf, ldg, H, N, D, V, vb, ve, ctiles, dW);
+      if (N % kBK == 0 && D % kBK == 0)
+        hipLaunchKernelGGL(lce_bwd_dw_kernel<true>, wgrid, block, 0, stream, Gbuf, ldg, H, N, D, V, vb, ve, ctiles, dW);
+      else
+        hipLaunchKernelGGL(lce_bwd_dw_kernel<false>, wgrid, block, 0, stream, Gbuf, ldg, H, N, D, V, vb, ve, ctiles, dW);
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
