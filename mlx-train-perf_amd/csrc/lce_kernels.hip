@@ -299,9 +299,13 @@ struct DmaRowOp {
   // from a descriptor 32 rows further on. Rows past the operand's end read zeros (their results
   // are discarded like those of the clamped rows).
   __device__ __forceinline__ void issue2(int kt, char* dst, int w, bool live = true) const {
-    const long o = kt * (2 * kBK);
-    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, live ? bytes - o : 0);
-    const __amdgpu_buffer_rsrc_t r2 = dma_rsrc(base + o + row32, live ? bytes - o - row32 : 0);
+    issue2_at(0, kt, dst, w, live);
+  }
+  // issue2 from the tile `shift` bytes further on (both tiles whole).
+  __device__ __forceinline__ void issue2_at(long shift, int kt, char* dst, int w, bool live = true) const {
+    const long o = shift + kt * (2 * kBK);
+    const __amdgpu_buffer_rsrc_t r = dma_rsrc(base + o, live ? bytes - (o - shift) : 0);
+    const __amdgpu_buffer_rsrc_t r2 = dma_rsrc(base + o + row32, live ? bytes - (o - shift) - row32 : 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       dma16(r, voff[i], dst + 1024 * (8 * i + w));
@@ -711,6 +715,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
 
   const int tid = threadIdx.x;
   const int lane = tid & 63, w = tid >> 6;
+  const int wsc = __builtin_amdgcn_readfirstlane(w);  // the wave index as a scalar
   const int wa = w & 1, wb = w >> 1;
   const int lhalf = lane >> 5, lcol = lane & 31;
   const int t0 = rt * kTile;
@@ -767,18 +772,21 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       const bool has_next = vt + 1 < vt_end;
       // Both this tile and the next are whole: the next one reuses this tile's lane offsets.
       const bool next_whole = v0 + 2 * kTile <= V;
+      // Only waves 0-3 copy the next tile's first two stages (theirs and their SIMD partner's, as
+      // in the stage loop): the other waves go straight on to the epilogue's exps meanwhile.
       auto next = [&]() {
+        if (wsc >= 4) return;
         if (next_whole) {
-          oa.issue_at(tile_bytes, 0, lds);
-          if (nk > 1) oa.issue_at(tile_bytes, 1, lds + kDmaStage);
+          oa.issue2_at(tile_bytes, 0, lds, wsc);
+          if (nk > 1) oa.issue2_at(tile_bytes, 1, lds + kDmaStage, wsc);
         } else {
           DmaRowOp na;
           na.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
-          na.issue(0, lds);
-          if (nk > 1) na.issue(1, lds + kDmaStage);
+          na.issue2(0, lds, wsc);
+          if (nk > 1) na.issue2(1, lds + kDmaStage, wsc);
         }
-        ob.issue(0, lds + 32768);
-        if (nk > 1) ob.issue(1, lds + kDmaStage + 32768);
+        ob.issue2(0, lds + 32768, wsc);
+        if (nk > 1) ob.issue2(1, lds + kDmaStage + 32768, wsc);
       };
       f32x16 acc[4][kNJ];
       gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next);
@@ -1124,6 +1132,8 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
         oa.issue(0, lds);
         oa.issue(1, lds);
       } else {
+        // Every wave copies here (with only waves 0-3 copying, as in the forward, this kernel
+        // measured 0.2% slower).
         if (next_whole) {
           oa.issue_at(tile_bytes, 0, lds);
           oa.issue_at(tile_bytes, 1, lds + kDmaStage);
