@@ -728,31 +728,33 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     s[j] = 0.f;
   }
 
-  // Online (max, sum exp2) update of this lane's token columns with one 256-row vocab tile.
+  // Online (max, sum exp2) update of this lane's token columns with one 256-row vocab tile, in the
+  // log2 domain: x = logit log2(e). The maximum is taken over the raw logits (rounding a product
+  // by a positive constant is monotonic, so max(z) log2(e) is max(z log2(e))) and the scale is
+  // folded into the exponent's fma.
   auto consume = [&](f32x16 (&acc)[4][kNJ], int v0) {
     const bool tail = (v0 + kTile) > V;
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) {
-      float mx = kNegInf;
+      float mz = kNegInf;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          float x = acc[i][j][r] * kLog2e;
           if (tail) {
             const int v = v0 + 128 * wa + 32 * i + 8 * (r >> 2) + 4 * lhalf + (r & 3);
-            if (v >= V) x = kNegInf;
+            if (v >= V) acc[i][j][r] = kNegInf;
           }
-          acc[i][j][r] = x;
-          mx = fmaxf(mx, x);
+          mz = fmaxf(mz, acc[i][j][r]);
         }
+      const float mx = mz * kLog2e;
       const float mn = fmaxf(m[j], mx);
       const float base = (mn == kNegInf) ? 0.f : mn;
       float sum = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sum += fast_exp2(acc[i][j][r] - base);
+        for (int r = 0; r < 16; ++r) sum += fast_exp2(__builtin_fmaf(acc[i][j][r], kLog2e, -base));
       s[j] = s[j] * fast_exp2(m[j] - base) + sum;
       m[j] = mn;
     }
