@@ -1428,19 +1428,30 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     start(0, st0, pb0, copy_src(1, niter > 1), st1);
     sync();
   }
-  // Step t: finish tile t (the dS wave uses its dP, still in a1), start tile t+1 (carrying the
-  // copies of tile t+2 into stage sx), then the barrier. (Starting first, for the P wave's
-  // probabilities to overlap its own dV products, measured 6% slower.)
-  auto step = [&](int t, const char* sc, const char* pc, const char* sn, char* pn, char* sx) __attribute__((always_inline)) {
-    finish(sc, pc);
-    start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
-    sync();
+  // Step t: the dS wave finishes tile t (with its dP, still in a1) and then starts tile t+1; the P
+  // wave starts tile t+1 first (its S products, the copies of tile t+2 into stage sx, P into pn)
+  // and then finishes tile t (its own P of tile t comes back from LDS), so its products fall where
+  // the dS wave forms dS and runs dP. Then the barrier. The roles run separate copies of the loop.
+  auto run = [&](auto pw) __attribute__((always_inline)) {
+    constexpr bool PW = decltype(pw)::value;
+    auto step = [&](int t, const char* sc, const char* pc, const char* sn, char* pn, char* sx) __attribute__((always_inline)) {
+      if constexpr (PW) {
+        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
+        finish(sc, pc);
+      } else {
+        finish(sc, pc);
+        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
+      }
+      sync();
+    };
+    for (int t = 0; t < nrun; t += 3) {
+      step(t, st0, pb0, st1, pb1, st2);
+      step(t + 1, st1, pb1, st2, pb2, st0);
+      step(t + 2, st2, pb2, st0, pb0, st1);
+    }
   };
-  for (int t = 0; t < nrun; t += 3) {
-    step(t, st0, pb0, st1, pb1, st2);
-    step(t + 1, st1, pb1, st2, pb2, st0);
-    step(t + 2, st2, pb2, st0, pb0, st1);
-  }
+  if (pwave) run(std::true_type{});
+  else run(std::false_type{});
 
   if (kvalid) {
     bf16_t* o = (pwave ? dv : dk) + (krow + kj) * DH;
