@@ -77,6 +77,12 @@ __device__ __forceinline__ float max_xhalf(float x) {
   asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
   return fmaxf(x, y);
 }
+// x of lane l plus x of lane l ^ 32 (see max_xhalf).
+__device__ __forceinline__ float sum_xhalf(float x) {
+  float y = x;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(x), "+v"(y));
+  return x + y;
+}
 
 // One LDS-DMA load: 16 bytes per lane from src + voff (lanes past `bytes` read zeros) to dst, a
 // wave-uniform LDS address.
@@ -1503,8 +1509,8 @@ struct Lanes {
 template <bool PACKED, bool DQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                       const bf16_t* __restrict__ d_o, const float* __restrict__ lse_in,
-                       const float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
+                       const bf16_t* __restrict__ d_o, const bf16_t* __restrict__ o_in, const float* __restrict__ lse_in,
+                       float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
                        const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
                        int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
   using namespace kv128;
@@ -1545,7 +1551,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
   const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
 
-  bf16x8 qf[kDK], df[DQ ? kDK : 1];
+  bf16x8 qf[kDK], df[DQ ? kDK : 1], of[DQ ? kDK : 1];
 #pragma unroll
   for (int ks = 0; ks < kDK; ++ks)
     qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(q + (qrow + qi) * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
@@ -1555,7 +1561,9 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     for (int ks = 0; ks < kDK; ++ks)
       df[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(d_o + (qrow + qi) * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
     l2q = qvalid ? lse_in[qrow + qi] * kLog2e : 0.f;
-    dq_row = qvalid ? dvec[qrow + qi] : 0.f;
+#pragma unroll
+    for (int ks = 0; ks < kDK; ++ks)
+      of[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(o_in + (qrow + qi) * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
   }
 
   const int wg_q0 = pb * P;
@@ -1620,8 +1628,18 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 #pragma unroll
   for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(qf[ks]));
   if constexpr (DQ) {
+    // D = rowsum(dO o O) of this lane's query (each lane holds half of the dO and O rows, lane
+    // l ^ 32 the other half), written out for the dK/dV pass. The O loads were issued with the dO
+    // loads, ahead of the first tile's copies, so their latency overlaps those.
+    float dp = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(df[ks]));
+    for (int ks = 0; ks < kDK; ++ks) {
+      asm volatile("" : "+v"(df[ks]), "+v"(of[ks]));
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dp = __builtin_fmaf((float)df[ks][j], (float)of[ks][j], dp);
+    }
+    dq_row = sum_xhalf(dp);
+    if (qvalid && hf == 0) dvec[qrow + qi] = dq_row;
   }
 
   // Tile t from stage cur; the copies of tile t+1 go to stage nxt (free since the barrier that ended
@@ -1843,8 +1861,8 @@ hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   const float sl2 = sh.scale * kLog2e;
   dim3 grid(fwd_grid(sh)), block(256);
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
     return hipGetLastError();
   }
   if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
@@ -1858,14 +1876,18 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
                   bf16_t* dk, bf16_t* dv, float* dvec, hipStream_t st) {
   const long rows = (long)sh.b * sh.hq * sh.s;
   dim3 block(256);
-  hipLaunchKernelGGL(attn_bwd_dvec_kernel<DH>, dim3((unsigned)((rows + 31) / 32)), block, 0, st, o, d_o, dvec, rows);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  hipError_t e = hipSuccess;
+  // head_dim 128: the dQ pass forms D itself (and writes it for dK/dV).
+  if constexpr (DH != 128) {
+    hipLaunchKernelGGL(attn_bwd_dvec_kernel<DH>, dim3((unsigned)((rows + 31) / 32)), block, 0, st, o, d_o, dvec, rows);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   const float sl2 = sh.scale * kLog2e;
   dim3 qgrid(fwd_grid(sh));
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
   } else {
   if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
   else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
