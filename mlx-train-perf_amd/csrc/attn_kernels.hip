@@ -367,7 +367,8 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward pre-pass: D[row] = sum_d dO[row][d] * O[row][d] (fp32). 8 lanes per row.
+// Backward pre-pass for head_dim 64 and 96: D[row] = sum_d dO[row][d] * O[row][d] (fp32), 8 lanes
+// per row. For head_dim 128 the dQ pass (attn_kv128_kernel<., true>) forms D itself.
 // ------------------------------------------------------------------------------------------
 template <int DH>
 __global__ __launch_bounds__(256) void attn_bwd_dvec_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ d_o,
