@@ -1740,10 +1740,14 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
             pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
           }
       } else {
-        // Online softmax in the log2 domain against a reference maximum m that is raised only when
-        // some row of the wave exceeds it by more than kRescaleLog2: O and l are then rescaled
+        // Online softmax in the log2 domain against a reference maximum m that a row raises only
+        // when its tile maximum exceeds m by more than kRescaleLog2: its O and l are then rescaled
         // together, otherwise probabilities up to 2^kRescaleLog2 accumulate against the old m.
-        // O / l and L = m + log2(l) are the same either way; most tiles skip the rescale.
+        // O / l and L = m + log2(l) are the same either way. The branch is taken by the whole wave
+        // when any row needs it (most tiles skip it), but each row decides for itself and the
+        // others multiply by exactly 1: a row's arithmetic depends only on its own scores, so rows
+        // of other packed segments sharing the wave come out bitwise the same whatever this row's
+        // keys hold.
         {
           float mx = kNegInf;
 #pragma unroll
@@ -1752,10 +1756,10 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
             for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, sacc[kb][r]), sacc[kb][r + 1]);
           mx = max_xhalf(mx);
           const float mt = mx * scale_log2;  // scale_log2 > 0: the max of the scaled scores
-          if (__builtin_amdgcn_ballot_w64(mt > m + kRescaleLog2) != 0) {
-            const float mn = fmaxf(m, mt);
-            const float alpha = fast_exp2(m - ((mn == kNegInf) ? 0.f : mn));
-            m = mn;
+          const bool up = mt > m + kRescaleLog2;  // false while mt = -inf (all keys hidden)
+          if (__builtin_amdgcn_ballot_w64(up) != 0) {
+            const float alpha = up ? fast_exp2(m - mt) : 1.f;  // m = -inf: alpha = 0 (O, l are 0)
+            m = up ? mt : m;
             l *= alpha;
 #pragma unroll
             for (int db = 0; db < kDB; ++db)

@@ -10,13 +10,14 @@ No silent fallback: unsupported configs raise the reference's typed errors.
 """
 from __future__ import annotations
 
+import weakref
 from typing import Literal
 
 import torch
 
 from mlx_train_perf import _compat, _native
 from mlx_train_perf.attention.reference import flash_attention_reference, kv_head_for
-from mlx_train_perf.attention.segments import PackedMask, segment_allowed
+from mlx_train_perf.attention.segments import PackedMask, layout_violation, segment_allowed
 from mlx_train_perf.errors import AttentionInputError, UnsupportedAttentionError
 
 _KERNEL_DTYPES = (torch.bfloat16,)
@@ -45,23 +46,46 @@ def _validate_shapes(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> None:
         raise AttentionInputError(f"sequence length mismatch: q={n_q}, k={n_k}, v={n_v}")
     if not (d_q == d_k == d_v):
         raise AttentionInputError(f"head_dim mismatch: q={d_q}, k={d_k}, v={d_v}")
+    if not (q.device == k.device == v.device):
+        raise AttentionInputError(f"q, k, v must be on one device; got {q.device}, {k.device}, {v.device}")
 
 
-def _validate_segments(q: torch.Tensor, segments: PackedMask) -> None:
+# Segment tensors whose layout passed `layout_violation`: weak references to the two tensors and their
+# version counters. A model calls flash_attention once per layer with the same mask, so the check
+# (one device pass and a host sync) runs once per mask rather than once per layer; an in-place edit
+# bumps a version and a new tensor is a new object, so either is checked again.
+_CHECKED_LAYOUTS: dict[int, tuple] = {}
+
+
+def _layout_seen(segments: PackedMask) -> bool:
+    ent = _CHECKED_LAYOUTS.get(id(segments.seg_id))
+    return (ent is not None and ent[0]() is segments.seg_id and ent[1]() is segments.seg_start
+            and ent[2] == (segments.seg_id._version, segments.seg_start._version))
+
+
+def _validate_segments(q: torch.Tensor, segments: PackedMask, *, check_layout: bool = False) -> None:
     b, _, n, _ = q.shape
     for name, t in (("seg_id", segments.seg_id), ("seg_start", segments.seg_start)):
         if tuple(t.shape) != (b, n):
             raise AttentionInputError(f"segments.{name} must have shape (B, N)=({b}, {n}); got {tuple(t.shape)}")
-        if t.dtype.is_floating_point:
+        if t.dtype.is_floating_point or t.dtype == torch.bool or t.dtype.is_complex:
             raise AttentionInputError(f"segments.{name} must be an integer tensor; got {t.dtype}")
+    if check_layout and not _layout_seen(segments):
+        problem = layout_violation(segments.seg_id, segments.seg_start)
+        if problem is not None:
+            raise AttentionInputError(f"segments violate the packed-row layout contract: {problem}")
+        if len(_CHECKED_LAYOUTS) > 64:
+            _CHECKED_LAYOUTS.clear()
+        sid, sst = segments.seg_id, segments.seg_start
+        _CHECKED_LAYOUTS[id(sid)] = (weakref.ref(sid), weakref.ref(sst), (sid._version, sst._version))
 
 
 def resolve_attention_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, impl: str, causal: bool = True,
-                           segments: PackedMask | None = None) -> str:
+                           segments: PackedMask | None = None, validate_segments: bool = False) -> str:
     """api.py:75-123: "reference" is always allowed; "auto"/"kernel" run the kernel-support gate."""
     _validate_shapes(q, k, v)
     if segments is not None:
-        _validate_segments(q, segments)
+        _validate_segments(q, segments, check_layout=validate_segments)
         if not causal:
             raise UnsupportedAttentionError(
                 "segments (packed attention) require causal=True (got causal=False); "
@@ -204,13 +228,17 @@ class _KernelAttention(torch.autograd.Function):
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool = True,
                     impl: Literal["auto", "kernel", "reference"] = "auto",
-                    segments: PackedMask | None = None) -> torch.Tensor:
+                    segments: PackedMask | None = None, validate_segments: bool = True) -> torch.Tensor:
     """softmax(scale * Q K^T + mask) V with GQA (api.py:281-439). Only O is returned; L stays internal.
 
     `segments` (requires causal=True) switches on packed block-diagonal-causal attention; the
     segment tensors are passed to the kernels per call (never captured), so every step masks with
-    its own layout."""
-    resolved = resolve_attention_impl(q, k, v, impl=impl, causal=causal, segments=segments)
+    its own layout. `validate_segments` checks the layout contract of `PackedMask` (seg_id from 0 in
+    steps of 0 or 1, seg_start the first position of each segment) and raises AttentionInputError
+    on a violation; the check costs one host sync per distinct mask (a model's layers share it).
+    Pass False on a trusted path, like the loss's `validate_targets`."""
+    resolved = resolve_attention_impl(q, k, v, impl=impl, causal=causal, segments=segments,
+                                      validate_segments=validate_segments)
     seg_id, seg_start = (None, None) if segments is None else _seg_args(q, segments.seg_id, segments.seg_start)
     if resolved == "kernel":
         o, _ = _KernelAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), seg_id, seg_start, float(scale))

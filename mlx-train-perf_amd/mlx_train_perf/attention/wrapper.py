@@ -54,6 +54,41 @@ def _resolve_mask(mask: Any) -> bool | PackedMask:
     )
 
 
+class _UnsupportedMask:
+    """What `_hf_mask` hands to the layers for a mask pattern the causal kernels cannot honour; the
+    attention call then refuses with `reason` instead of silently attending causally."""
+
+    __slots__ = ("reason",)
+
+    def __init__(self, reason: str) -> None:
+        self.reason = reason
+
+
+def _hf_mask(batch_size: int, q_length: int, kv_length: int, q_offset: int = 0, kv_offset: int = 0,
+             mask_function: Any = None, attention_mask: torch.Tensor | None = None, **kwargs: Any) -> Any:
+    """transformers mask-interface function for IMPL_NAME.
+
+    Returns None exactly when the layers may run plain causal attention: the pattern is the stock
+    causal one and the 2-D padding mask is absent or all ones. A padding mask with a zero, or any
+    other pattern (sliding window, packed sequences detected from `position_ids`, or/and overlays),
+    comes back as an `_UnsupportedMask`, so `_hf_flash_attention` raises `AttentionInputError`."""
+    from transformers.masking_utils import causal_mask_function  # noqa: PLC0415
+
+    if mask_function is not None and mask_function is not causal_mask_function:
+        return _UnsupportedMask(
+            "the model requested a non-causal mask pattern (sliding window, packed position_ids or a mask "
+            "overlay); the flash-attention path serves plain causal attention, or packed rows through "
+            "`mtp_segments=`")
+    if attention_mask is None:
+        return None
+    if attention_mask.dim() != 2:
+        return _UnsupportedMask(f"a {attention_mask.dim()}-D attention mask was given")
+    am = attention_mask[:, -kv_length:]
+    if am.shape[1] == kv_length and bool(am.all()):
+        return None
+    return _UnsupportedMask("the batch has padding (attention_mask holds zeros); pack the rows or trim the padding")
+
+
 def _hf_flash_attention(module: nn.Module, query: torch.Tensor, key: torch.Tensor, value: torch.Tensor,
                         attention_mask: Any, scaling: float, dropout: float = 0.0,
                         mtp_segments: PackedMask | None = None, **kwargs: Any):
@@ -61,10 +96,12 @@ def _hf_flash_attention(module: nn.Module, query: torch.Tensor, key: torch.Tenso
     returns (output (B,S,Hq,D), None)."""
     if dropout:
         raise UnsupportedAttentionError("flash-attention training path does not support attention dropout")
-    if attention_mask is not None and mtp_segments is None:
-        # transformers builds no mask for a registered implementation; an explicit one means padding
-        # or a sliding window, which this causal-only path cannot honour.
-        raise AttentionInputError("explicit attention masks are not supported by the flash-attention path")
+    if attention_mask is not None:
+        # `_hf_mask` returns None for every mask this path honours; anything else (padding, sliding
+        # windows, packed position_ids, a prepared 4-D mask) is refused, with or without mtp_segments.
+        reason = attention_mask.reason if isinstance(attention_mask, _UnsupportedMask) else \
+            "an explicit attention mask was given"
+        raise AttentionInputError(f"the flash-attention path cannot honour this mask: {reason}")
     impl = getattr(module.config, "_mtp_flash_impl", "auto")
     out = flash_attention(query, key, value, scale=float(scaling), causal=True, impl=impl, segments=mtp_segments)
     return out.transpose(1, 2).contiguous(), None
@@ -174,7 +211,7 @@ def enable_flash_attention(model: Any, *, impl: str = "auto", seq_len: int | Non
         try:
             from transformers import AttentionMaskInterface  # noqa: PLC0415
 
-            AttentionMaskInterface.register(IMPL_NAME, lambda *a, **k: None)
+            AttentionMaskInterface.register(IMPL_NAME, _hf_mask)
         except ImportError:
             pass
         cfg._mtp_flash_impl = impl

@@ -1,14 +1,24 @@
-"""Chunked linear-CE on torch tensors, `impl="chunked"`: never materializes the full (N,V) logits.
+"""`impl="chunked"`: linear cross-entropy in plain torch ops over vocab slabs.
 
-Mirrors src/mlx_train_perf/core/chunked.py on torch: `streamed_lse_and_target` (:35-49),
-`chunked_backward` (:52-90, fp32 d_hidden accumulator, g rounded to the weight dtype before
-g @ w_chunk), `make_chunked_dense` (:93-132, recompute-lse backward, trainable head gradient) and
-`make_chunked_quantized` (:135-183, chunk-sized dequantize). An explicit opt-in only; it runs with
-torch ops on whatever device the tensors live on and is never chosen by `impl="auto"`.
+No more than one (N, slab) block of logits exists at a time. The head is read through `_Slabs`,
+which hands out weight blocks in vocab order: a dense head is sliced, a 4-bit head has only the
+requested block dequantized. One autograd Function does the rest:
+
+- forward: a streaming log-sum-exp over the slabs (a running row maximum and a sum of exponentials
+  rescaled whenever the maximum rises, so each slab is exponentiated once), the target logit picked
+  from the slab that holds it, and the resulting `lse` saved as the only residual besides the inputs;
+- backward: each slab again, p = exp(z - lse) with the target's indicator subtracted, scaled by the
+  cotangent and rounded to the head dtype, then dL/dH += g @ W_slab in an fp32 accumulator and, for a
+  trainable dense head, dL/dW[slab] = g^T @ H written in place.
+
+The arithmetic is the reference's chunked path (src/mlx_train_perf/core/chunked.py:35-90: fp32
+logits, g cast to the weight dtype before its product, fp32 dH accumulation, one cast at the end,
+dW = g^T h per chunk). The one structural difference: the reference's custom vjp recomputes lse
+(chunked.py:118-121); here it is saved by the forward, as the kernel path does. An explicit opt-in
+only: it runs on whatever device holds the tensors and is never chosen by `impl="auto"`.
 """
 from __future__ import annotations
 
-from collections.abc import Callable
 from typing import NamedTuple
 
 import torch
@@ -17,7 +27,8 @@ from mlx_train_perf.core.quant import dequantize
 
 
 class QuantSpec(NamedTuple):
-    """Frozen quantized head pieces (MLX affine layout; groups along D)."""
+    """A frozen 4-bit affine head in the form this path reads it: packed words (V, D/8), per-group
+    scale and bias (V, D/group_size), group size and bit width (reference core/chunked.py:16-22)."""
     w_q: torch.Tensor
     scales: torch.Tensor
     biases: torch.Tensor
@@ -25,125 +36,89 @@ class QuantSpec(NamedTuple):
     bits: int
 
 
-MatmulChunk = Callable[[int, int], torch.Tensor]  # (v0, v1) -> (N, v1-v0) fp32 logits
-WChunk = Callable[[int, int], torch.Tensor]       # (v0, v1) -> (v1-v0, D) weights
-
-# Engagement counter (core/chunked.py:27-32): every custom backward increments its key first.
+# Test seam: each custom backward bumps its key ("dense" / "quantized") when it runs, so a test can
+# tell the hand-written backward from an autograd trace through the forward ops.
 VJP_CALLS: dict[str, int] = {}
 
 
-def streamed_lse_and_target(matmul_chunk: MatmulChunk, targets: torch.Tensor, *, v: int, chunk_size: int,
-                            n: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Stream vocab chunks -> (lse (N,) fp32, target_logit (N,) fp32)."""
-    dev = targets.device
-    lse = torch.full((n,), float("-inf"), dtype=torch.float32, device=dev)
-    tgt = torch.zeros((n,), dtype=torch.float32, device=dev)
-    for v0 in range(0, v, chunk_size):
-        v1 = min(v0 + chunk_size, v)
-        logits = matmul_chunk(v0, v1)
-        lse = torch.logaddexp(lse, torch.logsumexp(logits, dim=-1))
-        in_chunk = (targets >= v0) & (targets < v1)
-        idx = (targets - v0).clamp(0, v1 - v0 - 1)
-        got = logits.gather(1, idx[:, None]).squeeze(1)
-        tgt = torch.where(in_chunk, got, tgt)
-    return lse, tgt
+class _Slabs:
+    """Vocab slabs [v0, v1) of a head of `v` rows, `slab` rows each (the last one shorter)."""
+
+    def __init__(self, *, v: int, slab: int, quant: QuantSpec | None, dtype: torch.dtype):
+        if slab < 1:
+            raise ValueError(f"chunk_size must be >= 1 (got {slab})")
+        self.v, self.slab, self.quant, self.dtype = v, slab, quant, dtype
+
+    def bounds(self):
+        return ((v0, min(v0 + self.slab, self.v)) for v0 in range(0, self.v, self.slab))
+
+    def weight(self, v0: int, v1: int, dense: torch.Tensor | None) -> torch.Tensor:
+        if self.quant is None:
+            return dense[v0:v1]
+        q = self.quant
+        return dequantize(q.w_q[v0:v1], q.scales[v0:v1], q.biases[v0:v1], group_size=q.group_size, bits=q.bits,
+                          dtype=self.dtype)
 
 
-def chunked_backward(*, hidden: torch.Tensor, matmul_chunk: MatmulChunk, w_chunk: WChunk, targets: torch.Tensor,
-                     lse: torch.Tensor, cotangent: torch.Tensor, v: int, chunk_size: int,
-                     head_trainable: bool) -> tuple[torch.Tensor, torch.Tensor | None]:
-    """Given SAVED lse: d_hidden (hidden dtype) and d_w (or None if frozen)."""
-    n, d = hidden.shape
-    ct = cotangent.to(torch.float32)
-    d_hidden32 = torch.zeros((n, d), dtype=torch.float32, device=hidden.device)
-    d_w_chunks: list[torch.Tensor] = []
-    for v0 in range(0, v, chunk_size):
-        v1 = min(v0 + chunk_size, v)
-        logits = matmul_chunk(v0, v1)
-        p = torch.exp(logits - lse[:, None])
-        onehot = torch.arange(v0, v1, device=hidden.device)[None, :] == targets[:, None]
-        g32 = (p - onehot.to(p.dtype)) * ct[:, None]
-        wc = w_chunk(v0, v1)
-        g = g32.to(wc.dtype)
-        d_hidden32 += (g @ wc).to(torch.float32)
-        if head_trainable:
-            d_w_chunks.append(g.T @ hidden)
-    if not head_trainable:
-        return d_hidden32.to(hidden.dtype), None
-    return d_hidden32.to(hidden.dtype), torch.cat(d_w_chunks, dim=0)
+def _slab_logits(hidden: torch.Tensor, w_slab: torch.Tensor) -> torch.Tensor:
+    return (hidden @ w_slab.T).to(torch.float32)
 
 
-class _ChunkedDense(torch.autograd.Function):
+def _target_column(targets: torch.Tensor, v0: int, v1: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(in-slab flag, clamped column index) of each row's target for slab [v0, v1)."""
+    inside = (targets >= v0) & (targets < v1)
+    return inside, (targets - v0).clamp(0, v1 - v0 - 1)
+
+
+class _ChunkedLCE(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, hidden, w, targets, chunk_size):  # noqa: D401 -- torch signature
-        n, v = hidden.shape[0], w.shape[0]
-
-        def mm(v0: int, v1: int) -> torch.Tensor:
-            return (hidden @ w[v0:v1].T).to(torch.float32)
-
-        lse, tgt = streamed_lse_and_target(mm, targets, v=v, chunk_size=chunk_size, n=n)
-        ctx.save_for_backward(hidden, w, targets)
-        ctx.chunk_size = chunk_size
+    def forward(ctx, hidden, dense_w, targets, slabs):
+        n = hidden.shape[0]
+        dev = hidden.device
+        row_max = torch.full((n,), float("-inf"), dtype=torch.float32, device=dev)
+        row_sum = torch.zeros((n,), dtype=torch.float32, device=dev)
+        tgt = torch.zeros((n,), dtype=torch.float32, device=dev)
+        for v0, v1 in slabs.bounds():
+            z = _slab_logits(hidden, slabs.weight(v0, v1, dense_w))
+            new_max = torch.maximum(row_max, z.amax(dim=-1))
+            row_sum = row_sum * torch.exp(row_max - new_max) + torch.exp(z - new_max[:, None]).sum(dim=-1)
+            row_max = new_max
+            inside, col = _target_column(targets, v0, v1)
+            tgt = torch.where(inside, z.gather(1, col[:, None]).squeeze(1), tgt)
+        lse = row_max + torch.log(row_sum)
+        ctx.save_for_backward(hidden, dense_w, targets, lse)
+        ctx.slabs = slabs
         return lse - tgt
 
     @staticmethod
-    def backward(ctx, cotangent):
-        VJP_CALLS["dense"] = VJP_CALLS.get("dense", 0) + 1
-        hidden, w, targets = ctx.saved_tensors
-        n, v = hidden.shape[0], w.shape[0]
-        cs = ctx.chunk_size
-
-        def mm(v0: int, v1: int) -> torch.Tensor:
-            return (hidden @ w[v0:v1].T).to(torch.float32)
-
-        lse, _ = streamed_lse_and_target(mm, targets, v=v, chunk_size=cs, n=n)
-        d_hidden, d_w = chunked_backward(hidden=hidden, matmul_chunk=mm, w_chunk=lambda a, b: w[a:b],
-                                         targets=targets, lse=lse, cotangent=cotangent, v=v, chunk_size=cs,
-                                         head_trainable=ctx.needs_input_grad[1])
-        return d_hidden, d_w, None, None
-
-
-class _ChunkedQuant(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, hidden, targets, q, chunk_size):
-        n, v = hidden.shape[0], q.w_q.shape[0]
-
-        def mm(v0: int, v1: int) -> torch.Tensor:
-            wc = dequantize(q.w_q[v0:v1], q.scales[v0:v1], q.biases[v0:v1], group_size=q.group_size,
-                            bits=q.bits, dtype=hidden.dtype)
-            return (hidden @ wc.T).to(torch.float32)
-
-        lse, tgt = streamed_lse_and_target(mm, targets, v=v, chunk_size=chunk_size, n=n)
-        ctx.save_for_backward(hidden, targets)
-        ctx.q = q
-        ctx.chunk_size = chunk_size
-        return lse - tgt
-
-    @staticmethod
-    def backward(ctx, cotangent):
-        VJP_CALLS["quantized"] = VJP_CALLS.get("quantized", 0) + 1
-        hidden, targets = ctx.saved_tensors
-        q, cs = ctx.q, ctx.chunk_size
-        n, v = hidden.shape[0], q.w_q.shape[0]
-
-        def w_chunk(v0: int, v1: int) -> torch.Tensor:  # chunk-sized dequant only
-            return dequantize(q.w_q[v0:v1], q.scales[v0:v1], q.biases[v0:v1], group_size=q.group_size,
-                              bits=q.bits, dtype=hidden.dtype)
-
-        def mm(v0: int, v1: int) -> torch.Tensor:
-            return (hidden @ w_chunk(v0, v1).T).to(torch.float32)
-
-        lse, _ = streamed_lse_and_target(mm, targets, v=v, chunk_size=cs, n=n)
-        d_hidden, _ = chunked_backward(hidden=hidden, matmul_chunk=mm, w_chunk=w_chunk, targets=targets, lse=lse,
-                                       cotangent=cotangent, v=v, chunk_size=cs, head_trainable=False)
-        return d_hidden, None, None, None
+    def backward(ctx, grad_nll):
+        hidden, dense_w, targets, lse = ctx.saved_tensors
+        slabs: _Slabs = ctx.slabs
+        VJP_CALLS["quantized" if slabs.quant is not None else "dense"] = \
+            VJP_CALLS.get("quantized" if slabs.quant is not None else "dense", 0) + 1
+        want_dw = dense_w is not None and ctx.needs_input_grad[1]
+        ct = grad_nll.to(torch.float32)[:, None]
+        dh32 = torch.zeros(hidden.shape, dtype=torch.float32, device=hidden.device)
+        dw = torch.empty_like(dense_w) if want_dw else None
+        for v0, v1 in slabs.bounds():
+            w_slab = slabs.weight(v0, v1, dense_w)
+            g = torch.exp(_slab_logits(hidden, w_slab) - lse[:, None])
+            inside, col = _target_column(targets, v0, v1)
+            g.scatter_add_(1, col[:, None], -inside.to(g.dtype)[:, None])
+            g = (g * ct).to(w_slab.dtype)
+            dh32 += (g @ w_slab).to(torch.float32)
+            if want_dw:
+                dw[v0:v1] = g.T @ hidden
+        return dh32.to(hidden.dtype), dw, None, None
 
 
-def make_chunked_dense(chunk_size: int) -> Callable[[torch.Tensor, torch.Tensor, torch.Tensor], torch.Tensor]:
-    """Dense-head chunked CE. The head is an explicit input (its gradient flows if it requires grad)."""
-    return lambda hidden, w, targets: _ChunkedDense.apply(hidden, w, targets, chunk_size)
-
-
-def make_chunked_quantized(chunk_size: int, q: QuantSpec) -> Callable[[torch.Tensor, torch.Tensor], torch.Tensor]:
-    """Quantized-head chunked CE: d_hidden only (the quantized head is frozen)."""
-    return lambda hidden, targets: _ChunkedQuant.apply(hidden, targets, q, chunk_size)
+def chunked_nll(hidden: torch.Tensor, targets: torch.Tensor, *, chunk_size: int,
+                weight: torch.Tensor | None = None, quant: QuantSpec | None = None) -> torch.Tensor:
+    """Per-token NLL (N,) fp32 of `hidden` (N, D) against a dense `weight` (V, D) -- differentiable in
+    both, so a trainable head gets its gradient -- or a frozen 4-bit `quant` head (dL/dH only).
+    `targets` must lie in [0, V)."""
+    if (weight is None) == (quant is None):
+        raise ValueError("pass exactly one of weight= and quant=")
+    v = weight.shape[0] if quant is None else quant.w_q.shape[0]
+    slabs = _Slabs(v=v, slab=chunk_size, quant=quant, dtype=hidden.dtype)
+    return _ChunkedLCE.apply(hidden, weight, targets.long(), slabs)

@@ -33,6 +33,7 @@ from mlx_train_perf.plan import launch as _plan
 _KERNEL_DTYPES = (torch.bfloat16,)
 _KERNEL_ROW_TILE = 256  # token rows per workgroup tile (reported as Resolution.row_tiles)
 _DEFAULT_CHUNK = 8192   # chunked-impl vocab chunk (the reference's kernel tile, loss.py:25)
+_WORD_DTYPES = tuple(t for t in (torch.int32, getattr(torch, "uint32", None)) if t is not None)
 
 
 @dataclass(frozen=True, slots=True, kw_only=True)
@@ -94,6 +95,17 @@ def _require_kernel_supported(*, head: HeadRef, dtype: torch.dtype) -> None:
                 "kernel impl requires the quantized head's hidden dim to be a multiple of "
                 f"64 (got d={d}); use impl='chunked'."
             )
+        if head.w_q.dtype not in _WORD_DTYPES:
+            raise UnsupportedHeadError(
+                f"kernel impl reads w_q as 32-bit words (int32 or uint32 bit patterns); got {head.w_q.dtype}. "
+                "Use impl='chunked'."
+            )
+        for name, t in (("scales", head.scales), ("biases", head.biases)):
+            if t.dtype != torch.bfloat16:
+                raise UnsupportedHeadError(
+                    f"kernel impl reads the quantized head's {name} as bf16; got {t.dtype}. Use impl='chunked' "
+                    "(it dequantizes in the given dtype) or store them as bf16."
+                )
     else:
         d = head.weight.shape[-1]
         if d % 8 != 0:
@@ -152,12 +164,20 @@ def _validate_inputs(*, hidden: torch.Tensor, head: HeadRef, targets: torch.Tens
             )
         v = head.weight.shape[0]
     else:
+        if head.w_q.dim() != 2:
+            raise LossInputError(f"w_q must be 2-D (V, D*bits/32); got shape {tuple(head.w_q.shape)}")
         head_d = _quantized_head_d(head)
         if head_d != d:
             raise LossInputError(
                 f"quantized head implies D={head_d} (from w_q shape and bits), which does not match hidden's D={d}"
             )
         v = head.w_q.shape[0]
+        groups = (d + head.group_size - 1) // head.group_size
+        for name, t in (("scales", head.scales), ("biases", head.biases)):
+            if tuple(t.shape) != (v, groups):
+                raise LossInputError(
+                    f"quantized head {name} must have shape (V, D/group_size)=({v}, {groups}); got {tuple(t.shape)}"
+                )
     if validate_targets:
         # A host sync, skipped on the trusted training path (validate_targets=False).
         valid = targets[targets != ignore_index]
@@ -198,11 +218,11 @@ def _chunked_nll(hidden2, head, targets2, ignore_index, chunk_size):
     safe = torch.where(targets2 == ignore_index, torch.zeros_like(targets2), targets2).long()
     if isinstance(head, DenseHead):
         w = head.weight if head.trainable else head.weight.detach()
-        nll = _chunked.make_chunked_dense(chunk_size)(hidden2, w, safe)
+        nll = _chunked.chunked_nll(hidden2, safe, chunk_size=chunk_size, weight=w)
     else:
         q = _chunked.QuantSpec(w_q=head.w_q, scales=head.scales, biases=head.biases,
                                group_size=head.group_size, bits=head.bits)
-        nll = _chunked.make_chunked_quantized(chunk_size, q)(hidden2, safe)
+        nll = _chunked.chunked_nll(hidden2, safe, chunk_size=chunk_size, quant=q)
     return _mask_ignored(nll, targets2, ignore_index)
 
 
@@ -292,10 +312,25 @@ class _KernelLCE(torch.autograd.Function):
         return d_hidden, None, d_w, None, None, None, None, None, None, None
 
 
+def _require_same_device(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor) -> None:
+    """Every tensor the kernels read must live on hidden's GPU: a host or other-device pointer
+    handed to a launch would fault the GPU instead of raising."""
+    _compat.require_gpu_tensor(hidden2, error=UnsupportedHeadError)
+    parts = [("targets", targets2)]
+    if isinstance(head, DenseHead):
+        parts.append(("head.weight", head.weight))
+    else:
+        parts += [("head.w_q", head.w_q), ("head.scales", head.scales), ("head.biases", head.biases)]
+    for name, t in parts:
+        if t.device != hidden2.device:
+            raise LossInputError(f"{name} is on {t.device} but hidden is on {hidden2.device}; the kernel impl "
+                                 "needs every input on the same GPU")
+
+
 def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor, *, ignore_index: int = -100,
                          bwd_chunk: int | None = None) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """(nll, lse, tgt) from the kernel impl, differentiable in hidden2 through `nll` (test/bench seam)."""
-    _compat.require_gpu_tensor(hidden2, error=UnsupportedHeadError)
+    _require_same_device(hidden2, head, targets2)
     h = hidden2.contiguous()
     t = targets2.to(torch.int64).contiguous()
     if isinstance(head, DenseHead):

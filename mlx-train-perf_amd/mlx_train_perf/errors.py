@@ -1,55 +1,57 @@
-"""Typed error hierarchy, same names and meaning as the reference (src/mlx_train_perf/errors.py:1-76).
-
-Only the errors the hot path raises are defined; each keeps the reference's semantics:
-no silent fallback, refuse before launch.
+"""Exceptions of this package. The class names and the hierarchy are those of the reference
+(src/mlx_train_perf/errors.py:1-76), so callers can catch the same types; only the errors the hot
+path can raise are defined. Every refusal happens on the host, before anything is launched.
 """
 
 
 class MlxTrainPerfError(Exception):
-    """Root of all mlx-train-perf errors."""
+    """Base class: catching it catches every error this package raises on purpose."""
 
 
 class UnsupportedHeadError(MlxTrainPerfError):
-    """Head kind/dtype the requested impl cannot serve (no silent fallback)."""
+    """The requested loss impl cannot serve this head kind or dtype. The message names the impl that
+    can; nothing switches impls behind the caller's back."""
 
 
 class LaunchBudgetError(MlxTrainPerfError):
-    """A launch would exceed its workspace budget; refused before launch.
+    """A launch was refused because its workspace is missing or smaller than the plan needs.
 
-    (The reference raises it for the macOS GPU-watchdog budget, errors.py:13-14; on MI355X the only
-    budget is the caller-provided workspace.)"""
+    (The reference uses this type for its macOS GPU-watchdog time budget, errors.py:13-14; compute
+    queues on MI355X have no such watchdog, so the workspace is the only budget left.)"""
 
 
 class LossInputError(MlxTrainPerfError):
-    """Shape/dtype/target-range validation failure at the loss boundary."""
+    """The loss was called with inconsistent shapes, a wrong dtype, or targets outside [0, V)."""
 
 
 class PlanInputError(MlxTrainPerfError):
-    """Shape/config validation failure in the memory planner."""
+    """The memory planner was given a shape or config it cannot price (e.g. an unknown dtype)."""
 
 
 class DoesNotFitError(MlxTrainPerfError):
-    """Planner verdict: predicted peak exceeds the memory budget."""
+    """The memory planner predicts a peak above the memory available for the run."""
 
 
 class AdapterError(MlxTrainPerfError):
-    """The model cannot be split into trunk + head (unsupported architecture, missing modules)."""
+    """The model does not split into a trunk and a head the fused loss can use (unknown
+    architecture, missing modules, a head with a bias)."""
 
 
 class MissingDependencyError(MlxTrainPerfError):
-    """A required native component (the HIP extension) or optional dependency is absent."""
+    """Something required is absent: the built HIP library, or an optional Python package."""
 
 
 class UnsupportedAttentionError(MlxTrainPerfError):
-    """Attention impl/config combination the requested impl cannot serve (no silent fallback) --
-    e.g. an unsupported dtype, head_dim, or causal=False for impl='kernel'."""
+    """The requested attention impl cannot serve this configuration (dtype, head_dim, mask). The
+    message names the impl that can."""
 
 
 class AttentionInputError(MlxTrainPerfError):
-    """Shape validation failure at the flash_attention boundary (non-4D tensors, Hq not a
-    multiple of Hkv, mismatched N/D/batch across q/k/v)."""
+    """flash_attention was called with malformed inputs: tensors that are not 4-D, Hq not a multiple
+    of Hkv, disagreeing batch / length / head_dim, tensors on different devices, or a segment layout
+    that breaks the packed-row contract."""
 
 
 class PackingError(MlxTrainPerfError):
-    """Sequence-packing input validation failure (empty dataset, zero-length sequence,
-    non-positive pack_len) -- no silent fallback."""
+    """The sequence packer was given unusable input: no sequences, an empty sequence, or a
+    non-positive pack length."""

@@ -25,13 +25,13 @@ def segment_allowed(seg_id: torch.Tensor) -> torch.Tensor:
     """(B, 1, N, N) bool: key j visible to query i iff same segment and j <= i (segments.py:22-29)."""
     same = seg_id[:, None, :, None] == seg_id[:, None, None, :]
     n = seg_id.shape[-1]
-    causal = torch.tril(torch.ones(n, n, dtype=torch.bool))[None, None]
+    causal = torch.tril(torch.ones(n, n, dtype=torch.bool, device=seg_id.device))[None, None]
     return same & causal
 
 
 def _gather_kv(x: torch.Tensor, hq: int) -> torch.Tensor:
     hkv = x.shape[1]
-    idx = torch.tensor([kv_head_for(h, hq // hkv) for h in range(hq)])
+    idx = torch.tensor([kv_head_for(h, hq // hkv) for h in range(hq)], device=x.device)
     return x.index_select(1, idx)
 
 
@@ -39,14 +39,14 @@ def _scores(q, k, *, scale, causal, seg_id, dtype):
     hq = q.shape[1]
     if hq % k.shape[1]:
         raise ValueError("Hq must be a multiple of Hkv")
-    s = (q.to(dtype) @ _gather_kv(k, hq).to(dtype).transpose(-1, -2)) * scale
+    s = (q.to(dtype) @ _gather_kv(k, hq).to(dtype).transpose(-1, -2).contiguous()) * scale
     n = q.shape[2]
     if seg_id is not None:
         if not causal:
             raise ValueError("segments require causal=True")
         s = s.masked_fill(~segment_allowed(seg_id), float("-inf"))
     elif causal:
-        s = s.masked_fill(~torch.tril(torch.ones(n, n, dtype=torch.bool)), float("-inf"))
+        s = s.masked_fill(~torch.tril(torch.ones(n, n, dtype=torch.bool, device=q.device)), float("-inf"))
     return s
 
 
@@ -73,11 +73,11 @@ def attention_backward(q, k, v, o, lse, d_o, *, scale: float, causal: bool = Tru
     dvec = (do32 * o32).sum(-1)
     s = _scores(q, k, scale=scale, causal=causal, seg_id=seg_id, dtype=dtype)
     p = torch.exp(s - lse.to(dtype)[..., None])
-    dp = do32 @ vg.transpose(-1, -2)
+    dp = do32 @ vg.transpose(-1, -2).contiguous()
     ds = p * (dp - dvec[..., None])
     dq = scale * (ds @ kg)
-    dv_h = p.transpose(-1, -2) @ do32
-    dk_h = scale * (ds.transpose(-1, -2) @ q32)
+    dv_h = p.transpose(-1, -2).contiguous() @ do32
+    dk_h = scale * (ds.transpose(-1, -2).contiguous() @ q32)
     dv = dv_h.reshape(b, hkv, grp, n, dd).sum(2)
     dk = dk_h.reshape(b, hkv, grp, n, dd).sum(2)
     return dq, dk, dv

@@ -9,6 +9,9 @@ Follows:
   g @ w_chunk with g = (exp(logits - lse) - onehot) * ct, g rounded to the weight dtype before the
   product (chunked.py:84-86), fp32 accumulation.
 
+Every function runs on the device its inputs live on (CPU here; the GPU parity tests run it in fp64
+on the GPU for the flagship shapes).
+
 The ignore_index contract of this build (the reference masks in its trainer adapter,
 adapters/mlx_lm.py:206-216): rows whose target equals ignore_index get nll = 0, tgt = 0, a zero
 gradient row, and are excluded from the mean.
@@ -44,8 +47,8 @@ def forward(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, *, ign
     v = w.shape[0]
     h = hidden.to(dtype)
     y = targets.long()
-    lse = torch.full((n,), float("-inf"), dtype=dtype)
-    tgt = torch.zeros((n,), dtype=dtype)
+    lse = torch.full((n,), float("-inf"), dtype=dtype, device=hidden.device)
+    tgt = torch.zeros((n,), dtype=dtype, device=hidden.device)
     for v0 in range(0, v, chunk):
         v1 = min(v0 + chunk, v)
         logits = h @ w[v0:v1].to(dtype).T
@@ -74,13 +77,13 @@ def backward(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, lse: 
     y = targets.long()
     ct = torch.where(y == ignore_index, torch.zeros_like(cotangent, dtype=dtype), cotangent.to(dtype))
     lse_ = lse.to(dtype)
-    dh = torch.zeros((n, d), dtype=dtype)
+    dh = torch.zeros((n, d), dtype=dtype, device=hidden.device)
     for v0 in range(0, v, chunk):
         v1 = min(v0 + chunk, v)
         wc = w[v0:v1].to(dtype)
         logits = h @ wc.T
         p = torch.exp(logits - lse_[:, None])
-        onehot = (torch.arange(v0, v1)[None, :] == y[:, None]).to(dtype)
+        onehot = (torch.arange(v0, v1, device=hidden.device)[None, :] == y[:, None]).to(dtype)
         g = (p - onehot) * ct[:, None]
         if round_g_bf16:
             g = _bf16_round(g)
@@ -97,12 +100,12 @@ def backward_dw(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, ls
     h = hidden.to(dtype)
     y = targets.long()
     ct = torch.where(y == ignore_index, torch.zeros_like(cotangent, dtype=dtype), cotangent.to(dtype))
-    out = torch.empty((v, hidden.shape[1]), dtype=dtype)
+    out = torch.empty((v, hidden.shape[1]), dtype=dtype, device=hidden.device)
     for v0 in range(0, v, chunk):
         v1 = min(v0 + chunk, v)
         wc = w[v0:v1].to(dtype)
         p = torch.exp(h @ wc.T - lse.to(dtype)[:, None])
-        onehot = (torch.arange(v0, v1)[None, :] == y[:, None]).to(dtype)
+        onehot = (torch.arange(v0, v1, device=hidden.device)[None, :] == y[:, None]).to(dtype)
         g = (p - onehot) * ct[:, None]
         if round_g_bf16:
             g = _bf16_round(g)
@@ -111,6 +114,7 @@ def backward_dw(hidden: torch.Tensor, w: torch.Tensor, targets: torch.Tensor, ls
 
 
 def reduce_mean(nll: torch.Tensor, targets: torch.Tensor, ignore_index: int = -100) -> torch.Tensor:
-    """Mean over non-ignored rows (the adapter's (nll * mask).sum() / ntoks, adapters/mlx_lm.py:212-216)."""
+    """Mean over non-ignored rows (the adapter's (nll * mask).sum() / ntoks, adapters/mlx_lm.py:212-216);
+    0 when every row is ignored. Pinned by a hand-computed case in tests/test_oracle_lce.py."""
     valid = targets.long() != ignore_index
     return nll[valid].sum() / valid.sum().clamp(min=1)

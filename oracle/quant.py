@@ -37,7 +37,7 @@ def quantize_affine(w: torch.Tensor, group_size: int = 64, bits: int = 4,
     s_safe = torch.where(s == 0, torch.ones_like(s), s)
     q = torch.round((wf - biases.to(torch.float32)[..., None]) / s_safe[..., None]).clamp(0, 2 ** bits - 1)
     q = q.to(torch.int64).reshape(v, d // 8, 8)
-    shifts = torch.arange(8, dtype=torch.int64) * 4
+    shifts = torch.arange(8, dtype=torch.int64, device=w.device) * 4
     words = (q << shifts).sum(dim=-1)  # < 2^32
     words = torch.where(words >= 2 ** 31, words - 2 ** 32, words).to(torch.int32)
     return words, scales, biases
@@ -46,7 +46,7 @@ def quantize_affine(w: torch.Tensor, group_size: int = 64, bits: int = 4,
 def unpack_nibbles(w_q: torch.Tensor) -> torch.Tensor:
     """(V, D/8) uint32 words (as int32 bit patterns) -> (V, D) codes in [0, 15], low nibble first."""
     words = w_q.to(torch.int64) & 0xFFFFFFFF
-    shifts = torch.arange(8, dtype=torch.int64) * 4
+    shifts = torch.arange(8, dtype=torch.int64, device=w_q.device) * 4
     return ((words[..., None] >> shifts) & 0xF).reshape(w_q.shape[0], -1)
 
 

@@ -96,3 +96,121 @@ def test_packed_loss_equals_per_document_losses():
 def test_packed_loss_requires_enable():
     with pytest.raises(AdapterError):
         make_packed_loss_fn(_tiny_llama())
+
+
+def test_padding_mask_is_refused_not_ignored():
+    """A left-padded batch must raise: running it as plain causal attention would silently attend to
+    the padding (transformers builds no mask for a registered implementation unless asked)."""
+    from mlx_train_perf.errors import AttentionInputError
+
+    m = _tiny_llama(head_dim=64)
+    x = torch.randint(0, 97, (2, 20), generator=torch.Generator().manual_seed(4))
+    ref = m(input_ids=x, attention_mask=torch.ones(2, 20, dtype=torch.long)).logits
+    enable_flash_attention(m, impl="reference")
+    out = m(input_ids=x, attention_mask=torch.ones(2, 20, dtype=torch.long)).logits  # all ones: accepted
+    assert torch.allclose(out, ref, atol=1e-4)
+    padded = torch.ones(2, 20, dtype=torch.long)
+    padded[1, :3] = 0
+    with pytest.raises(AttentionInputError, match="padding"):
+        m(input_ids=x, attention_mask=padded)
+    # per-document position_ids make transformers ask for a packed mask: refused too (packed rows go
+    # through mtp_segments=)
+    pid = torch.cat([torch.arange(10), torch.arange(10)])[None].repeat(2, 1)
+    with pytest.raises(AttentionInputError, match="non-causal"):
+        m(input_ids=x, position_ids=pid, use_cache=False)
+
+
+class _Rope(torch.nn.Module):
+    """Rotary embedding on (B, H, L, D), the mlx-lm `nn.RoPE` convention (traditional=False)."""
+
+    def __init__(self, dim: int, base: float = 10000.0):
+        super().__init__()
+        self.register_buffer("inv", base ** (-torch.arange(0, dim, 2).float() / dim), persistent=False)
+
+    def forward(self, x):
+        pos = torch.arange(x.shape[-2], dtype=torch.float32)
+        ang = pos[:, None] * self.inv[None]
+        cos, sin = ang.cos().to(x.dtype), ang.sin().to(x.dtype)
+        x1, x2 = x[..., : x.shape[-1] // 2], x[..., x.shape[-1] // 2:]
+        return torch.cat([x1 * cos - x2 * sin, x1 * sin + x2 * cos], dim=-1)
+
+
+class _MlxStyleAttention(torch.nn.Module):
+    """An mlx-lm-shaped attention block (q/k/v/o_proj, rope, n_heads, n_kv_heads, scale) with the
+    stock materialized causal attention."""
+
+    def __init__(self, dim=64, n_heads=4, n_kv_heads=2, head_dim=64, seed=0):
+        super().__init__()
+        torch.manual_seed(seed)
+        self.n_heads, self.n_kv_heads, self.scale = n_heads, n_kv_heads, head_dim ** -0.5
+        self.q_proj = torch.nn.Linear(dim, n_heads * head_dim, bias=False)
+        self.k_proj = torch.nn.Linear(dim, n_kv_heads * head_dim, bias=False)
+        self.v_proj = torch.nn.Linear(dim, n_kv_heads * head_dim, bias=False)
+        self.o_proj = torch.nn.Linear(n_heads * head_dim, dim, bias=False)
+        self.rope = _Rope(head_dim)
+
+    def forward(self, x, mask=None, cache=None):
+        b, n, _ = x.shape
+        q = self.rope(self.q_proj(x).reshape(b, n, self.n_heads, -1).transpose(1, 2))
+        k = self.rope(self.k_proj(x).reshape(b, n, self.n_kv_heads, -1).transpose(1, 2))
+        v = self.v_proj(x).reshape(b, n, self.n_kv_heads, -1).transpose(1, 2)
+        rep = self.n_heads // self.n_kv_heads
+        k, v = k.repeat_interleave(rep, dim=1), v.repeat_interleave(rep, dim=1)
+        s = (q @ k.transpose(-1, -2)) * self.scale
+        s = s.masked_fill(~torch.tril(torch.ones(n, n, dtype=torch.bool)), float("-inf"))
+        o = torch.softmax(s, dim=-1) @ v
+        return self.o_proj(o.transpose(1, 2).reshape(b, n, -1))
+
+
+def _mlx_style_model(layers=2):
+    from types import SimpleNamespace
+
+    blocks = torch.nn.ModuleList([torch.nn.Module() for _ in range(layers)])
+    for i, blk in enumerate(blocks):
+        blk.self_attn = _MlxStyleAttention(seed=i)
+    inner = torch.nn.Module()
+    inner.layers = blocks
+    model = torch.nn.Module()
+    model.model = inner
+    model.args = SimpleNamespace(num_attention_heads=4, num_key_value_heads=2, hidden_size=64, head_dim=64)
+    return model
+
+
+def test_flash_attention_wrapper_mlx_style_module():
+    """enable_flash_attention on an mlx-lm-shaped model wraps each self_attn in FlashAttentionWrapper:
+    the original submodules stay reachable under their names (LoRA by module path), the output matches
+    the stock block, a PackedMask mask runs block-diagonal attention, and array masks / KV caches are
+    refused."""
+    from mlx_train_perf.attention import FlashAttentionWrapper, PackedMask
+    from mlx_train_perf.attention.wrapper import is_enabled
+    from mlx_train_perf.errors import AttentionInputError
+
+    model = _mlx_style_model()
+    x = torch.randn(2, 12, 64, generator=torch.Generator().manual_seed(5))
+    stock = [blk.self_attn for blk in model.model.layers]
+    refs = [a(x) for a in stock]
+    enable_flash_attention(model, impl="reference")
+    assert is_enabled(model)
+    for blk, orig, ref in zip(model.model.layers, stock, refs):
+        w = blk.self_attn
+        assert isinstance(w, FlashAttentionWrapper)
+        assert w.q_proj is orig.q_proj and w.o_proj is orig.o_proj and w.rope is orig.rope
+        assert dict(w.named_parameters()).keys() == dict(orig.named_parameters()).keys()
+        assert torch.allclose(w(x), ref, atol=1e-5)
+        assert torch.allclose(w(x, mask="causal"), ref, atol=1e-5)
+    # packed: two documents of 5 and 7 tokens; each must equal the stock block run on it alone
+    # (RoPE is relative, so the second document's absolute offset does not matter)
+    sid = torch.tensor([[0] * 5 + [1] * 7] * 2, dtype=torch.int32)
+    sst = torch.tensor([[0] * 5 + [5] * 7] * 2, dtype=torch.int32)
+    w0, orig0 = model.model.layers[0].self_attn, stock[0]
+    out = w0(x, mask=PackedMask(seg_id=sid, seg_start=sst))
+    assert torch.allclose(out[:, :5], orig0(x[:, :5]), atol=1e-5)
+    assert torch.allclose(out[:, 5:], orig0(x[:, 5:]), atol=1e-4)
+    with pytest.raises(AttentionInputError):
+        w0(x, mask=torch.zeros(12, 12))
+    with pytest.raises(AttentionInputError):
+        w0(x, mask="sliding")
+    with pytest.raises(AttentionInputError):
+        w0(x, cache=object())
+    enable_flash_attention(model, impl="reference")   # idempotent: no double wrapping
+    assert isinstance(model.model.layers[0].self_attn.q_proj, torch.nn.Linear)

@@ -162,3 +162,98 @@ def test_reference_impl_matches_oracle(packed):
     for got, want in zip((qq.grad, kk.grad, vv.grad), grads):
         assert torch.allclose(got.double(), want, atol=1e-5)
     assert math.isfinite(float(o.detach().sum()))
+
+
+def test_quantized_head_kernel_gate_checks_dtypes_and_shapes():
+    """The kernels read w_q as 32-bit words and scales/biases as bf16 (V, D/64): other dtypes are
+    refused by the kernel gate (naming impl='chunked'), wrong shapes by the input check (any impl)."""
+    bf = torch.bfloat16
+    wq, sc, bi = oq.quantize_affine(torch.randn(10, 64), scale_dtype=torch.float32)
+    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 scales
+        resolve_impl(head=QuantizedHead(w_q=wq, scales=sc, biases=bi.to(bf)), dtype=bf, n=8)
+    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 biases
+        resolve_impl(head=QuantizedHead(w_q=wq, scales=sc.to(bf), biases=bi), dtype=bf, n=8)
+    with pytest.raises(UnsupportedHeadError, match="32-bit"):  # 64-bit words
+        resolve_impl(head=QuantizedHead(w_q=wq.long(), scales=sc.to(bf), biases=bi.to(bf)), dtype=bf, n=8)
+    h = torch.randn(4, 64).to(bf)
+    t = torch.tensor([0, 1, 2, 3])
+    for bad in (sc[:, :0], sc[:5], torch.cat([sc, sc], dim=1)):
+        with pytest.raises(LossInputError, match="scales"):
+            linear_cross_entropy(h, QuantizedHead(w_q=wq, scales=bad.to(bf), biases=bi.to(bf)), t, impl="chunked")
+    with pytest.raises(LossInputError, match="biases"):
+        linear_cross_entropy(h, QuantizedHead(w_q=wq, scales=sc.to(bf), biases=bi[:3].to(bf)), t, impl="chunked")
+
+
+def test_kernel_path_requires_inputs_on_hidden_device(monkeypatch):
+    """A targets / head tensor on another device than hidden is refused before any launch (a host
+    pointer passed to a kernel would fault the GPU). Run on the CPU with the GPU gate stubbed out
+    and hidden on the `meta` device standing in for the GPU."""
+    from mlx_train_perf import _compat
+    from mlx_train_perf.core import loss as L
+
+    monkeypatch.setattr(_compat, "require_gpu_tensor", lambda t, error: None)
+    h = torch.empty(4, 64, dtype=torch.bfloat16, device="meta")
+    w = torch.empty(10, 64, dtype=torch.bfloat16, device="meta")
+    t_meta = torch.empty(4, dtype=torch.int64, device="meta")
+    with pytest.raises(LossInputError, match="targets"):
+        L._require_same_device(h, DenseHead(weight=w), torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(LossInputError, match="head.weight"):
+        L._require_same_device(h, DenseHead(weight=torch.zeros(10, 64, dtype=torch.bfloat16)), t_meta)
+    wq, sc, bi = oq.quantize_affine(torch.randn(10, 64))
+    qh = QuantizedHead(w_q=wq.to("meta"), scales=sc.to("meta"), biases=bi)
+    with pytest.raises(LossInputError, match="head.biases"):
+        L._require_same_device(h, qh, t_meta)
+    L._require_same_device(h, DenseHead(weight=w), t_meta)  # all on one device: accepted
+
+
+def test_attention_requires_one_device():
+    q, k, v = _attn()
+    with pytest.raises(AttentionInputError, match="one device"):
+        flash_attention(q, k.to("meta"), v, scale=1.0, impl="reference")
+
+
+@pytest.mark.parametrize(("sid", "sst", "what"), [
+    ([[0, 0, 1, 1, 1]], [[0, 0, 2, 2, 2]], None),
+    ([[0, 0, 0, 0, 0]], [[0, 0, 0, 0, 0]], None),
+    ([[0, 1, 2, 3, 4]], [[0, 1, 2, 3, 4]], None),
+    ([[1, 1, 2, 2, 2]], [[0, 0, 2, 2, 2]], "start at 0"),
+    ([[0, 0, 2, 2, 2]], [[0, 0, 2, 2, 2]], "contiguous"),
+    ([[0, 0, 1, 1, 0]], [[0, 0, 2, 2, 4]], "contiguous"),
+    ([[0, 0, 1, 1, 1]], [[0, 0, 2, 2, 3]], "seg_start"),
+    ([[0, 0, 1, 1, 1]], [[0, 0, 0, 0, 0]], "seg_start"),
+    ([[0, 0, 1, 1, 1]], [[-1, 0, 2, 2, 2]], "seg_start"),
+    ([[0, 0, 1, 1, 1], [0, 1, 1, 1, 1]], [[0, 0, 2, 2, 2], [0, 1, 1, 1, 2]], "seg_start"),
+])
+def test_packed_layout_contract(sid, sst, what):
+    """layout_violation accepts exactly the PackedMask contract; flash_attention refuses a violating
+    layout with AttentionInputError (the kernels mask by seg_start ranges, the oracle by seg_id, so
+    the two agree only on valid layouts), and skips the check when asked to."""
+    from mlx_train_perf.attention.segments import layout_violation
+
+    sid_t = torch.tensor(sid, dtype=torch.int32)
+    sst_t = torch.tensor(sst, dtype=torch.int32)
+    got = layout_violation(sid_t, sst_t)
+    if what is None:
+        assert got is None
+        return
+    assert got is not None and what in got
+    b = sid_t.shape[0]
+    q, k, v = _attn(b=b, n=5)
+    with pytest.raises(AttentionInputError, match="layout contract"):
+        flash_attention(q, k, v, scale=1.0, impl="reference", segments=PackedMask(seg_id=sid_t, seg_start=sst_t))
+    flash_attention(q, k, v, scale=1.0, impl="reference", segments=PackedMask(seg_id=sid_t, seg_start=sst_t),
+                    validate_segments=False)
+
+
+def test_packed_layout_check_runs_again_after_in_place_edit():
+    from mlx_train_perf.attention import api
+
+    sid, sst = oa.segments_from_lengths([2, 3])
+    pm = PackedMask(seg_id=sid[None].clone(), seg_start=sst[None].clone())
+    q, k, v = _attn(n=5)
+    flash_attention(q, k, v, scale=1.0, impl="reference", segments=pm)
+    assert api._layout_seen(pm)
+    pm.seg_start[0, 4] = 3   # breaks the contract in place
+    assert not api._layout_seen(pm)
+    with pytest.raises(AttentionInputError):
+        flash_attention(q, k, v, scale=1.0, impl="reference", segments=pm)

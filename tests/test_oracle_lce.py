@@ -129,3 +129,22 @@ def test_dw_matches_autograd_of_naive():
     nll = olce.naive_linear_ce(h.double(), ww, safe, dtype=torch.float64)
     (nll * torch.where(t == -100, 0.0, ct.double())).sum().backward()
     assert torch.allclose(dw, ww.grad, atol=1e-12)
+
+
+def test_reduce_mean_hand_computed():
+    """reduce_mean: sum of the non-ignored rows over their count, by hand. Rows 1 and 3 are ignored;
+    the kept rows hold 1.5, 4.0 and 0.5, so the mean is 6.0 / 3 = 2.0. A version that divided by all
+    rows (1.2 with the ignored rows' 0 nll, 2.4 if they kept their values) or summed the ignored rows
+    (12.0 / 3) fails; all ignored gives 0, not a division by zero."""
+    nll = torch.tensor([1.5, 7.0, 4.0, -1.0, 0.5], dtype=torch.float64)
+    t = torch.tensor([3, -100, 0, -100, 9])
+    assert olce.reduce_mean(nll, t).item() == 2.0
+    assert olce.reduce_mean(nll, t, ignore_index=9).item() == (1.5 + 7.0 + 4.0 - 1.0) / 4
+    assert olce.reduce_mean(nll, torch.full((5,), -100)).item() == 0.0
+    # it is the public reduction="mean" of the forward's per-row nll (ignored rows excluded)
+    from mlx_train_perf import DenseHead, linear_cross_entropy
+
+    h, w, tt = lce_inputs(40, 16, 50, seed=6, ignore_frac=0.25)
+    got = linear_cross_entropy(h.float(), DenseHead(weight=w.float()), tt, impl="naive", reduction="mean")
+    onll, _, _ = olce.forward(h, w, tt)
+    assert abs(got.item() - olce.reduce_mean(onll, tt).item()) < 1e-6
