@@ -11,12 +11,13 @@
  * Conventions (all entry points):
  *   - Plain pointers and sizes; the caller allocates every tensor and the workspace and owns the
  *     stream (a hipStream_t passed as void*; NULL = the default stream). The library never
- *     allocates device memory and never synchronizes the host.
+ *     allocates device memory and never synchronizes the host. (mtp_lce_fwd_noalloc takes no
+ *     workspace: it uses a fixed device array the library holds per GPU.)
  *   - Tensors are dense row-major; bf16 values are stored as uint16 bit patterns.
  *   - Return 0 on success or a negative MTP_ERR_* code; mtp_last_error() then returns a
  *     thread-local message naming the offending argument.
  *   - Calls are stream-ordered and re-entrant: there is no global mutable state besides the
- *     thread-local error message.
+ *     thread-local error message and mtp_lce_fwd_noalloc's per-GPU scratch array.
  */
 #ifndef MTP_HIP_H
 #define MTP_HIP_H
@@ -66,6 +67,21 @@ int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
                 const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
                 int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt,
                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Forward as mtp_lce_fwd, allocating nothing and taking no workspace: the per-split partials live
+ * in a fixed device array inside the library (one per GPU, held until the process ends), whose size
+ * mtp_lce_fwd_noalloc_max_workspace_bytes() returns (4 MiB: n up to 524288 tokens at any v). A call
+ * whose mtp_lce_fwd_workspace_bytes(n, d, v, head_kind) exceeds it returns MTP_ERR_WORKSPACE before
+ * any launch. The first call on a device looks up that device's array address (no allocation).
+ * Outputs are bitwise those of mtp_lce_fwd. Calls on one GPU share its array: two calls whose work
+ * overlaps in time on that GPU (different streams, or different host threads) race on it.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). */
+int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
+                        const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                        int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt,
+                        void* stream);
+size_t mtp_lce_fwd_noalloc_max_workspace_bytes(void);
 
 /* Vocab columns per backward chunk for a workspace budget (bytes); a multiple of 256. */
 int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);

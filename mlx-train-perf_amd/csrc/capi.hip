@@ -5,8 +5,18 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "../../include/mtp_hip.h"
 #include "mtp_launch.hpp"
+
+// Scratch of mtp_lce_fwd_noalloc: the forward's per-(vocab split, token) partial maxima and sums,
+// held in a file-scope device array so that entry point allocates nothing. Each GPU the library
+// runs on holds its own copy until the process ends. The host may not pass the array's name to a
+// kernel (in host code it is a stand-in, not a device address): its device address, per device, is
+// looked up once with hipGetSymbolAddress and used everywhere host code needs the array.
+static constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
 
 namespace {
 
@@ -81,6 +91,28 @@ int check_attn(const void* q, const void* k, const void* v, int64_t b, int64_t h
   return MTP_OK;
 }
 
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+int scratch_for_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(MTP_ERR_RUNTIME, "device index %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(MTP_ERR_RUNTIME, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return MTP_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -108,6 +140,30 @@ int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
   hipError_t e = mtp::launch_lce_fwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
                                      targets, (int)n, (int)d, (int)v, (long long)ignore_index, nll, lse, tgt,
                                      static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t mtp_lce_fwd_noalloc_max_workspace_bytes(void) { return kNoAllocScratchBytes; }
+
+int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
+                        const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                        int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt, void* stream) {
+  int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
+  if (rc) return rc;
+  if (!nll || !lse || !tgt) return fail(MTP_ERR_INPUT, "nll, lse, tgt outputs must be non-null");
+  const size_t need = lce_fwd_ws(n, v);
+  if (need > kNoAllocScratchBytes)
+    return fail(MTP_ERR_WORKSPACE, "mtp_lce_fwd_noalloc: n=%lld, v=%lld needs %zu bytes of scratch, above its fixed "
+                "%zu; use mtp_lce_fwd with a caller workspace", (long long)n, (long long)v, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  rc = scratch_for_current_device(&ws);
+  if (rc) return rc;
+  // Every partial the forward reads is written by the same launch before it is read (one entry
+  // per vocab split and token), so the scratch needs no clearing between calls.
+  hipError_t e = mtp::launch_lce_fwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
+                                     targets, (int)n, (int)d, (int)v, (long long)ignore_index, nll, lse, tgt,
+                                     static_cast<float*>(ws), static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce forward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
