@@ -176,7 +176,7 @@ def bench_lce(steps, warmup, head_kind="dense"):
     p = plan.lce_plan(n=N, v=V, d=D)
     from mlx_train_perf.core import loss as _loss
 
-    head_t = sum(e[1].numel() * e[1].element_size() for e in _loss._HEAD_T_CACHE.values())
+    head_t = _loss.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_kernel_ms": fwd_kernel_ms,
             "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9,
             "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks, "transposed_head_cache_gb": head_t / 1e9}

@@ -115,15 +115,9 @@ __device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
                  "+v"(f[3][0]), "+v"(f[3][1]), "+v"(f[3][2]), "+v"(f[3][3]));
 }
 
-// The dQ kernel stages one K/V tile in LDS (51 KiB at head_dim 128) and prefetches the next into
-// registers, so two workgroups (8 waves) share a CU; MTP_DQ_BUFS=2 double-buffers instead.
-#ifndef MTP_DQ_BUFS
-#define MTP_DQ_BUFS 1
-#endif
-// The dK/dV kernel processes each 64-query tile as two 32-query halves (fewer live registers).
-#ifndef MTP_DKV_HALVES
-#define MTP_DKV_HALVES 1
-#endif
+// The dQ kernel (head_dim 64 and 96) stages one K/V tile in LDS and prefetches the next into
+// registers, so two workgroups (8 waves) share a CU. The dK/dV kernel processes each 64-query tile
+// as two 32-query halves (fewer live registers).
 
 template <int DH>
 struct AttnCfg {
@@ -397,15 +391,14 @@ __global__ __launch_bounds__(256) void attn_bwd_dvec_kernel(const bf16_t* __rest
 // Backward dQ (query-row owners; no atomics).
 // ------------------------------------------------------------------------------------------
 template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(MTP_DQ_BUFS == 1 ? 2 : 1, MTP_DQ_BUFS == 1 ? 2 : 1)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                         const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
                         const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                         bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
   using C = AttnCfg<DH>;
   constexpr int kStage = 2 * C::kNatBytes + C::kTBytes + 256;  // K, V natural; K^T; key segment ids
-  constexpr int kBufs = MTP_DQ_BUFS;
-  __shared__ __attribute__((aligned(16))) char lds[kBufs * kStage];
+  __shared__ __attribute__((aligned(16))) char lds[kStage];
 
   const int G = Hq / Hkv;
   const int hpw = heads_per_wg(G);
@@ -493,7 +486,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
   }
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
-    const char* cur = lds + (kBufs == 2 ? (t & 1) * kStage : 0);
+    const char* cur = lds;
     const int kv0 = kv_begin + t * kKT;
     const bool more = t + 1 < ntiles;
     if (more) load_tile(t + 1);
@@ -536,15 +529,10 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) acc[db] = mfma32(t_frag(kt, 32 * db + col, ks, hf), sf[ks], acc[db]);
     }
-    if constexpr (kBufs == 2) {
-      if (more) store_tile(lds + ((t + 1) & 1) * kStage);
+    __syncthreads();
+    if (more) {
+      store_tile(lds);
       __syncthreads();
-    } else {
-      __syncthreads();
-      if (more) {
-        store_tile(lds);
-        __syncthreads();
-      }
     }
   }
 
@@ -689,7 +677,6 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
       const int* segs = reinterpret_cast<const int*>(l2s + 128);
       const char* qt = cur + 2 * C::kNatBytes;
       const char* dt = qt + C::kTBytes;
-#if MTP_DKV_HALVES
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         f32x16 sacc, pacc;
@@ -731,51 +718,6 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
             dka[db] = mfma32(t_frag(qt, 32 * db + col, 2 * qb + kk, hf), sf[kk], dka[db]);
           }
       }
-#else
-      f32x16 sacc[2], pacc[2];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[qb][r] = 0.f;
-          pacc[qb][r] = 0.f;
-        }
-#pragma unroll
-        for (int ks = 0; ks < C::kDK; ++ks) {
-          sacc[qb] = mfma32(nat_frag<DH>(cur, 32 * qb + col, ks, hf), kf[ks], sacc[qb]);
-          pacc[qb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * qb + col, ks, hf), vf[ks], pacc[qb]);
-        }
-      }
-      bf16x8 pf[4], sf[4];
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int r = 4 * rq + u;
-            float p = fast_exp2(sacc[qb][r] * scale_log2 - l4[u]);
-            if (need_mask) {
-              const int qq = q0 + ql0 + u;
-              bool ok = (kj <= qq) && (qq < S) && kvalid;
-              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
-              if (!ok) p = 0.f;
-            }
-            pf[2 * qb + (r >> 3)][r & 7] = (__bf16)p;
-            sf[2 * qb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[qb][r] - d4[u]));
-          }
-        }
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          dva[db] = mfma32(t_frag(dt, 32 * db + col, ks, hf), pf[ks], dva[db]);
-          dka[db] = mfma32(t_frag(qt, 32 * db + col, ks, hf), sf[ks], dka[db]);
-        }
-#endif
     }
     if (more) store_tile(lds + ((it + 1) & 1) * kStage);
     __syncthreads();
@@ -799,32 +741,18 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward dK, dV for head_dim 128, DMA-fed. Same ownership and math as attn_bwd_dkv_kernel; the
-// 64-query Q and dO tiles are copied global -> LDS by buffer_load ... lds (16 bytes per lane, rows
-// past S read as zeros) into 256 B rows whose 16-byte chunks are XOR-swizzled by
-// sw(r) = 4 (r & 3) + ((r >> 2) & 3): a bijection over any 16 consecutive rows (row fragments, 16
-// lanes per LDS cycle) that also sends the aligned 4-chunk block of each of 4 consecutive rows to a
-// different quarter of the banks (transposed fragments, 32 lanes x 8 bytes per LDS cycle). Row
-// fragments (S = Q K^T, dP = dO V^T) are ds_read_b128; the transposed operands of dV += dO^T P and
-// dK += Q^T dS are ds_read_b64_tr_b16 of the same tiles. The two reads of a transposed fragment
-// start at query rows 4 hf and 4 hf + 8 of each 16-row slab, which is the order of the
-// probability / dS registers (MFMA accumulator rows), so no permuted copy of the tiles is kept.
-//
-// One wave per SIMD, so the wave overlaps its own phases. A 64-query tile is two 32-query halves,
-// software-pipelined as
-//   P1: S, dP of half 0                     | row fragments of half 1, per-query scalars
-//   P2: S, dP of half 1                     | probabilities and dS of half 0, its transposed reads
-//   P3: dV, dK of half 0                    | probabilities and dS of half 1, its transposed reads
-//   (one barrier: the next tile's copies have landed, this tile's buffer is free)
-//   P4: dV, dK of half 1                    | row fragments of half 0 of the next tile
-// so the MFMA pipe always has independent work beside the VALU and LDS traffic. Whether a tile
-// needs masking is decided per wave (scalar branches around two small blocks that set the hidden
-// scores of a half to -inf): only tiles that cross the wave's diagonal, the sequence end or (packed) the end of
-// a key's segment compare positions. Packed: with contiguous, gapless segments, query q shares key
-// k's segment and q >= k iff k <= q < seg_end(k), the first position whose seg_start exceeds k, so
-// the mask is a range test on a per-lane limit. Waits are compiler-visible builtins (an inline-asm
-// wait is opaque to the compiler's own wait insertion, which then keeps older loads outstanding and
-// waits for the in-flight copies of the next tile too).
+// Operand tiles of the head_dim-128 backward: 64-query Q and dO tiles are copied global -> LDS by
+// buffer_load ... lds (16 bytes per lane, rows past S read as zeros) into 256 B rows whose 16-byte
+// chunks are XOR-swizzled by sw(r) = 4 (r & 3) + ((r >> 2) & 3): a bijection over any 16
+// consecutive rows (row fragments, 16 lanes per LDS cycle) that also sends the aligned 4-chunk block
+// of each of 4 consecutive rows to a different quarter of the banks (transposed fragments, 32 lanes
+// x 8 bytes per LDS cycle). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128; the transposed
+// operands of dV += dO^T P and dK += Q^T dS are ds_read_b64_tr_b16 of the same tiles. The two reads
+// of a transposed fragment start at query rows 4 hf and 4 hf + 8 of each 16-row slab, which is the
+// order of the probability / dS registers (MFMA accumulator rows), so no permuted copy of a tile is
+// kept. Packed: with contiguous, gapless segments, query q shares key k's segment and q >= k iff
+// k <= q < seg_end(k), the first position whose seg_start exceeds k, so the mask is a range test on
+// a per-lane limit.
 // ------------------------------------------------------------------------------------------
 namespace dkv128 {
 constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
@@ -843,308 +771,6 @@ __device__ __forceinline__ int first_above(const int32_t* a, int lo, int hi, int
 }
 }  // namespace dkv128
 
-template <bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                            const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
-                            const float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
-                            const int32_t* __restrict__ seg_start, bf16_t* __restrict__ dk, bf16_t* __restrict__ dv,
-                            int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
-  using namespace dkv128;
-  constexpr int DH = 128;
-  constexpr int kDK = DH / 16, kDB = DH / 32;
-  // The two stages are separate arrays and the tile loop is unrolled by two, so every LDS read
-  // names its stage statically: the compiler then knows the reads of one stage do not alias the
-  // copies in flight into the other, and inserts no wait for those copies before them.
-  __shared__ __attribute__((aligned(1024))) char lds0[kStage];
-  __shared__ __attribute__((aligned(1024))) char lds1[kStage];
-
-  const int G = Hq / Hkv;
-  const int nkv = B * Hkv;
-  const int g = blockIdx.x;
-  const int kvi = g % nkv;
-  const int ktile = g / nkv;  // earliest keys (most work under the causal mask) first
-  const int bidx = kvi / Hkv;
-  const int kvh = kvi % Hkv;
-  const int k0 = ktile * 128;
-
-  const int tid = threadIdx.x;
-  // The wave index is read as a scalar so the per-wave masking decision is a scalar branch.
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hf = lane >> 5, col = lane & 31;
-  const int kw0 = k0 + 32 * w;
-  const int kj = kw0 + col;
-  const bool kvalid = kj < S;
-
-  const long krow = (long)(bidx * Hkv + kvh) * S;
-  const bf16_t* kh = k + krow * DH;
-  const bf16_t* vh = v + krow * DH;
-  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
-
-  bf16x8 kf[kDK], vf[kDK];
-#pragma unroll
-  for (int ks = 0; ks < kDK; ++ks) {
-    kf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(kh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-    vf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(vh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-  }
-
-  const int q_begin = (k0 / kKT) * kKT;
-  int q_end = S;
-  if (PACKED) {
-    const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
-    q_end = __builtin_amdgcn_readfirstlane(first_above(sst, 0, S, klast));
-  }
-  // Queries q with kj <= q < my_lim see key kj; w_lim is the wave's smallest limit (its first key's:
-  // segment ends do not decrease along the keys).
-  int my_lim = S, w_lim = S;
-  if (PACKED) {
-    my_lim = kvalid ? first_above(sst, kj, q_end, kj) : S;
-    w_lim = __builtin_amdgcn_readfirstlane(my_lim);
-  }
-  const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
-  const int niter = G * ntq;
-
-  f32x16 dka[kDB], dva[kDB];
-#pragma unroll
-  for (int db = 0; db < kDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dka[db][r] = 0.f;
-      dva[db][r] = 0.f;
-    }
-
-  // Copy lanes: wave w issues 4 x 1 KiB per tile and operand (rows 4 (4 j + w) .. +3).
-  uint32_t coff[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = 4 * (4 * j + w) + (lane >> 4);
-    coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
-  }
-  // Row-fragment lane offsets (per k16 step ks): row = 32 qb + col, chunk 2 ks + hf.
-  int ro[kDK];
-#pragma unroll
-  for (int ks = 0; ks < kDK; ++ks) ro[ks] = col * kRowB + (((2 * ks + hf) ^ sw(col & 15)) << 4);
-  // Transposed-fragment lane offsets: read t covers rows 4 hf + 8 t + (s >> 2) of a 16-row slab,
-  // columns 32 db + 16 (g & 1) + 4 (s & 3) (g = lane >> 4, s = lane & 15).
-  int tro[2][kDB];
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
-    const int swt = sw(rl);
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      const int c = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-      tro[t][db] = rl * kRowB + ((c ^ swt) << 4) + 8 * (lane & 1);
-    }
-  }
-
-  // Copies of tile `it` into stage `st`; a copy that is not `live` gets a zero-byte range (no
-  // memory access) so the call needs no branch.
-  auto issue = [&](int it, char* st, bool live) {
-    const int itc = live ? it : 0;
-    const int hh = itc / ntq, tq = itc % ntq;
-    const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
-    const int q0 = q_begin + tq * kKT;
-    const int bytes = live ? ((S - q0 < kKT) ? S - q0 : kKT) * kRowB : 0;
-    const char* qb_ = reinterpret_cast<const char*>(q + (qrow + q0) * DH);
-    const char* db_ = reinterpret_cast<const char*>(d_o + (qrow + q0) * DH);
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(qb_), (short)0, bytes, 0x00020000);
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(db_), (short)0, bytes, 0x00020000);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (__attribute__((address_space(3))) void*)(st + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (__attribute__((address_space(3))) void*)(st + kTile + 1024 * (4 * j + w)), 16, coff[j], 0, 0, 0);
-    }
-  };
-  // Per-query scalars of a tile (wave 0): raw loads now, stored to the stage after the barrier.
-  float lse_reg = 0.f, d_reg = 0.f;
-  auto load_scal = [&](int it) {
-    if (tid < kKT) {
-      const int hh = it / ntq, tq = it % ntq;
-      const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
-      const int qq = q_begin + tq * kKT + tid;
-      const bool ok = qq < S;
-      lse_reg = ok ? lse[qrow + qq] : 0.f;
-      d_reg = ok ? dvec[qrow + qq] : 0.f;
-    }
-  };
-  auto store_scal = [&](char* st) {
-    if (tid < kKT) {
-      float* sc = reinterpret_cast<float*>(st + 2 * kTile);
-      sc[tid] = lse_reg * kLog2e;
-      sc[64 + tid] = d_reg;
-    }
-  };
-
-  if (niter <= 0) {
-    // No visible query: dK = dV = 0.
-  } else {
-    issue(0, lds0, true);
-    load_scal(0);
-    store_scal(lds0);
-    issue(1, lds1, niter > 1);
-    if (niter > 1) load_scal(1);
-    vm_wait0();
-    if (niter > 1) store_scal(lds1);
-    lgkm_wait0();
-    asm volatile("s_barrier" ::: "memory");
-  }
-  // The kernel-start K/V fragment loads are complete here (vmcnt(0) above): tell the compiler.
-#pragma unroll
-  for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(kf[ks]), "+v"(vf[ks]));
-
-  // Row fragments of half qb of the tile at `st`.
-  bf16x8 rqf[kDK], rdf[kDK];
-  auto read_rows = [&](const char* st, int qb, bf16x8 (&fq)[kDK], bf16x8 (&fd)[kDK]) {
-#pragma unroll
-    for (int ks = 0; ks < kDK; ++ks) {
-      fq[ks] = as_bf16x8(lds_read16(st, 32 * qb * kRowB + ro[ks]));
-      fd[ks] = as_bf16x8(lds_read16(st + kTile, 32 * qb * kRowB + ro[ks]));
-    }
-  };
-  auto sdp = [&](const bf16x8 (&fq)[kDK], const bf16x8 (&fd)[kDK], f32x16& sacc, f32x16& pacc) {
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      sacc[r] = 0.f;
-      pacc[r] = 0.f;
-    }
-#pragma unroll
-    for (int ks = 0; ks < kDK; ++ks) {
-      sacc = mfma32(fq[ks], kf[ks], sacc);
-      pacc = mfma32(fd[ks], vf[ks], pacc);
-    }
-  };
-  // Transposed fragments of half qb: [kk][db] for dO^T (x) and Q^T (y).
-  auto read_tr = [&](const char* st, int qb, bf16x8 (&x)[2][kDB], bf16x8 (&y)[2][kDB]) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const int slab = (32 * qb + 16 * kk) * kRowB;
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        const bf16x4 a0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + kTile + slab + tro[0][db]));
-        const bf16x4 a1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + kTile + slab + tro[1][db]));
-        const bf16x4 b0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + slab + tro[0][db]));
-        const bf16x4 b1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(st + slab + tro[1][db]));
-        x[kk][db] = bf16x8{a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-        y[kk][db] = bf16x8{b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3]};
-      }
-    }
-  };
-  auto dvdk = [&](const bf16x8 (&x)[2][kDB], const bf16x8 (&y)[2][kDB], const bf16x8 (&pf)[2], const bf16x8 (&sf)[2]) {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) {
-        dva[db] = mfma32(x[kk][db], pf[kk], dva[db]);
-        dka[db] = mfma32(y[kk][db], sf[kk], dka[db]);
-      }
-  };
-
-  if (niter > 0) read_rows(lds0, 0, rqf, rdf);
-  // Tile `it` runs on stage it & 1. An odd tile count gets one phantom tile at the end: its copy is
-  // zero bytes (Q and dO rows read as zeros) and every pair is hidden, so it adds exactly zero.
-  auto body = [&](auto stage, int it) {
-    char* cur = decltype(stage)::value ? lds1 : lds0;
-    char* nxt = decltype(stage)::value ? lds0 : lds1;
-    const bool phantom = it >= niter;
-    const int q0 = q_begin + (it % ntq) * kKT;
-    const bool more2 = it + 2 < niter;
-    if (more2) load_scal(it + 2);
-    // Query row 32 qb + 8 rq + 4 hf + u of the tile is visible to this lane's key iff
-    // c = 32 qb + 8 rq + u satisfies thr <= c < lim.
-    const int thr = (kvalid && !phantom) ? kj - q0 - 4 * hf : (1 << 20);
-    const int lim = my_lim - q0 - 4 * hf;
-    const bool need_mask = phantom || (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && q0 + kKT > w_lim);
-    const float* l2s = reinterpret_cast<const float*>(cur + 2 * kTile);
-    const float* ds_ = l2s + 64;
-
-    // Per-query L log2(e) and D of half qb, rows 8 rq + 4 hf + 0..3.
-    auto scal = [&](int qb, f32x4 (&l4)[4], f32x4 (&d4)[4]) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int ql0 = 32 * qb + 8 * rq + 4 * hf;
-        l4[rq] = *reinterpret_cast<const f32x4*>(l2s + ql0);
-        d4[rq] = *reinterpret_cast<const f32x4*>(ds_ + ql0);
-      }
-    };
-    // Scores of hidden pairs of half qb set to -inf, so that their probabilities are exp2(-inf) = 0.
-    auto mask = [&](int qb, f32x16& sacc) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int c = 32 * qb + 8 * rq + u;
-          sacc[4 * rq + u] = (c >= thr && c < lim) ? sacc[4 * rq + u] : kNegInf;
-        }
-    };
-    auto probs = [&](const f32x16& sacc, const f32x16& pacc, const f32x4 (&l4)[4], const f32x4 (&d4)[4],
-                     bf16x8 (&pf)[2], bf16x8 (&sf)[2]) {
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int r = 4 * rq + u;
-          const float p = fast_exp2(__builtin_fmaf(sacc[r], scale_log2, -l4[rq][u]));
-          pf[r >> 3][r & 7] = (__bf16)p;
-          sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[rq][u]));
-        }
-    };
-
-    // P1: S, dP of half 0 | row fragments of half 1, scalars of half 0.
-    f32x16 s0, p0, s1, p1;
-    bf16x8 rqf1[kDK], rdf1[kDK];
-    f32x4 la[4], da[4], lb[4], db4[4];
-    sdp(rqf, rdf, s0, p0);
-    read_rows(cur, 1, rqf1, rdf1);
-    scal(0, la, da);
-    if (need_mask) mask(0, s0);
-    // P2: S, dP of half 1 | probabilities and dS of half 0, its transposed reads.
-    bf16x8 pf0[2], sf0[2], pf1[2], sf1[2];
-    bf16x8 x0[2][kDB], y0[2][kDB], x1[2][kDB], y1[2][kDB];
-    sdp(rqf1, rdf1, s1, p1);
-    probs(s0, p0, la, da, pf0, sf0);
-    read_tr(cur, 0, x0, y0);
-    scal(1, lb, db4);
-    if (need_mask) mask(1, s1);
-    // P3: dV, dK of half 0 | probabilities and dS of half 1, its transposed reads.
-    dvdk(x0, y0, pf0, sf0);
-    probs(s1, p1, lb, db4, pf1, sf1);
-    read_tr(cur, 1, x1, y1);
-    // Every read of `cur` has returned and this wave's copies of the next tile have landed;
-    // after the barrier `cur` receives the tile after next.
-    lgkm_wait0();
-    vm_wait0();
-    asm volatile("s_barrier" ::: "memory");
-    // Scalars first: a store after the copy into the same stage would wait for that copy.
-    if (more2) store_scal(cur);
-    issue(it + 2, cur, more2);
-    // P4: dV, dK of half 1 | row fragments of half 0 of the next tile (stale when there is none;
-    // never used then).
-    read_rows(nxt, 0, rqf, rdf);
-    dvdk(x1, y1, pf1, sf1);
-  };
-  for (int it = 0; it < niter; it += 2) {
-    body(std::integral_constant<int, 0>{}, it);
-    body(std::integral_constant<int, 1>{}, it + 1);
-  }
-
-  if (kvalid) {
-    bf16_t* ko = dk + (krow + kj) * DH;
-    bf16_t* vo = dv + (krow + kj) * DH;
-#pragma unroll
-    for (int db = 0; db < kDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        *reinterpret_cast<u32x2*>(ko + d) =
-            u32x2{pack_bf16x2(dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale),
-                  pack_bf16x2(dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale)};
-        *reinterpret_cast<u32x2*>(vo + d) = u32x2{pack_bf16x2(dva[db][4 * rq], dva[db][4 * rq + 1]),
-                                                  pack_bf16x2(dva[db][4 * rq + 2], dva[db][4 * rq + 3])};
-      }
-  }
-}
-
 // ------------------------------------------------------------------------------------------
 // Backward dK, dV for head_dim 128, operand-split: 8 waves per 128-key workgroup, two per SIMD.
 // Waves 0-3 ("P waves") own 32 keys each and hold K: S = Q K^T, P = exp2(S scale log2 e - L log2 e)
@@ -1155,8 +781,7 @@ void attn_bwd_dkv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
 // (dV) and starts tile t+1 (S, P), the dS wave finishes tile t (dS, dK) and starts tile t+1 (dP),
 // so each has 32 products with its probability or dS arithmetic between them, and the SIMD
 // overlaps the arithmetic of one with the products of the other. Q and dO tiles are copied
-// global -> LDS exactly as in attn_bwd_dkv128_kernel (same swizzle and fragment reads) into a ring
-// of three stages, the copy of tile t+3 issued when tile t's stage is released; P goes through a
+// global -> LDS in the layout above (same swizzle and fragment reads) into a ring of three stages, the copy of tile t+3 issued when tile t's stage is released; P goes through a
 // ring of three LDS buffers. The loop is unrolled by three so every stage is named statically.
 // ------------------------------------------------------------------------------------------
 namespace dkvab {
@@ -1844,15 +1469,6 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 // Launchers
 // ------------------------------------------------------------------------------------------
 namespace {
-// dK/dV at head_dim 128: the operand-split kernel (8 waves) unless MTP_DKV_SPLIT=0.
-bool dkv_split() {
-  static const bool on = [] {
-    const char* e = getenv("MTP_DKV_SPLIT");
-    return !(e && e[0] == '0');
-  }();
-  return on;
-}
-
 int fwd_grid(const AttnShape& sh) {
   const int G = sh.hq / sh.hkv;
   const int hpw = (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1);
@@ -1901,13 +1517,8 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   if (e != hipSuccess) return e;
   dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
   if constexpr (DH == 128) {
-    if (dkv_split()) {
-      if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-      else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-      return hipGetLastError();
-    }
-    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_kernel<true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_bwd_dkv128_kernel<false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
     return hipGetLastError();
   }
   if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);

@@ -485,13 +485,11 @@ __device__ __forceinline__ void dma_mfma(const bf16x8 (&fa)[4], const bf16x8 (&f
 // Interleave the 8 MFMAs of a k-step with the NR LDS reads of the next one. The reads are packed
 // into the first FRONT MFMAs so that they complete before the next k-step needs them (FRONT = 6
 // measured best at the flagship: step 23.9 ms against 24.4 ms with 4 and 24.1 ms with 8).
-#ifndef MTP_DMA_FRONT
-#define MTP_DMA_FRONT 6
-#endif
+constexpr int kDmaFront = 6;
 template <int NR, int S = 0>
 __device__ __forceinline__ void dma_sched() {
   if constexpr (S < 8) {
-    constexpr int F = MTP_DMA_FRONT;
+    constexpr int F = kDmaFront;
     __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
     constexpr int r = S < F ? NR * (S + 1) / F - NR * S / F : 0;
     if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);

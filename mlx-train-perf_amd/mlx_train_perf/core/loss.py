@@ -16,6 +16,7 @@ MI355X specifics:
 from __future__ import annotations
 
 import os
+import threading
 import weakref
 from dataclasses import dataclass
 from typing import Literal
@@ -228,18 +229,33 @@ def _chunked_nll(hidden2, head, targets2, ignore_index, chunk_size):
 
 VJP_CALLS: dict[str, int] = {}
 
-# Transposed copies of heads for the backward's dH product (mtp_lce_head_transpose), one per device:
-# (owner weakref, data_ptr, shape, version) -> bf16 [D][mtp_lce_head_t_ld(V)]. The owner is the
-# caller's weight tensor (the packed w_q of a 4-bit head, whose copy holds the dequantized values);
-# an in-place update through it bumps its version and invalidates the entry. A frozen head is
-# therefore transposed once; a trainable one after every optimizer step.
-_HEAD_T_CACHE: dict[int, tuple[tuple, torch.Tensor]] = {}
+# Transposed copies of heads for the backward's dH product (mtp_lce_head_transpose): per device, a
+# short most-recently-used list of (owner weakref, data_ptr, shape, version) -> bf16
+# [D][mtp_lce_head_t_ld(V)]. The owner is the caller's weight tensor (the packed w_q of a 4-bit head,
+# whose copy holds the dequantized values); an in-place update through it bumps its version and
+# replaces its entry. A frozen head is therefore transposed once; a trainable one after every
+# optimizer step. Up to MTP_LCE_HEAD_T_CACHE heads (default 2) are kept per device, so two models
+# (or a model and its reference copy) on one GPU do not evict each other on every call; entries of
+# heads that were freed are dropped. Guarded by a lock: trainer threads may share a device.
+_HEAD_T_CACHE: dict[int, list[tuple[tuple, torch.Tensor]]] = {}
+_HEAD_T_LOCK = threading.Lock()
+
+
+def _head_t_capacity() -> int:
+    return max(1, int(os.environ.get("MTP_LCE_HEAD_T_CACHE", "2")))
 
 
 def clear_transposed_head_cache() -> None:
     """Drop the cached transposed heads (e.g. after changing a head through `.data`, which does not
     bump the tensor's version counter)."""
-    _HEAD_T_CACHE.clear()
+    with _HEAD_T_LOCK:
+        _HEAD_T_CACHE.clear()
+
+
+def transposed_head_cache_bytes() -> int:
+    """Device bytes held by the cached transposed heads, over all devices."""
+    with _HEAD_T_LOCK:
+        return sum(t.numel() * t.element_size() for ents in _HEAD_T_CACHE.values() for _, t in ents)
 
 
 def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_kind: int, v: int,
@@ -248,17 +264,22 @@ def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_ki
         return None
     dev = owner.device.index if owner.device.index is not None else torch.cuda.current_device()
     key = (owner.data_ptr(), tuple(owner.shape), owner._version)
-    ent = _HEAD_T_CACHE.get(dev)
-    if ent is not None and ent[0][0]() is owner and ent[0][1:] == key:
-        return ent[1]
-    _HEAD_T_CACHE.pop(dev, None)
-    lib = _native.load()
-    wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=owner.device)
-    rc = lib.mtp_lce_head_transpose(_native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases), v, d,
-                                    head_kind, wt.data_ptr(), _native.stream_of(owner))
-    _native.check(rc, domain="loss")
-    _HEAD_T_CACHE[dev] = ((weakref.ref(owner),) + key, wt)
-    return wt
+    with _HEAD_T_LOCK:
+        ents = _HEAD_T_CACHE.setdefault(dev, [])
+        # drop entries whose head was freed, and this head's entry from before an in-place update
+        ents[:] = [e for e in ents if e[0][0]() is not None and not (e[0][0]() is owner and e[0][1:] != key)]
+        for i, e in enumerate(ents):
+            if e[0][0]() is owner:
+                ents.append(ents.pop(i))
+                return e[1]
+        lib = _native.load()
+        wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=owner.device)
+        rc = lib.mtp_lce_head_transpose(_native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases),
+                                        v, d, head_kind, wt.data_ptr(), _native.stream_of(owner))
+        _native.check(rc, domain="loss")
+        ents.append(((weakref.ref(owner),) + key, wt))
+        del ents[:-_head_t_capacity()]
+        return wt
 
 
 class _KernelLCE(torch.autograd.Function):

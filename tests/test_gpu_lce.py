@@ -213,3 +213,41 @@ def test_transposed_head_cache_follows_in_place_updates(monkeypatch):
                                        bwd_chunk=1024)
     nll.backward(ct.cuda())
     assert rel_l2(hd.grad.float(), grads[1].float()) <= 2e-3
+
+
+def test_transposed_head_cache_keeps_two_heads():
+    """Two frozen heads used alternately on one device (two models) both stay cached: each is
+    transposed once, and freeing a head drops its entry."""
+    from mlx_train_perf.core import loss as L
+
+    print("[lce transposed-head cache: two heads]", flush=True)
+    L.clear_transposed_head_cache()
+    n, d, v = 256, 128, 2000
+    h, w1, t = lce_inputs(n, d, v, seed=101)
+    _, w2, _ = lce_inputs(n, d, v, seed=102)
+    heads = [L.DenseHead(weight=w.cuda(), trainable=False) for w in (w1, w2)]
+    per_head = d * L._native.load().mtp_lce_head_t_ld(v) * 2
+    ct = _cotangent(t)
+
+    def grad(i):
+        hd = h.cuda().requires_grad_(True)
+        nll, _, _ = L.kernel_forward_parts(hd, heads[i], t.cuda(), ignore_index=IGN)
+        nll.backward(ct.cuda())
+        return hd.grad.cpu()
+
+    for _ in range(2):
+        for i, w in enumerate((w1, w2)):
+            _, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
+            odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, dtype=torch.float64)
+            assert rel_l2(grad(i), odh) <= 1e-2
+        assert L.transposed_head_cache_bytes() == 2 * per_head
+    ents = L._HEAD_T_CACHE[torch.cuda.current_device()]
+    wts = sorted(e[1].data_ptr() for e in ents)
+    grad(0)
+    assert sorted(e[1].data_ptr() for e in ents) == wts   # reused, not rebuilt
+    del heads[1]
+    import gc
+
+    gc.collect()
+    grad(0)
+    assert L.transposed_head_cache_bytes() == per_head
