@@ -128,8 +128,9 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
  * contract of segments.py:9-19 applies: segment ids contiguous, ascending and gapless along each
  * row, seg_start[i] the first position of i's segment. Under it the rule equals
  * seg_start[i] <= j <= i, which the head_dim-128 kernels test (and all kernels use seg_start to
- * bound their loops, as the reference does). Both NULL means plain causal. causal must be 1 (the
- * reference kernel serves causal only, api.py:109-113).
+ * bound their loops, as the reference does). Both NULL means plain causal (causal = 1) or full
+ * attention (causal = 0: every key visible to every query; an extension -- the reference kernel
+ * serves causal only and refuses causal=False, api.py:109-113). Segments require causal = 1.
  * ------------------------------------------------------------------------------------------- */
 
 /* Forward: o = softmax(scale * q k^T + mask) v, lse = row logsumexp of the masked scaled scores.

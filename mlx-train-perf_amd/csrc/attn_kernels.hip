@@ -196,7 +196,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                      const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                      bf16_t* __restrict__ o, float* __restrict__ lse, int B, int Hq, int Hkv, int S,
-                     float scale_log2) {
+                     float scale_log2, int causal) {
   using C = AttnCfg<DH>;
   constexpr int kStage = C::kNatBytes + C::kTBytes + 256;
   __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
@@ -239,7 +239,7 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
                     : as_bf16x8(zero4());
 
   const int wg_q0 = pb * P;
-  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  const int wg_q1 = (causal && wg_q0 + P < S) ? wg_q0 + P : S;  // non-causal: every key
   int kv_begin = 0;
   if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
   const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
@@ -284,7 +284,7 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
     const int kv0 = kv_begin + t * kKT;
     const bool more = t + 1 < ntiles;
     if (more) load_tile(t + 1);
-    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
     if (!skip) {
       f32x16 sacc[2];
 #pragma unroll
@@ -294,7 +294,7 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
 #pragma unroll
         for (int ks = 0; ks < C::kDK; ++ks) sacc[kb] = mfma32(nat_frag<DH>(cur, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
       }
-      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
       const int* segs = reinterpret_cast<const int*>(cur + C::kNatBytes + C::kTBytes);
       float mt = kNegInf;
 #pragma unroll
@@ -305,7 +305,7 @@ void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k,
           if (need_mask) {
             const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
             const int j = kv0 + jl;
-            bool ok = (j <= qi) && (j < S) && qvalid;
+            bool ok = (!causal || j <= qi) && (j < S) && qvalid;
             if (PACKED) ok = ok && (segs[jl] == my_seg);
             if (!ok) x = kNegInf;
           }
@@ -395,7 +395,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                         const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
                         const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
-                        bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
+                        bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
   using C = AttnCfg<DH>;
   constexpr int kStage = 2 * C::kNatBytes + C::kTBytes + 256;  // K, V natural; K^T; key segment ids
   __shared__ __attribute__((aligned(16))) char lds[kStage];
@@ -443,7 +443,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
   const float dq_row = qvalid ? dvec[qrow + qi] : 0.f;
 
   const int wg_q0 = pb * P;
-  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  const int wg_q1 = (causal && wg_q0 + P < S) ? wg_q0 + P : S;  // non-causal: every key
   int kv_begin = 0;
   if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
   const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
@@ -490,7 +490,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
     const int kv0 = kv_begin + t * kKT;
     const bool more = t + 1 < ntiles;
     if (more) load_tile(t + 1);
-    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
     if (!skip) {
       f32x16 sacc[2], pacc[2];
 #pragma unroll
@@ -506,7 +506,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
           pacc[kb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * kb + col, ks, hf), df[ks], pacc[kb]);
         }
       }
-      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
       const int* segs = reinterpret_cast<const int*>(cur + 2 * C::kNatBytes + C::kTBytes);
       bf16x8 sf[4];
 #pragma unroll
@@ -517,7 +517,7 @@ void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__
           if (need_mask) {
             const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
             const int j = kv0 + jl;
-            bool ok = (j <= qi) && (j < S) && qvalid;
+            bool ok = (!causal || j <= qi) && (j < S) && qvalid;
             if (PACKED) ok = ok && (segs[jl] == my_seg);
             if (!ok) p = 0.f;
           }
@@ -569,7 +569,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
                          const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
                          const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                          bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
-                         float scale_log2, float scale) {
+                         float scale_log2, float scale, int causal) {
   using C = AttnCfg<DH>;
   // Q, dO natural; Q^T, dO^T; then L*log2e, D and segment ids of the 64 queries.
   constexpr int kStage = 2 * C::kNatBytes + 2 * C::kTBytes + 3 * 256;
@@ -606,7 +606,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
   }
   const int my_seg = (PACKED && kvalid) ? sid[kj] : -3;
 
-  const int q_begin = (k0 / kKT) * kKT;
+  const int q_begin = causal ? (k0 / kKT) * kKT : 0;  // non-causal: every query
   int q_end = S;
   if (PACKED) {
     const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
@@ -664,14 +664,14 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
     const int q0 = q_begin + (it % ntq) * kKT;
     const bool more = it + 1 < niter;
     if (more) load_tile(it + 1);
-    bool skip = !wave_has || (q0 + kKT - 1 < kw0);
+    bool skip = !wave_has || (causal && q0 + kKT - 1 < kw0);
     int sst_last = 0;
     if (PACKED && !skip) {
       skip = sst[q0] > kw0 + 31;
       sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
     }
     if (!skip) {
-      const bool need_mask = (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
+      const bool need_mask = (causal && q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
       const float* l2s = reinterpret_cast<const float*>(cur + 2 * C::kNatBytes + 2 * C::kTBytes);
       const float* ds_ = l2s + 64;
       const int* segs = reinterpret_cast<const int*>(l2s + 128);
@@ -702,7 +702,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
             float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
             if (need_mask) {
               const int qq = q0 + ql0 + u;
-              bool ok = (kj <= qq) && (qq < S) && kvalid;
+              bool ok = (!causal || kj <= qq) && (qq < S) && kvalid;
               if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
               if (!ok) p = 0.f;
             }
@@ -796,7 +796,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
                                const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
                                const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
                                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
-                               float scale_log2, float scale) {
+                               float scale_log2, float scale, int causal) {
   using namespace dkv128;
   constexpr int DH = 128;
   constexpr int kDK = DH / 16, kDB = DH / 32;
@@ -837,7 +837,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       opf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(src + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
   }
 
-  const int q_begin = (k0 / kKT) * kKT;
+  const int q_begin = causal ? (k0 / kKT) * kKT : 0;  // non-causal: every query
   int q_end = S;
   if (PACKED) {
     const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
@@ -948,9 +948,9 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       const bool phantom = it >= niter;
       const int q0 = q_begin + (it % ntq) * kKT;
       // Query row 32 h + 8 rq + 4 hf + u is visible to key kj iff thr <= c < lim, c = 32 h + 8 rq + u.
-      const int thr = (kvalid && !phantom) ? kj - q0 - 4 * hf : (1 << 20);
+      const int thr = (kvalid && !phantom) ? (causal ? kj - q0 - 4 * hf : -(1 << 20)) : (1 << 20);
       const int lim = my_lim - q0 - 4 * hf;
-      const bool need_mask = phantom || (q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && q0 + kKT > w_lim);
+      const bool need_mask = phantom || (causal && q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && q0 + kKT > w_lim);
       if (need_mask) {
 #pragma unroll
         for (int h = 0; h < 2; ++h)
@@ -1138,7 +1138,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
                        const bf16_t* __restrict__ d_o, const bf16_t* __restrict__ o_in, const float* __restrict__ lse_in,
                        float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
                        const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
-                       int B, int Hq, int Hkv, int S, float scale_log2, float scale) {
+                       int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
   using namespace kv128;
   constexpr int DH = 128;
   constexpr int kDK = DH / 16, kDB = DH / 32;
@@ -1193,7 +1193,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   }
 
   const int wg_q0 = pb * P;
-  const int wg_q1 = (wg_q0 + P < S) ? wg_q0 + P : S;
+  const int wg_q1 = (causal && wg_q0 + P < S) ? wg_q0 + P : S;  // non-causal: every key
   int kv_begin = 0;
   if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
   const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
@@ -1272,7 +1272,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   // tile t-1).
   auto body = [&](int t, const char* cur, char* nxt) __attribute__((always_inline)) {
     const int kv0 = kv_begin + t * kKT;
-    const bool skip = !wave_has || kv0 > wq_last || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
     const char* kt = cur;
     const char* vt = cur + kTile;
     int kb_ = kbase, t0_ = tbase0, t1_ = tbase1;
@@ -1339,8 +1339,8 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
       // start). Only tiles that cross the wave's diagonal, the sequence end or (packed) a segment
       // start are masked (scores of hidden keys set to -inf, so their probabilities are 0); the
       // test is per wave, a scalar branch.
-      const bool need_mask = (kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
-      const int thr = qvalid ? ((qi < S - 1 ? qi : S - 1) - kv0 - 4 * hf) : -1;
+      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int thr = qvalid ? ((causal && qi < S - 1 ? qi : S - 1) - kv0 - 4 * hf) : -1;
       const int lo = my_sst - kv0 - 4 * hf;
       auto visible = [&](int kb, int r) {
         const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
@@ -1482,12 +1482,12 @@ hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   const float sl2 = sh.scale * kLog2e;
   dim3 grid(fwd_grid(sh)), block(256);
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
     return hipGetLastError();
   }
-  if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
-  else hipLaunchKernelGGL((attn_fwd_kernel<DH, false>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2);
+  if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.causal);
+  else hipLaunchKernelGGL((attn_fwd_kernel<DH, false>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.causal);
   return hipGetLastError();
 }
 
@@ -1507,22 +1507,22 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   const float sl2 = sh.scale * kLog2e;
   dim3 qgrid(fwd_grid(sh));
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
   } else {
-  if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-  else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
     return hipGetLastError();
   }
-  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
-  else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale);
+  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
   return hipGetLastError();
 }
 }  // namespace

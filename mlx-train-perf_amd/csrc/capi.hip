@@ -84,8 +84,9 @@ int check_attn(const void* q, const void* k, const void* v, int64_t b, int64_t h
   if (hq % hkv != 0) return fail(MTP_ERR_INPUT, "Hq=%lld must be a multiple of Hkv=%lld for GQA grouping", (long long)hq, (long long)hkv);
   if (b * hq * s > kMaxDim || s > (int64_t(1) << 24)) return fail(MTP_ERR_INPUT, "b*hq*s must be < 2^31 and s < 2^24");
   if (dh != 64 && dh != 96 && dh != 128) return fail(MTP_ERR_UNSUPPORTED, "kernel impl only supports head_dim in (64, 96, 128) (got %lld); use impl='reference'", (long long)dh);
-  if (!causal) return fail(MTP_ERR_UNSUPPORTED, "kernel impl only supports causal=True (got causal=False); use impl='reference'");
+  if (causal != 0 && causal != 1) return fail(MTP_ERR_INPUT, "causal must be 0 or 1 (got %d)", (int)causal);
   if ((seg_id == nullptr) != (seg_start == nullptr)) return fail(MTP_ERR_INPUT, "seg_id and seg_start must be both given or both null");
+  if (seg_id && !causal) return fail(MTP_ERR_UNSUPPORTED, "segments (packed attention) require causal=1; packing composes on top of the causal triangle");
   if (!q || !k || !v) return fail(MTP_ERR_INPUT, "q, k, v must be non-null");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(MTP_ERR_UNSUPPORTED, "q, k, v must be 16-byte aligned");
   return MTP_OK;
@@ -248,7 +249,7 @@ int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t
   if (rc) return rc;
   if (!o || !lse) return fail(MTP_ERR_INPUT, "o and lse must be non-null");
   if (!aligned16(o)) return fail(MTP_ERR_UNSUPPORTED, "o must be 16-byte aligned");
-  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale};
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale, (int)causal};
   hipError_t e = mtp::launch_attn_fwd(sh, static_cast<const mtp::bf16_t*>(q), static_cast<const mtp::bf16_t*>(k),
                                       static_cast<const mtp::bf16_t*>(v), seg_id, seg_start,
                                       static_cast<mtp::bf16_t*>(o), lse, static_cast<hipStream_t>(stream));
@@ -275,7 +276,7 @@ int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   const size_t need = mtp_attn_bwd_workspace_bytes(b, hq, hkv, s, dh);
   if (!workspace || workspace_bytes < need)
     return fail(MTP_ERR_WORKSPACE, "attention backward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
-  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale};
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale, (int)causal};
   hipError_t e = mtp::launch_attn_bwd(sh, static_cast<const mtp::bf16_t*>(q), static_cast<const mtp::bf16_t*>(k),
                                       static_cast<const mtp::bf16_t*>(v), static_cast<const mtp::bf16_t*>(o), lse,
                                       static_cast<const mtp::bf16_t*>(d_o), seg_id, seg_start,

@@ -41,6 +41,7 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 struct AttnShape {
   int b, hq, hkv, s, dh;
   float scale;
+  int causal;  // 1: key j visible to query i iff j <= i (and, packed, same segment); 0: every key
 };
 
 hipError_t launch_attn_fwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,

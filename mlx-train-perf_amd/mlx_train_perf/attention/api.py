@@ -4,7 +4,8 @@ Residual contract (api.py:1-18): the autograd Function returns (O, L); L is a re
 non-differentiable, and only O reaches the caller. The backward reads q, k, v and the saved O, L.
 
 `impl="auto"`/`"kernel"`: the HIP kernels of libmtp_hip.so (bf16, head_dim in {64, 96, 128},
-causal, optional packed segments). `impl="reference"`: the materialized oracle with the hand-written
+causal with optional packed segments, or non-causal -- an extension: the reference kernel refuses
+causal=False, api.py:109-113). `impl="reference"`: the materialized oracle with the hand-written
 FlashAttention backward over full tensors -- an explicit opt-in, O(N^2) memory, small N only.
 No silent fallback: unsupported configs raise the reference's typed errors.
 """
@@ -104,10 +105,6 @@ def resolve_attention_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise UnsupportedAttentionError(
             f"kernel impl only supports head_dim in {_KERNEL_HEAD_DIMS} (got {head_dim}); use impl='reference'."
         )
-    if not causal:
-        raise UnsupportedAttentionError(
-            "kernel impl only supports causal=True (got causal=False); use impl='reference'."
-        )
     _compat.check_device_verified(allow_unverified=False, error=UnsupportedAttentionError)
     _compat.require_gpu_tensor(q, error=UnsupportedAttentionError)
     return "kernel"
@@ -176,21 +173,21 @@ def _seg_args(q, seg_id, seg_start):
 
 
 def kernel_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float,
-                   seg_id: torch.Tensor | None = None, seg_start: torch.Tensor | None = None):
-    """(O, L) from mtp_attn_fwd; q/k/v contiguous bf16 on the GPU."""
+                   seg_id: torch.Tensor | None = None, seg_start: torch.Tensor | None = None, causal: bool = True):
+    """(O, L) from mtp_attn_fwd; q/k/v contiguous bf16 on the GPU. causal=False: every key visible."""
     lib = _native.load()
     b, hq, n, dh = q.shape
     hkv = k.shape[1]
     o = torch.empty_like(q)
     lse = torch.empty((b, hq, n), dtype=torch.float32, device=q.device)
-    rc = lib.mtp_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale), 1,
+    rc = lib.mtp_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale), int(causal),
                           _native.ptr(seg_id), _native.ptr(seg_start), o.data_ptr(), lse.data_ptr(),
                           _native.stream_of(q))
     _native.check(rc, domain="attention")
     return o, lse
 
 
-def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_start=None):
+def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_start=None, causal: bool = True):
     """(dQ, dK, dV) from mtp_attn_bwd."""
     lib = _native.load()
     b, hq, n, dh = q.shape
@@ -201,7 +198,7 @@ def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_star
     ws_bytes = lib.mtp_attn_bwd_workspace_bytes(b, hq, hkv, n, dh)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
     rc = lib.mtp_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), d_o.data_ptr(),
-                          b, hq, hkv, n, dh, float(scale), 1, _native.ptr(seg_id), _native.ptr(seg_start),
+                          b, hq, hkv, n, dh, float(scale), int(causal), _native.ptr(seg_id), _native.ptr(seg_start),
                           dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(q))
     _native.check(rc, domain="attention")
     return dq, dk, dv
@@ -209,10 +206,10 @@ def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_star
 
 class _KernelAttention(torch.autograd.Function):
     @staticmethod
-    def forward(ctx, q, k, v, seg_id, seg_start, scale):
-        o, lse = kernel_forward(q, k, v, scale=scale, seg_id=seg_id, seg_start=seg_start)
+    def forward(ctx, q, k, v, seg_id, seg_start, scale, causal):
+        o, lse = kernel_forward(q, k, v, scale=scale, seg_id=seg_id, seg_start=seg_start, causal=causal)
         ctx.save_for_backward(q, k, v, o, lse, seg_id, seg_start)
-        ctx.scale = scale
+        ctx.scale, ctx.causal = scale, causal
         ctx.mark_non_differentiable(lse)
         return o, lse
 
@@ -222,8 +219,8 @@ class _KernelAttention(torch.autograd.Function):
         VJP_CALLS["flash_attention_kernel_bwd"] = VJP_CALLS.get("flash_attention_kernel_bwd", 0) + 1
         q, k, v, o, lse, seg_id, seg_start = ctx.saved_tensors
         dq, dk, dv = kernel_backward(q, k, v, o, lse, d_o.contiguous(), scale=ctx.scale, seg_id=seg_id,
-                                     seg_start=seg_start)
-        return dq, dk, dv, None, None, None
+                                     seg_start=seg_start, causal=ctx.causal)
+        return dq, dk, dv, None, None, None, None
 
 
 def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: float, causal: bool = True,
@@ -241,7 +238,8 @@ def flash_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale:
                                       validate_segments=validate_segments)
     seg_id, seg_start = (None, None) if segments is None else _seg_args(q, segments.seg_id, segments.seg_start)
     if resolved == "kernel":
-        o, _ = _KernelAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), seg_id, seg_start, float(scale))
+        o, _ = _KernelAttention.apply(q.contiguous(), k.contiguous(), v.contiguous(), seg_id, seg_start, float(scale),
+                                      bool(causal))
         return o
     o, _ = _ReferenceAttention.apply(q, k, v, seg_id, seg_start, float(scale), causal)
     return o

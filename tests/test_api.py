@@ -136,11 +136,11 @@ def test_attention_validation():
     with pytest.raises(UnsupportedAttentionError):
         resolve_attention_impl(qb, kb, vb, impl="auto")
     qb, kb, vb = _attn(d=64, dtype=torch.bfloat16)
-    with pytest.raises(UnsupportedAttentionError):
-        resolve_attention_impl(qb, kb, vb, impl="kernel", causal=False)
-    if not torch.cuda.is_available():
+    if not torch.cuda.is_available():   # no GPU: refused, never a CPU fallback (causal or not)
         with pytest.raises(UnsupportedAttentionError):
             resolve_attention_impl(qb, kb, vb, impl="auto")
+        with pytest.raises(UnsupportedAttentionError):
+            resolve_attention_impl(qb, kb, vb, impl="kernel", causal=False)
 
 
 @pytest.mark.parametrize("packed", [False, True])

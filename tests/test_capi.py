@@ -90,7 +90,8 @@ def test_attention_refusals():
 
     assert fwd(hq=3) == _native.MTP_ERR_INPUT
     assert fwd(dh=80) == _native.MTP_ERR_UNSUPPORTED
-    assert fwd(causal=0) == _native.MTP_ERR_UNSUPPORTED
+    assert fwd(causal=2) == _native.MTP_ERR_INPUT
+    assert fwd(causal=0, sid=FAKE, sst=FAKE) == _native.MTP_ERR_UNSUPPORTED   # packed needs causal
     assert fwd(sid=FAKE) == _native.MTP_ERR_INPUT
     assert fwd(o=False) == _native.MTP_ERR_INPUT
     rc = lib.mtp_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 4, 2, 16, 64, 0.1, 1, None, None, FAKE, FAKE, FAKE,

@@ -33,23 +33,24 @@ def _segs(lengths, b=1):
     return sid[None].repeat(b, 1), sst[None].repeat(b, 1)
 
 
-def _run_kernel(q, k, v, do, scale, seg=None):
+def _run_kernel(q, k, v, do, scale, seg=None, causal=True):
     from mlx_train_perf.attention.api import kernel_backward, kernel_forward
 
     qd, kd, vd, dod = (x.cuda().contiguous() for x in (q, k, v, do))
     sid = sst = None
     if seg is not None:
         sid, sst = (x.cuda().contiguous() for x in seg)
-    o, lse = kernel_forward(qd, kd, vd, scale=scale, seg_id=sid, seg_start=sst)
-    dq, dk, dv = kernel_backward(qd, kd, vd, o, lse, dod, scale=scale, seg_id=sid, seg_start=sst)
+    o, lse = kernel_forward(qd, kd, vd, scale=scale, seg_id=sid, seg_start=sst, causal=causal)
+    dq, dk, dv = kernel_backward(qd, kd, vd, o, lse, dod, scale=scale, seg_id=sid, seg_start=sst, causal=causal)
     torch.cuda.synchronize()
     return [x.cpu() for x in (o, lse, dq, dk, dv)]
 
 
-def _check(res, q, k, v, do, scale, seg_id=None):
+def _check(res, q, k, v, do, scale, seg_id=None, causal=True):
     o, lse, dq, dk, dv = res
-    oo, ol = oatt.attention_forward(q, k, v, scale=scale, seg_id=seg_id, dtype=torch.float64)
-    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, seg_id=seg_id, dtype=torch.float64)
+    oo, ol = oatt.attention_forward(q, k, v, scale=scale, causal=causal, seg_id=seg_id, dtype=torch.float64)
+    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, causal=causal, seg_id=seg_id,
+                                            dtype=torch.float64)
     assert torch.isfinite(o.float()).all() and torch.isfinite(lse).all()
     assert rel_l2(o, oo) <= 1e-2
     assert (o.double() - oo).abs().max() <= 1.2e-2 * max(1.0, oo.abs().max().item())
@@ -137,3 +138,43 @@ def test_golden_fixtures(name):
     assert rel_l2(o, g["o"]) <= 1e-2 and (lse.double() - g["lse"]).abs().max() <= 2e-3
     for got, key in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
         assert rel_l2(got, g[key]) <= 1e-2
+
+
+NONCAUSAL_SHAPES = [  # (b, hq, hkv, s, d)
+    (1, 4, 2, 61, 64),
+    (2, 4, 1, 130, 96),
+    (2, 4, 2, 257, 128),
+    (1, 8, 2, 1100, 128),
+    (1, 32, 8, 64, 128),
+    (1, 6, 3, 300, 96),
+]
+
+
+@pytest.mark.parametrize("shape", NONCAUSAL_SHAPES)
+def test_noncausal_parity(shape):
+    """causal=False: every key visible to every query (an extension; the reference kernel refuses it,
+    attention/api.py:109-113), against the oracle with causal=False."""
+    b, hq, hkv, s, d = shape
+    print(f"[attn non-causal] {shape}", flush=True)
+    q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=3 * s + d)
+    scale = 1.0 / math.sqrt(d)
+    _check(_run_kernel(q, k, v, do, scale, causal=False), q, k, v, do, scale, causal=False)
+
+
+def test_noncausal_differs_from_causal_and_public_api():
+    """The flag reaches the kernels: non-causal differs from causal on every row but the last, and
+    flash_attention(causal=False) with autograd gives the kernel's outputs and gradients."""
+    from mlx_train_perf.attention import flash_attention
+
+    q, k, v, do = attn_inputs(1, 4, 2, 130, 128, seed=12)
+    scale = 1.0 / math.sqrt(128)
+    full = _run_kernel(q, k, v, do, scale, causal=False)
+    tri = _run_kernel(q, k, v, do, scale, causal=True)
+    # the last row sees every key either way
+    assert (full[0][:, :, -1].float() - tri[0][:, :, -1].float()).abs().max() <= 1e-2
+    assert (full[0][:, :, :-1].float() - tri[0][:, :, :-1].float()).abs().amax(dim=-1).min() > 0
+    qd, kd, vd = (x.cuda().requires_grad_(True) for x in (q, k, v))
+    o = flash_attention(qd, kd, vd, scale=scale, causal=False)
+    o.backward(do.cuda())
+    for got, want in zip((o, qd.grad, kd.grad, vd.grad), (full[0], full[2], full[3], full[4])):
+        assert torch.equal(got.detach().cpu(), want)
