@@ -1,15 +1,21 @@
 """Bench harness: fused linear cross-entropy fwd+bwd on one MI355X, with the
-flash-attention (config 4, 5) and QLoRA (config 3) timings reported beside it.
+flash-attention (configs 4, 5), QLoRA (config 3), size ladders and CPU baselines reported beside it.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--parts ...]
 
 One step = one LCE forward + backward (dL/dH, frozen head) at N=8192 (batch 1 x seq 8192), D=4096,
 V=151936, bf16, synthetic seeded inputs resident in HBM before the timed region. Prints ONE JSON line.
 
 Per the reference's bench discipline (src/mlx_train_perf/bench/worker.py:93-142,
-scripts/bench_attention_op.py:225-296): seeded inputs, warm-up outside the window, timed window
-bracketed by device synchronization; forward marginal peak memory measured the worker's way
+scripts/bench_attention_op.py:225-296, scripts/bench_loss_layer.py:44-142): seeded inputs, warm-up
+outside the window, timed window bracketed by device synchronization, medians of repeated runs for
+the ladders and the CPU baselines; marginal peak memory measured the worker's way
 (max_memory_allocated - allocated_before after a reset).
+
+Profiling modes (their output is what profiles/ holds):
+    python bench.py --pmc-workload                      # the program rocprofv3 --pmc passes profile
+    python bench.py --pmc-summary CMD DIR [DIR ...]     # counters of those passes -> markdown
+    python bench.py --trace-summary CSV TITLE CMD       # rocprofv3 --kernel-trace csv -> markdown
 """
 from __future__ import annotations
 
@@ -18,6 +24,7 @@ import json
 import math
 import os
 import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -31,6 +38,7 @@ PEAK_HBM_GBS = 8000.0
 
 N, D, V = 8192, 4096, 151936
 IGNORE = -100
+ATT_B, ATT_HQ, ATT_HKV, ATT_DH = 1, 32, 8, 128
 
 
 def _cpu_model() -> str:
@@ -56,6 +64,19 @@ def lce_inputs_gpu(n, d, v, seed=0, ignore_frac=0.05):
     return h, w, t
 
 
+def packed_lengths(total: int, lo: int = 64, hi: int = 2048, seed: int = 0) -> list[int]:
+    """document lengths uniform in [lo, hi] from `seed` until `total` is filled."""
+    import random
+
+    rng = random.Random(seed)
+    lens, used = [], 0
+    while used < total:
+        n = min(rng.randint(lo, hi), total - used)
+        lens.append(n)
+        used += n
+    return lens
+
+
 def time_region(fn, steps, warmup):
     import torch
 
@@ -67,6 +88,37 @@ def time_region(fn, steps, warmup):
         fn()
     torch.cuda.synchronize()
     return (time.perf_counter() - t0) / steps
+
+
+def event_ms(fn, reps, warmup=2):
+    """Per-call durations (ms) of `fn` with HIP events on torch's current stream, the stream every
+    launch here is issued on."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    torch.cuda.synchronize()
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) for a, b in ev]
+
+
+def marginal_peak_bytes(fn):
+    """max_memory_allocated - allocated_before around fn (bench/worker.py:117-132 semantics)."""
+    import torch
+
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
+    torch.cuda.reset_peak_memory_stats()
+    out = fn()
+    torch.cuda.synchronize()
+    peak = torch.cuda.max_memory_allocated() - before
+    return peak, out
 
 
 def mfma_ceiling_tflops():
@@ -90,122 +142,167 @@ def mfma_ceiling_tflops():
     return flops / (ms * 1e-3) / 1e12
 
 
-def bench_lce(steps, warmup, head_kind="dense"):
-    """LCE fwd+bwd step timing + per-phase event timing of the forward kernel window."""
+# ------------------------------------------------------------------------------------------------
+# LCE (configs 2, 3)
+# ------------------------------------------------------------------------------------------------
+def _lce_head(w, head_kind):
+    from mlx_train_perf.core.loss import DenseHead, QuantizedHead
+    from mlx_train_perf.core.quant import quantize
+
+    if head_kind == "dense":
+        return DenseHead(weight=w, trainable=False)
+    wq, sc, bi = quantize(w)
+    return QuantizedHead(w_q=wq, scales=sc, biases=bi)
+
+
+def _fwd_launcher(h, head, t, head_kind):
+    """A closure issuing one mtp_lce_fwd (the roofline kernel + its finalize) through the C-ABI."""
     import torch
 
-    from mlx_train_perf.core.loss import DenseHead, QuantizedHead, kernel_forward_parts
-    from mlx_train_perf.core.quant import quantize
+    from mlx_train_perf import _native
+
+    lib = _native.load()
+    n_, d_ = h.shape
+    v_ = head.weight.shape[0] if head_kind == "dense" else head.w_q.shape[0]
+    outs = [torch.empty(n_, dtype=torch.float32, device="cuda") for _ in range(3)]
+    kind = _native.HEAD_DENSE if head_kind == "dense" else _native.HEAD_Q4
+    ws_b = lib.mtp_lce_fwd_workspace_bytes(n_, d_, v_, kind)
+    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
+    args = ((head.weight.data_ptr(), None, None, None) if head_kind == "dense" else
+            (None, head.w_q.data_ptr(), head.scales.data_ptr(), head.biases.data_ptr()))
+
+    def launch():
+        rc = lib.mtp_lce_fwd(h.data_ptr(), *args, t.data_ptr(), n_, d_, v_, kind, IGNORE, outs[0].data_ptr(),
+                             outs[1].data_ptr(), outs[2].data_ptr(), ws.data_ptr(), ws_b,
+                             torch.cuda.current_stream().cuda_stream)
+        _native.check(rc, domain="loss")
+
+    return launch
+
+
+def bench_lce(steps, warmup, head_kind="dense"):
+    """LCE fwd+bwd step timing, per-launch event timing of the forward, per-phase times, memory."""
+    import torch
+
+    from mlx_train_perf.core import loss as L
     from mlx_train_perf.plan import launch as plan
 
     h, w, t = lce_inputs_gpu(N, D, V)
-    if head_kind == "dense":
-        head = DenseHead(weight=w, trainable=False)
-    else:
-        wq, sc, bi = quantize(w)
+    head = _lce_head(w, head_kind)
+    if head_kind != "dense":
         del w
-        head = QuantizedHead(w_q=wq, scales=sc, biases=bi)
     hd = h.detach().requires_grad_(True)
     valid = (t != IGNORE)
     ct = (valid.float() / valid.sum()).contiguous()  # cotangent of the masked mean
 
     def step():
         hd.grad = None
-        nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
         nll.backward(ct)
 
     sec = time_region(step, steps, warmup)
 
-    # Roofline kernel: the forward launch (lce_fwd_kernel + its finalize) through the C-ABI, timed with
-    # events on the stream it is launched on.
-    from mlx_train_perf import _native
+    # Roofline kernel: the forward launch (lce_fwd_kernel + its finalize), one event pair per launch on
+    # the stream it is launched on; the median over `steps` launches is the figure the roofline uses.
+    fwd_ms = event_ms(_fwd_launcher(h.contiguous(), head, t.contiguous(), head_kind), steps, warmup=1)
 
-    lib = _native.load()
-    stream = torch.cuda.current_stream()
-    n_, d_, v_ = h.shape[0], h.shape[1], V
-    outs = [torch.empty(n_, dtype=torch.float32, device="cuda") for _ in range(3)]
-    kind = _native.HEAD_DENSE if head_kind == "dense" else _native.HEAD_Q4
-    ws_b = lib.mtp_lce_fwd_workspace_bytes(n_, d_, v_, kind)
-    ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
-    hw = h.contiguous()
-    tt = t.contiguous()
-    args = ((head.weight.data_ptr(), None, None, None) if head_kind == "dense" else
-            (None, head.w_q.data_ptr(), head.scales.data_ptr(), head.biases.data_ptr()))
-
-    def fwd_launch():
-        rc = lib.mtp_lce_fwd(hw.data_ptr(), *args, tt.data_ptr(), n_, d_, v_, kind, IGNORE, outs[0].data_ptr(),
-                             outs[1].data_ptr(), outs[2].data_ptr(), ws.data_ptr(), ws_b, stream.cuda_stream)
-        _native.check(rc, domain="loss")
-
-    fwd_launch()
-    kev = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(steps)]
-    torch.cuda.synchronize()
-    for i in range(steps):
-        kev[i][0].record(stream)
-        fwd_launch()
-        kev[i][1].record(stream)
-    torch.cuda.synchronize()
-    fwd_kernel_ms = sum(e[0].elapsed_time(e[1]) for e in kev) / steps
-    del ws
-
-    # Live per-phase durations with events on the launch stream: [fwd][bwd] per step.
+    # Per-phase durations, events on the launch stream: [fwd][bwd] per step.
     stream = torch.cuda.current_stream()
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
     torch.cuda.synchronize()
     for i in range(steps):
         hd.grad = None
         evs[i][0].record(stream)
-        nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
         evs[i][1].record(stream)
         nll.backward(ct)
         evs[i][2].record(stream)
     torch.cuda.synchronize()
-    fwd_ms = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
-    bwd_ms = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    phase_fwd = statistics.median(e[0].elapsed_time(e[1]) for e in evs)
+    phase_bwd = statistics.median(e[1].elapsed_time(e[2]) for e in evs)
 
-    # Forward marginal peak (bench/worker.py:117-132 semantics).
-    torch.cuda.synchronize()
+    # Loss-layer memory, the worker's way: the forward's marginal peak, then the backward's (G chunk
+    # + dH; the transposed head is already cached by the warm-up and reported on its own).
+    hd.grad = None
     torch.cuda.empty_cache()
-    before = torch.cuda.memory_allocated()
-    torch.cuda.reset_peak_memory_stats()
-    with torch.no_grad():
-        nll, _, _ = kernel_forward_parts(h, head, t, ignore_index=IGNORE)
-    torch.cuda.synchronize()
-    fwd_peak = torch.cuda.max_memory_allocated() - before
+    fwd_peak, (nll, _, _) = marginal_peak_bytes(lambda: L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE))
+    bwd_peak, _ = marginal_peak_bytes(lambda: nll.backward(ct))
     del nll
     p = plan.lce_plan(n=N, v=V, d=D)
-    from mlx_train_perf.core import loss as _loss
+    head_t = L.transposed_head_cache_bytes()
+    return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,
+            "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),
+            "fwd_kernel_launches": len(fwd_ms),
+            "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_marginal_peak_gb": bwd_peak / 1e9,
+            "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks,
+            "transposed_head_cache_gb": head_t / 1e9,
+            "bwd_footprint_gb": (bwd_peak + head_t) / 1e9}
 
-    head_t = _loss.transposed_head_cache_bytes()
-    return {"sec_per_step": sec, "fwd_ms": fwd_ms, "bwd_ms": bwd_ms, "fwd_kernel_ms": fwd_kernel_ms,
-            "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9,
-            "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks, "transposed_head_cache_gb": head_t / 1e9}
+
+def lce_ladder(reps=10):
+    """Forward loss layer at n in {512, 2048, 8192} (D=4096, V=151936): the fused kernel against the
+    same-device naive path (full bf16 logits, fp32 logsumexp; core/naive.py), the reference's
+    kernel-vs-naive gate being <= 1.7x (scripts/bench_loss_layer.py:44-51); plus the fused fwd+bwd."""
+    import torch
+
+    from mlx_train_perf.core import loss as L
+    from mlx_train_perf.core.naive import naive_linear_ce
+
+    out = {}
+    _, w, _ = lce_inputs_gpu(8, D, V, seed=1)
+    head = L.DenseHead(weight=w, trainable=False)
+    for n in (512, 2048, 8192):
+        h, _, t = lce_inputs_gpu(n, D, V, seed=n)
+        ts = torch.where(t == IGNORE, torch.zeros_like(t), t)
+        k_ms = statistics.median(event_ms(_fwd_launcher(h, head, t, "dense"), reps))
+        naive_ms = statistics.median(event_ms(lambda: naive_linear_ce(h, w, ts), max(3, reps // 2)))
+        torch.cuda.empty_cache()
+        k_peak, _ = marginal_peak_bytes(lambda: L.kernel_forward_parts(h, head, t, ignore_index=IGNORE))
+        n_peak, _ = marginal_peak_bytes(lambda: naive_linear_ce(h, w, ts))
+        hd = h.detach().requires_grad_(True)
+        ct = torch.full((n,), 1.0 / n, device="cuda")
+
+        def fb():
+            hd.grad = None
+            nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+            nll.backward(ct)
+
+        fb_ms = statistics.median(event_ms(fb, reps))
+        out[f"n{n}"] = {"fwd_kernel_ms": k_ms, "fwd_naive_ms": naive_ms, "kernel_over_naive": k_ms / naive_ms,
+                        "fwd_kernel_peak_gb": k_peak / 1e9, "fwd_naive_peak_gb": n_peak / 1e9,
+                        "fwd_tflops": 2.0 * n * V * D / (k_ms * 1e-3) / 1e12,
+                        "fwdbwd_kernel_ms": fb_ms, "fwdbwd_tflops": 6.0 * n * V * D / (fb_ms * 1e-3) / 1e12}
+        del h, t, ts, hd
+        torch.cuda.empty_cache()
+    return out
 
 
-def bench_attention(steps, warmup, packed=False):
+# ------------------------------------------------------------------------------------------------
+# Attention (configs 4, 5)
+# ------------------------------------------------------------------------------------------------
+def _attn_inputs(s, seed=0, b=ATT_B):
+    import torch
+
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    mk = lambda h: torch.randn(b, h, s, ATT_DH, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
+    return mk(ATT_HQ), mk(ATT_HKV), mk(ATT_HKV), mk(ATT_HQ)
+
+
+def bench_attention(steps, warmup, mode="causal", s=None):
+    """Flash attention fwd and fwd+bwd at B=1, Hq=32, Hkv=8, head_dim 128. mode: "causal" (config 4,
+    S=8192), "packed" (config 5, S=16384, seeded document lengths), "full" (non-causal, S=8192)."""
     import torch
 
     from mlx_train_perf.attention.api import kernel_backward, kernel_forward
     from mlx_train_perf.plan import launch as plan
 
-    b, hq, hkv, dh = 1, 32, 8, 128
-    s = 16384 if packed else 8192
-    g = torch.Generator(device="cuda").manual_seed(0)
-    q = torch.randn(b, hq, s, dh, generator=g, device="cuda").to(torch.bfloat16)
-    k = torch.randn(b, hkv, s, dh, generator=g, device="cuda").to(torch.bfloat16)
-    v = torch.randn(b, hkv, s, dh, generator=g, device="cuda").to(torch.bfloat16)
-    do = torch.randn(b, hq, s, dh, generator=g, device="cuda").to(torch.bfloat16)
-    scale = 1.0 / math.sqrt(dh)
+    s = s or (16384 if mode == "packed" else 8192)
+    q, k, v, do = _attn_inputs(s)
+    scale = 1.0 / math.sqrt(ATT_DH)
     sid = sst = None
-    if packed:
-        import random
-
-        rng = random.Random(0)
-        lens, used = [], 0
-        while used < s:
-            n_ = min(rng.randint(64, 2048), s - used)
-            lens.append(n_)
-            used += n_
+    causal = mode != "full"
+    if mode == "packed":
+        lens = packed_lengths(s)
         ids, starts, pos = [], [], 0
         for i, n_ in enumerate(lens):
             ids += [i] * n_
@@ -214,41 +311,184 @@ def bench_attention(steps, warmup, packed=False):
         sid = torch.tensor([ids], dtype=torch.int32, device="cuda")
         sst = torch.tensor([starts], dtype=torch.int32, device="cuda")
         pairs = plan.packed_pairs(lens)
+    elif mode == "full":
+        pairs = s * s
     else:
         pairs = plan.causal_pairs(s)
     state = {}
 
     def fwd():
-        state["o"], state["l"] = kernel_forward(q, k, v, scale=scale, seg_id=sid, seg_start=sst)
+        state["o"], state["l"] = kernel_forward(q, k, v, scale=scale, seg_id=sid, seg_start=sst, causal=causal)
+        return state["o"]
 
     def fwdbwd():
         fwd()
-        kernel_backward(q, k, v, state["o"], state["l"], do, scale=scale, seg_id=sid, seg_start=sst)
+        return kernel_backward(q, k, v, state["o"], state["l"], do, scale=scale, seg_id=sid, seg_start=sst,
+                               causal=causal)
 
     fwd_s = time_region(fwd, steps, warmup)
     fb_s = time_region(fwdbwd, steps, warmup)
-    flops_fb = 2.0 * 7 * dh * hq * b * pairs
+    state.clear()
+    torch.cuda.empty_cache()
+    fwd_peak, _ = marginal_peak_bytes(fwd)
+    state.clear()
+    torch.cuda.empty_cache()
+    fb_peak, _ = marginal_peak_bytes(fwdbwd)
+    state.clear()
+    flops_fwd = 2.0 * 2 * ATT_DH * ATT_HQ * ATT_B * pairs
+    flops_fb = 2.0 * 7 * ATT_DH * ATT_HQ * ATT_B * pairs
     out = {"seq": s, "fwd_ms": fwd_s * 1e3, "fwdbwd_ms": fb_s * 1e3, "bwd_ms": (fb_s - fwd_s) * 1e3,
            "pairs_per_head": pairs, "algorithmic_tflop": flops_fb / 1e12,
-           "tflops": flops_fb / fb_s / 1e12, "mfma_frac": flops_fb / fb_s / 1e12 / PEAK_BF16_TFLOPS}
-    if packed:
+           "fwd_tflops": flops_fwd / fwd_s / 1e12, "tflops": flops_fb / fb_s / 1e12,
+           "mfma_frac": flops_fb / fb_s / 1e12 / PEAK_BF16_TFLOPS,
+           "fwd_marginal_peak_gb": fwd_peak / 1e9, "fwdbwd_marginal_peak_gb": fb_peak / 1e9}
+    if mode == "packed":
         out["segments"] = len(lens)
     return out
 
 
+def attention_ladder(steps, warmup):
+    """Causal fwd and fwd+bwd at S in {2048, 4096, 8192} (the reference publishes all three,
+    community-benchmarks flash_n2048 / n4096 / n8192)."""
+    out = {}
+    for s in (2048, 4096, 8192):
+        r = bench_attention(steps, warmup, "causal", s=s)
+        out[f"s{s}"] = {k: r[k] for k in ("fwd_ms", "fwdbwd_ms", "fwd_tflops", "tflops", "mfma_frac")}
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
-# HBM traffic of the roofline kernel (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, calibrated against a
-# 1 GiB device copy). `--pmc-workload` is the program those passes profile; `--pmc-summary` turns
-# the two passes' csv output into the markdown committed under profiles/, whose json block
-# committed_traffic() reads back.
+# CPU baselines: the oracle (PyTorch-CPU fp32 restatement of the reference's naive / stock paths) on
+# the GPU box's host cores, median of 3 after one warm-up (bench/worker.py:121-133).
+# ------------------------------------------------------------------------------------------------
+def _cpu_threads():
+    import torch
+
+    if "OMP_NUM_THREADS" not in os.environ:  # the GPU box sets it to its CPU share
+        torch.set_num_threads(os.cpu_count() or 1)
+    return torch.get_num_threads()
+
+
+def _median_runs(run, reps=3):
+    run(warm=True)
+    ts = [run(warm=False) for _ in range(reps)]
+    return statistics.median(ts), ts
+
+
+def cpu_baseline_lce(budget_s: float = 4.0):
+    """Flagship LCE fwd+bwd (full D, V) on a bounded sample of the 8192 tokens."""
+    import torch
+
+    from oracle import lce as olce
+
+    cores = _cpu_threads()
+    g = torch.Generator().manual_seed(0)
+    w = (torch.randn(V, D, generator=g) * 0.02).to(torch.bfloat16).to(torch.float32)  # bf16 values, fp32 storage
+
+    def sample(rows):
+        h = torch.randn(rows, D, generator=g)
+        h = (h / torch.sqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+        return h, torch.randint(0, V, (rows,), generator=g)
+
+    def timed(h, t):
+        t0 = time.perf_counter()
+        _, lse, _ = olce.forward(h, w, t, ignore_index=IGNORE, dtype=torch.float32)
+        olce.backward(h, w, t, lse, torch.full((t.shape[0],), 1.0 / t.shape[0]), ignore_index=IGNORE,
+                      dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    timed(*sample(8))
+    probe = 256
+    dt = timed(*sample(probe))
+    rows = int(max(64, min(N, probe * budget_s / max(dt, 1e-3))))
+    h, t = sample(rows)
+    med, ts = _median_runs(lambda warm: timed(h, t) if not warm else timed(*sample(8)))
+    return {"value": rows / med, "unit": "tokens/s", "cores": cores, "kind": "port",
+            "sample": f"LCE fwd+bwd on {rows} of the {N} tokens (D={D}, V={V}), oracle/lce.py fp32, median of "
+                      f"{len(ts)} runs ({', '.join(f'{x:.2f}' for x in ts)} s); CPU {_cpu_model()}",
+            "reps": len(ts)}
+
+
+def cpu_baseline_c1():
+    """BASELINE config 1 in full: N=1024, D=512, V=32000 fp32, 10% ignore_index, fwd+bwd."""
+    import torch
+
+    from oracle import lce as olce
+
+    cores = _cpu_threads()
+    n, d, v = 1024, 512, 32000
+    g = torch.Generator().manual_seed(1)
+    h = torch.randn(n, d, generator=g)
+    w = torch.randn(v, d, generator=g) * 0.02
+    t = torch.randint(0, v, (n,), generator=g)
+    t[torch.randperm(n, generator=g)[: round(0.1 * n)]] = IGNORE
+    valid = t != IGNORE
+
+    def run(warm):
+        t0 = time.perf_counter()
+        _, lse, _ = olce.forward(h, w, t, ignore_index=IGNORE, dtype=torch.float32)
+        olce.backward(h, w, t, lse, valid.float() / valid.sum(), ignore_index=IGNORE, round_g_bf16=False,
+                      dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    med, ts = _median_runs(run)
+    return {"value": n / med, "unit": "tokens/s", "ms": med * 1e3, "tflops": 6.0 * n * v * d / med / 1e12,
+            "cores": cores, "kind": "port", "reps": len(ts),
+            "sample": f"config 1 in full (N={n}, D={d}, V={v}, fp32, 10% ignore), oracle/lce.py, median of "
+                      f"{len(ts)}; CPU {_cpu_model()}"}
+
+
+def cpu_baseline_attention(max_s: float = 6.0):
+    """Config 4 on one kv-head group (4 query heads, S=8192, head_dim 128), fp32, materialized scores
+    and the FlashAttention backward equations (oracle/attention.py); the full config is 8 groups."""
+    import torch
+
+    from oracle import attention as oatt
+    from mlx_train_perf.plan import launch as plan
+
+    cores = _cpu_threads()
+    s, grp = 8192, ATT_HQ // ATT_HKV
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(1, grp, s, ATT_DH, generator=g).to(torch.bfloat16)
+    k = torch.randn(1, 1, s, ATT_DH, generator=g).to(torch.bfloat16)
+    v = torch.randn(1, 1, s, ATT_DH, generator=g).to(torch.bfloat16)
+    do = torch.randn(1, grp, s, ATT_DH, generator=g).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(ATT_DH)
+
+    def run(warm):
+        qq, kk, vv, dd = (x[..., : 256, :] if warm else x for x in (q, k, v, do))
+        t0 = time.perf_counter()
+        o, lse = oatt.attention_forward(qq, kk, vv, scale=scale, dtype=torch.float32)
+        oatt.attention_backward(qq, kk, vv, o, lse, dd, scale=scale, dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    run(True)
+    first = run(False)
+    ts = [first] + ([run(False), run(False)] if first < max_s else [])
+    med = statistics.median(ts)
+    flop = 2.0 * 7 * ATT_DH * grp * plan.causal_pairs(s)
+    return {"value": med * 1e3, "unit": "ms per kv-head group", "full_config_ms": 8 * med * 1e3,
+            "tflops": flop / med / 1e12, "cores": cores, "kind": "port", "reps": len(ts),
+            "sample": f"config 4 on 1 of its 8 kv-head groups (Hq=4, Hkv=1, S={s}, d={ATT_DH}), fp32, oracle/"
+                      f"attention.py fwd+bwd, {'median of 3' if len(ts) == 3 else 'one run (reps=1)'}; "
+                      f"CPU {_cpu_model()}"}
+
+
+# ------------------------------------------------------------------------------------------------
+# Profiles. `--pmc-workload` is the program the rocprofv3 --pmc passes profile; `--pmc-summary`
+# merges the passes' counter csv files into the markdown committed under profiles/, whose json
+# block committed_traffic() reads back. Traffic: FETCH_SIZE / WRITE_SIZE (KiB per dispatch) scaled
+# by what they read for a 1 GiB device copy in the same run. MFMA: SQ_VALU_MFMA_BUSY_CYCLES over
+# 4 x SQ_BUSY_CU_CYCLES (reads ~1.0 on the register-only MFMA loop of mtp_bench_mfma_ceiling, which
+# the workload runs as the calibration), SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 = executed bf16 flop.
 # ------------------------------------------------------------------------------------------------
 PMC_COPY_BYTES = 1 << 30
-TRAFFIC_PROFILE = ROOT / "profiles" / "lce_attention_hbm_traffic_pmc.md"
+PMC_PROFILE = ROOT / "profiles" / "pmc_bench_workload_traffic_mfma.md"
 
 
 def committed_traffic(kernel: str):
     try:
-        text = TRAFFIC_PROFILE.read_text()
+        text = PMC_PROFILE.read_text()
         blob = text.split("```json", 1)[1].split("```", 1)[0]
         return json.loads(blob)["kernels"][kernel]["traffic_bytes"]
     except (OSError, IndexError, KeyError, ValueError):
@@ -256,12 +496,16 @@ def committed_traffic(kernel: str):
 
 
 def pmc_workload():
-    """One pass of each profiled workload (no timing): a 1 GiB device copy (the calibration),
-    the flagship LCE forward + backward, and causal attention forward + backward at S=8192."""
+    """One pass of each profiled workload (no timing): the 1 GiB copy and the MFMA loop
+    (calibrations), the flagship LCE forward + backward (dense and 4-bit), causal attention
+    (S=8192) and packed attention (S=16384, config 5). Each kernel instantiation serves one workload
+    here, so per-kernel counter means are per-workload figures (non-causal attention would share the
+    causal instantiations, and is left out)."""
     import torch
 
+    from mlx_train_perf import _native
     from mlx_train_perf.attention.api import kernel_backward, kernel_forward
-    from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
+    from mlx_train_perf.core.loss import kernel_forward_parts
 
     x = torch.empty(PMC_COPY_BYTES // 2, dtype=torch.int16, device="cuda").fill_(1)
     y = torch.empty_like(x)
@@ -269,27 +513,45 @@ def pmc_workload():
         y.copy_(x)
     torch.cuda.synchronize()
     del x, y
-    h, w, t = lce_inputs_gpu(N, D, V)
-    hd = h.requires_grad_(True)
-    for _ in range(2):
-        nll, _, _ = kernel_forward_parts(hd, DenseHead(weight=w, trainable=False), t, ignore_index=IGNORE)
-        nll.backward(torch.ones_like(nll))
+    out = torch.zeros(1024, device="cuda")
+    _native.load().mtp_bench_mfma_ceiling(1024, 2000, out.data_ptr(), torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    del h, w, t, hd
-    g = torch.Generator(device="cuda").manual_seed(0)
-    q = torch.randn(1, 32, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
-    k = torch.randn(1, 8, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
-    v = torch.randn(1, 8, 8192, 128, generator=g, device="cuda").to(torch.bfloat16)
-    do = torch.randn_like(q)
-    for _ in range(2):
-        o, l = kernel_forward(q, k, v, scale=1 / math.sqrt(128))
-        kernel_backward(q, k, v, o, l, do, scale=1 / math.sqrt(128))
-    torch.cuda.synchronize()
+    print("pmc workload: calibrations done", flush=True)
+    for kind in ("dense", "q4"):
+        h, w, t = lce_inputs_gpu(N, D, V)
+        head = _lce_head(w, kind)
+        hd = h.requires_grad_(True)
+        for _ in range(2):
+            nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+            nll.backward(torch.full_like(nll, 1.0 / N))
+        torch.cuda.synchronize()
+        del h, w, t, hd, head
+        torch.cuda.empty_cache()
+        print(f"pmc workload: lce {kind} done", flush=True)
+    for mode in ("causal", "packed"):
+        s = 16384 if mode == "packed" else 8192
+        q, k, v, do = _attn_inputs(s)
+        sid = sst = None
+        if mode == "packed":
+            lens = packed_lengths(s)
+            sid = torch.tensor([sum(([i] * n for i, n in enumerate(lens)), [])], dtype=torch.int32, device="cuda")
+            starts, pos = [], 0
+            for n in lens:
+                starts += [pos] * n
+                pos += n
+            sst = torch.tensor([starts], dtype=torch.int32, device="cuda")
+        for _ in range(2):
+            o, l = kernel_forward(q, k, v, scale=1 / math.sqrt(ATT_DH), seg_id=sid, seg_start=sst,
+                                  causal=mode != "full")
+            kernel_backward(q, k, v, o, l, do, scale=1 / math.sqrt(ATT_DH), seg_id=sid, seg_start=sst,
+                            causal=mode != "full")
+        torch.cuda.synchronize()
+        print(f"pmc workload: attention {mode} done", flush=True)
     print("pmc workload done", flush=True)
 
 
-def _pmc_means(root: str) -> dict:
-    """Per kernel, the mean over dispatches of each counter (summed over its dimension rows)."""
+def _pmc_dispatches(root: str) -> dict:
+    """kernel -> counter -> {dispatch id: value summed over the counter's dimension rows}."""
     import collections
     import csv
     import glob
@@ -301,93 +563,104 @@ def _pmc_means(root: str) -> dict:
             for row in csv.DictReader(fh):
                 name = re.sub(r"\(.*", "", row["Kernel_Name"]).replace("void ", "").strip()
                 acc[name][row["Counter_Name"]][row["Dispatch_Id"]] += float(row["Counter_Value"])
-    return {k: {c: (sum(d.values()) / len(d), max(d.values()), len(d)) for c, d in cs.items()} for k, cs in acc.items()}
+    return acc
 
 
-def pmc_summary(fetch_dir: str, write_dir: str, command: str) -> str:
-    fetch, write = _pmc_means(fetch_dir), _pmc_means(write_dir)
-    copy = [k for k in fetch if "copyBuffer" in k or "copy" in k.lower()]
-    # calibration: the largest copy dispatch (the 1 GiB copy) in each pass, counters in KiB
-    cf = max(fetch[k]["FETCH_SIZE"][1] for k in copy if "FETCH_SIZE" in fetch[k])
-    cw = max(write[k]["WRITE_SIZE"][1] for k in copy if k in write and "WRITE_SIZE" in write[k])
-    f_fetch, f_write = PMC_COPY_BYTES / (cf * 1024.0), PMC_COPY_BYTES / (cw * 1024.0)
-    algorithmic = {  # bytes that must cross HBM at least once per launch
+def pmc_summary(command: str, *dirs: str) -> str:
+    merged: dict = {}
+    for d in dirs:
+        for k, cs in _pmc_dispatches(d).items():
+            merged.setdefault(k, {}).update(cs)
+    mean = {k: {c: sum(v.values()) / len(v) for c, v in cs.items()} for k, cs in merged.items()}
+    calls = {k: max(len(v) for v in cs.values()) for k, cs in merged.items()}
+    copy = [k for k in merged if "copyBuffer" in k]   # the runtime's blit kernel: the 1 GiB copy
+    cal = {}
+    if any("FETCH_SIZE" in merged[k] for k in copy):
+        cf = max(max(merged[k]["FETCH_SIZE"].values()) for k in copy if "FETCH_SIZE" in merged[k])
+        cw = max(max(merged[k]["WRITE_SIZE"].values()) for k in copy if "WRITE_SIZE" in merged[k])
+        cal.update(copy_bytes=PMC_COPY_BYTES, fetch_kib=cf, write_kib=cw,
+                   fetch_factor=PMC_COPY_BYTES / (cf * 1024.0), write_factor=PMC_COPY_BYTES / (cw * 1024.0))
+    ceil = next((k for k in merged if "mfma_ceiling" in k), None)
+    if ceil and "SQ_VALU_MFMA_BUSY_CYCLES" in mean[ceil]:
+        c = mean[ceil]
+        cal["mfma_busy_ceiling_kernel"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * c["SQ_BUSY_CU_CYCLES"])
+    algorithmic_bytes = {   # bytes that must cross HBM at least once per launch
         "lce_fwd_kernel<0>": 2.0 * (V * D + N * D),
+        "lce_fwd_kernel<1>": 0.5 * V * D + 4.0 * V * D / 64 + 2.0 * N * D,
         "attn_kv128_kernel<false, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
     }
     kernels = {}
-    for k in sorted(fetch):
-        if not k.startswith("mtp::") or "FETCH_SIZE" not in fetch[k]:
+    for k in sorted(merged):
+        if not k.startswith("mtp::"):
             continue
+        m, r = mean[k], {"dispatches": calls[k]}
+        if "FETCH_SIZE" in m and "fetch_factor" in cal:
+            r["fetch_bytes"] = m["FETCH_SIZE"] * 1024.0 * cal["fetch_factor"]
+            r["write_bytes"] = m.get("WRITE_SIZE", 0.0) * 1024.0 * cal["write_factor"]
+            r["traffic_bytes"] = r["fetch_bytes"] + r["write_bytes"]
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in m and m.get("SQ_BUSY_CU_CYCLES"):
+            r["mfma_busy"] = m["SQ_VALU_MFMA_BUSY_CYCLES"] / (4.0 * m["SQ_BUSY_CU_CYCLES"])
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in m:
+            r["executed_bf16_tflop"] = m["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0 / 1e12
+        if "GRBM_GUI_ACTIVE" in m:
+            r["gui_active_cycles"] = m["GRBM_GUI_ACTIVE"]
         short = k[len("mtp::"):]
-        fb = fetch[k]["FETCH_SIZE"][0] * 1024.0 * f_fetch
-        wb = write.get(k, {}).get("WRITE_SIZE", (0.0,))[0] * 1024.0 * f_write
-        kernels[short] = {"fetch_bytes": fb, "write_bytes": wb, "traffic_bytes": fb + wb,
-                          "dispatches": fetch[k]["FETCH_SIZE"][2]}
-        if short in algorithmic:
-            kernels[short]["algorithmic_bytes"] = algorithmic[short]
-    lines = ["# HBM traffic per launch: LCE (N=8192 D=4096 V=151936) and causal attention (S=8192)", "",
-             "Commands (repository root on the GPU box; one rocprofv3 pass per counter):", "", "```", command, "```", "",
-             f"Calibration: a {PMC_COPY_BYTES} B device copy read FETCH_SIZE={cf:.0f} KiB and WRITE_SIZE={cw:.0f} KiB "
-             f"per dispatch, so bytes = KiB x 1024 x {f_fetch:.4f} (fetch) and x {f_write:.4f} (write).", "",
-             "| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB |", "|---|---:|---:|---:|---:|---:|"]
+        if short in algorithmic_bytes:
+            r["algorithmic_bytes"] = algorithmic_bytes[short]
+        kernels[short] = r
+    lines = ["# Counters per launch: bench.py --pmc-workload (LCE N=8192 D=4096 V=151936 dense <0> and 4-bit <1>; "
+             "attention S=8192 causal <false, *>, S=16384 packed <true, *>)", "",
+             "Commands (repository root on the GPU box; one rocprofv3 pass per counter group):", "", "```", command,
+             "```", ""]
+    if "fetch_factor" in cal:
+        lines += [f"Traffic calibration: a {PMC_COPY_BYTES} B device copy read FETCH_SIZE={cal['fetch_kib']:.0f} KiB "
+                  f"and WRITE_SIZE={cal['write_kib']:.0f} KiB per dispatch, so bytes = KiB x 1024 x "
+                  f"{cal['fetch_factor']:.4f} (fetch) and x {cal['write_factor']:.4f} (write).", ""]
+    if "mfma_busy_ceiling_kernel" in cal:
+        lines += ["MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES); the register-only MFMA loop "
+                  f"(`mfma_ceiling_kernel`) reads {cal['mfma_busy_ceiling_kernel']:.3f}. Executed bf16 TFLOP = "
+                  "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.", ""]
+    lines += ["| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB | MFMA busy | "
+              "executed bf16 TFLOP |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
+
+    def f(x, scale=1e9, fmt="{:.3f}"):
+        return "" if x is None else fmt.format(x / scale)
+
     for k, r in kernels.items():
-        alg = r.get("algorithmic_bytes")
-        lines.append(f"| `{k}` | {r['dispatches']} | {r['fetch_bytes'] / 1e9:.3f} | {r['write_bytes'] / 1e9:.3f} | "
-                     f"{r['traffic_bytes'] / 1e9:.3f} | {'' if alg is None else f'{alg / 1e9:.3f}'} |")
-    blob = {"calibration": {"copy_bytes": PMC_COPY_BYTES, "fetch_kib": cf, "write_kib": cw,
-                            "fetch_factor": f_fetch, "write_factor": f_write}, "kernels": kernels}
+        lines.append(f"| `{k}` | {r['dispatches']} | {f(r.get('fetch_bytes'))} | {f(r.get('write_bytes'))} | "
+                     f"{f(r.get('traffic_bytes'))} | {f(r.get('algorithmic_bytes'))} | "
+                     f"{f(r.get('mfma_busy'), 1, '{:.3f}')} | {f(r.get('executed_bf16_tflop'), 1, '{:.3f}')} |")
+    blob = {"calibration": cal, "kernels": kernels}
     lines += ["", "```json", json.dumps(blob, indent=1), "```", ""]
     return "\n".join(lines)
 
 
-def trace_summary(stats_csv: str, title: str, command: str) -> str:
-    """Markdown table of this library's kernels from a rocprofv3 --kernel-trace --stats csv."""
+def trace_summary(trace_csv: str, title: str, command: str) -> str:
+    """Markdown table of this library's kernels from a rocprofv3 --kernel-trace csv (one row per
+    dispatch), one line per (kernel, grid size) -- i.e. per launch shape, since the ladders reuse the
+    kernels at other sizes: calls, median, mean, the mean without the shape's first dispatch (its
+    warm-up), min and max."""
+    import collections
     import csv
     import re
 
-    rows = [r for r in csv.DictReader(open(stats_csv)) if "mtp::" in r["Name"]]
-    rows.sort(key=lambda r: -float(r["TotalDurationNs"]))
+    durs = collections.defaultdict(list)
+    for r in sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"])):
+        if "mtp::" in r["Kernel_Name"]:
+            name = re.sub(r"\(.*", "", r["Kernel_Name"]).replace("void ", "").replace("mtp::", "").strip()
+            grid = int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0)
+            durs[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     out = [f"# {title}", "", "Command (repository root on the GPU box):", "", "```", command, "```", "",
-           "Per-kernel durations from `rocprofv3 --kernel-trace --stats` (kernel_stats.csv), microseconds.", "",
-           "| kernel | calls | avg us | min us | max us | total us |", "|---|---:|---:|---:|---:|---:|"]
-    for r in rows:
-        name = re.sub(r"\(.*", "", r["Name"]).replace("void ", "").strip()
-        out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
-                   f"{float(r['MaxNs']) / 1e3:.1f} | {float(r['TotalDurationNs']) / 1e3:.1f} |")
+           "Per-launch-shape durations from `rocprofv3 --kernel-trace` (one row per dispatch), microseconds; "
+           "grid = work-items. The bench line's roofline uses the median of its per-launch event times; compare "
+           "it with the median here.", "",
+           "| kernel | grid | calls | median us | mean us | mean w/o first us | min us | max us |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    for (name, grid), d in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
+        rest = d[1:] or d
+        out.append(f"| `{name}` | {grid} | {len(d)} | {statistics.median(d):.1f} | {sum(d) / len(d):.1f} | "
+                   f"{sum(rest) / len(rest):.1f} | {min(d):.1f} | {max(d):.1f} |")
     return "\n".join(out) + "\n"
-
-
-def cpu_baseline(budget_s: float = 15.0):
-    """The oracle (PyTorch-CPU fp32 restatement of the reference's naive path) on a bounded sample
-    of the same workload: `rows` tokens of the flagship LCE fwd+bwd (full D, V)."""
-    import torch
-
-    from oracle import lce as olce
-
-    if "OMP_NUM_THREADS" not in os.environ:  # the GPU box sets it to its CPU share
-        torch.set_num_threads(os.cpu_count() or 1)
-    g = torch.Generator().manual_seed(0)
-    w = (torch.randn(V, D, generator=g) * 0.02).to(torch.bfloat16).to(torch.float32)  # bf16 values, fp32 storage
-
-    def run(rows):
-        h = torch.randn(rows, D, generator=g)
-        h = (h / torch.sqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
-        t = torch.randint(0, V, (rows,), generator=g)
-        t0 = time.perf_counter()
-        nll, lse, _ = olce.forward(h, w, t, ignore_index=IGNORE, dtype=torch.float32)
-        olce.backward(h, w, t, lse, torch.full((rows,), 1.0 / rows), ignore_index=IGNORE, dtype=torch.float32)
-        return time.perf_counter() - t0
-
-    run(8)  # warm-up outside the window
-    rows = 256  # a probe large enough that per-call overheads do not inflate the per-row cost
-    dt = run(rows)
-    # scale the sample toward the budget (the work is linear in rows), capped
-    rows = int(max(64, min(8192, rows * budget_s / max(dt, 1e-3))))
-    dt = run(rows)
-    return {"value": rows / dt, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"LCE fwd+bwd on {rows} of the {N} tokens (D={D}, V={V}), oracle/lce.py fp32, "
-                      f"{dt:.1f} s; CPU {_cpu_model()}"}
 
 
 def main():
@@ -398,12 +671,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--pmc-workload", action="store_true", help="run the profiled workloads once (no timing)")
-    ap.add_argument("--pmc-summary", nargs=3, metavar=("FETCH_DIR", "WRITE_DIR", "COMMAND"),
-                    help="summarize two rocprofv3 --pmc csv outputs into markdown")
-    ap.add_argument("--trace-summary", nargs=3, metavar=("STATS_CSV", "TITLE", "COMMAND"),
-                    help="summarize a rocprofv3 --kernel-trace --stats csv into markdown")
-    ap.add_argument("--parts", default="lce,qlora,attention",
-                    help="comma list of lce, qlora, attention (lce is the headline line)")
+    ap.add_argument("--pmc-summary", nargs="+", metavar="ARG",
+                    help="COMMAND DIR [DIR ...]: summarize rocprofv3 --pmc csv outputs into markdown")
+    ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "TITLE", "COMMAND"),
+                    help="summarize a rocprofv3 --kernel-trace csv into markdown")
+    ap.add_argument("--parts", default="lce,qlora,attention,ladder",
+                    help="comma list of lce, qlora, attention, ladder (lce is the headline line)")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary))
@@ -428,7 +701,7 @@ def main():
     sec = lce["sec_per_step"]
     flops_step = 6.0 * N * V * D
     fwd_flops = 2.0 * N * V * D
-    ach = fwd_flops / (lce["fwd_kernel_ms"] * 1e-3) / 1e12
+    ach = fwd_flops / (lce["fwd_kernel_ms_median"] * 1e-3) / 1e12
     result = {
         "metric": "fused-LCE fwd+bwd tokens/s @N8192 V151936 D4096 (bf16, frozen head)",
         "value": N / sec,
@@ -446,7 +719,8 @@ def main():
                    "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "mfma", "kernel": "lce_fwd_kernel<0> (+ lce_fwd_finalize_kernel in the event window)",
                      "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
-                     "traffic": committed_traffic("lce_fwd_kernel<0>")},
+                     "traffic": committed_traffic("lce_fwd_kernel<0>"),
+                     "timing": f"median of {lce['fwd_kernel_launches']} launches, HIP events on the launch stream"},
         "step_mfma_frac": flops_step / sec / 1e12 / PEAK_BF16_TFLOPS,
         "lce": {**lce, "step_tflops": flops_step / sec / 1e12},
     }
@@ -462,10 +736,17 @@ def main():
                                "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
     if not args.no_extras and "attention" in parts:
         torch.cuda.empty_cache()
-        result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, packed=False)
-        result["attention_packed_s16384"] = bench_attention(args.steps, args.warmup, packed=True)
+        result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, "causal")
+        result["attention_packed_s16384"] = bench_attention(args.steps, args.warmup, "packed")
+        result["attention_noncausal_s8192"] = bench_attention(args.steps, args.warmup, "full")
+    if not args.no_extras and "ladder" in parts:
+        torch.cuda.empty_cache()
+        result["lce_ladder_fwd"] = lce_ladder()
+        result["attention_ladder_causal"] = attention_ladder(max(3, args.steps // 2), 2)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline()
+        result["cpu_baseline"] = cpu_baseline_lce()
+        result["cpu_baseline_c1"] = cpu_baseline_c1()
+        result["cpu_baseline_attention"] = cpu_baseline_attention()
     print(json.dumps(result), flush=True)
 
 
