@@ -140,8 +140,16 @@ int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t
                  int64_t s, int64_t dh, float scale, int32_t causal, const int32_t* seg_id,
                  const int32_t* seg_start, void* o, float* lse, void* stream);
 
-/* Workspace bytes for mtp_attn_bwd: the fp32 row term D = rowsum(dO * O), [b][hq][s]. */
+/* Workspace bytes for mtp_attn_bwd: the fp32 row term D = rowsum(dO * O), [b][hq][s], plus, at
+ * shapes where the dK/dV pass splits its key blocks (mtp_attn_bwd_dkv_splits > 1 for either value
+ * of causal), fp32 dK/dV partials [splits][2][b][hkv][s][dh] after D padded to 256 bytes. */
 size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh);
+
+/* Workgroups per 128-key block of the dK/dV pass (1, 2, 4 or 8): the launch plan's
+ * size table, chosen so the heaviest workgroup holds no more than ~1.15x a CU's share of the
+ * pass's work (1 at B=1, Hq=32, Hkv=8, S=8192 causal; 4 at S=2048). Replaces the reference's tile
+ * and variant selection by sequence bucket (attention/kernel/dispatch.py:46-133). */
+int mtp_attn_bwd_dkv_splits(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh, int32_t causal);
 
 /* Backward from the saved (o, lse): dq like q, dk and dv like k (summed over each kv head's
  * query-head group); all bf16.

@@ -569,7 +569,7 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
                          const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
                          const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
                          bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
-                         float scale_log2, float scale, int causal) {
+                         float scale_log2, float scale, int causal, int nsplit, float* __restrict__ part) {
   using C = AttnCfg<DH>;
   // Q, dO natural; Q^T, dO^T; then L*log2e, D and segment ids of the 64 queries.
   constexpr int kStage = 2 * C::kNatBytes + 2 * C::kTBytes + 3 * 256;
@@ -577,9 +577,12 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
 
   const int G = Hq / Hkv;
   const int nkv = B * Hkv;
+  // Block g: split g % nsplit of key block (g / nsplit) / nkv of kv head (g / nsplit) % nkv; the
+  // earliest keys (most work under the causal mask) first.
   const int g = blockIdx.x;
-  const int kvi = g % nkv;
-  const int kt = g / nkv;  // earliest keys (most work under the causal mask) first
+  const int split = g % nsplit;
+  const int kvi = (g / nsplit) % nkv;
+  const int kt = (g / nsplit) / nkv;
   const int bidx = kvi / Hkv;
   const int kvh = kvi % Hkv;
   const int k0 = kt * 128;
@@ -614,6 +617,9 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
   }
   const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
   const int niter = G * ntq;
+  // This workgroup's share of the key block's (head, query tile) items: [it0, it1).
+  const int it0 = (int)((long)niter * split / nsplit);
+  const int it1 = (int)((long)niter * (split + 1) / nsplit);
 
   f32x16 dka[C::kDB], dva[C::kDB];
 #pragma unroll
@@ -654,15 +660,15 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
     }
   };
 
-  if (niter > 0) {
-    load_tile(0);
+  if (it1 > it0) {
+    load_tile(it0);
     store_tile(lds);
   }
   __syncthreads();
-  for (int it = 0; it < niter; ++it) {
-    const char* cur = lds + (it & 1) * kStage;
+  for (int it = it0; it < it1; ++it) {
+    const char* cur = lds + ((it - it0) & 1) * kStage;
     const int q0 = q_begin + (it % ntq) * kKT;
-    const bool more = it + 1 < niter;
+    const bool more = it + 1 < it1;
     if (more) load_tile(it + 1);
     bool skip = !wave_has || (causal && q0 + kKT - 1 < kw0);
     int sst_last = 0;
@@ -719,11 +725,11 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
           }
       }
     }
-    if (more) store_tile(lds + ((it + 1) & 1) * kStage);
+    if (more) store_tile(lds + ((it + 1 - it0) & 1) * kStage);
     __syncthreads();
   }
 
-  if (kvalid) {
+  if (kvalid && nsplit == 1) {
     bf16_t* ko = dk + (krow + kj) * DH;
     bf16_t* vo = dv + (krow + kj) * DH;
 #pragma unroll
@@ -736,6 +742,21 @@ void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict_
                   pack_bf16x2(dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale)};
         *reinterpret_cast<u32x2*>(vo + d) = u32x2{pack_bf16x2(dva[db][4 * rq], dva[db][4 * rq + 1]),
                                                   pack_bf16x2(dva[db][4 * rq + 2], dva[db][4 * rq + 3])};
+      }
+  } else if (kvalid) {
+    // fp32 partials of this split: part[split][dk | dv][b][kv head][key][d] (attn_dkv_reduce_kernel).
+    const long plane = (long)B * Hkv * S * DH;
+    float* ko = part + (2L * split) * plane + (krow + kj) * DH;
+    float* vo = ko + plane;
+#pragma unroll
+    for (int db = 0; db < C::kDB; ++db)
+#pragma unroll
+      for (int rq = 0; rq < 4; ++rq) {
+        const int d = 32 * db + 8 * rq + 4 * hf;
+        *reinterpret_cast<f32x4*>(ko + d) = f32x4{dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale,
+                                                  dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale};
+        *reinterpret_cast<f32x4*>(vo + d) = f32x4{dva[db][4 * rq], dva[db][4 * rq + 1], dva[db][4 * rq + 2],
+                                                  dva[db][4 * rq + 3]};
       }
   }
 }
@@ -796,7 +817,8 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
                                const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
                                const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
                                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
-                               float scale_log2, float scale, int causal) {
+                               float scale_log2, float scale, int causal, int nsplit,
+                               float* __restrict__ part) {
   using namespace dkv128;
   constexpr int DH = 128;
   constexpr int kDK = DH / 16, kDB = DH / 32;
@@ -809,9 +831,12 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
 
   const int G = Hq / Hkv;
   const int nkv = B * Hkv;
+  // Block g: split g % nsplit of key block (g / nsplit) / nkv of kv head (g / nsplit) % nkv; the
+  // earliest keys (most work under the causal mask) first.
   const int g = blockIdx.x;
-  const int kvi = g % nkv;
-  const int ktile = g / nkv;  // earliest keys (most work under the causal mask) first
+  const int split = g % nsplit;
+  const int kvi = (g / nsplit) % nkv;
+  const int ktile = (g / nsplit) / nkv;
   const int bidx = kvi / Hkv;
   const int kvh = kvi % Hkv;
   const int k0 = ktile * 128;
@@ -852,6 +877,9 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   }
   const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
   const int niter = G * ntq;
+  // This workgroup's share of the key block's (head, query tile) items: [it0, it0 + nloc).
+  const int it0 = (int)((long)niter * split / nsplit);
+  const int nloc = (int)((long)niter * (split + 1) / nsplit) - it0;
 
   f32x16 acc[kDB];  // dV^T (P wave) or dK^T (dS wave)
 #pragma unroll
@@ -896,7 +924,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     int bytes, sbytes;
   };
   auto copy_src = [&](int it, bool live) __attribute__((always_inline)) {
-    const int itc = live ? it : 0;
+    const int itc = live ? it0 + it : 0;
     const int hh = itc / ntq, tq = itc % ntq;
     const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
     const int q0 = q_begin + tq * kKT;
@@ -945,8 +973,8 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       }
     }
     if (pwave) {
-      const bool phantom = it >= niter;
-      const int q0 = q_begin + (it % ntq) * kKT;
+      const bool phantom = it >= nloc;
+      const int q0 = q_begin + ((it0 + it) % ntq) * kKT;
       // Query row 32 h + 8 rq + 4 hf + u is visible to key kj iff thr <= c < lim, c = 32 h + 8 rq + u.
       const int thr = (kvalid && !phantom) ? (causal ? kj - q0 - 4 * hf : -(1 << 20)) : (1 << 20);
       const int lim = my_lim - q0 - 4 * hf;
@@ -1046,7 +1074,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   // At the start of step t, tile t+1 sits in stage (t+1) % 3 and stage (t+2) % 3 is free (tile t-1
   // was finished in step t-1): step t copies tile t+2 into it, spread over the products of
   // start(t+1), and the sync that ends the step waits for those copies.
-  const int nrun = (niter + 2) / 3 * 3;
+  const int nrun = (nloc + 2) / 3 * 3;
   if (nrun > 0) {
     if (pwave) {
       const CopySrc c0 = copy_src(0, true);
@@ -1057,7 +1085,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     sync();
 #pragma unroll
     for (int ks = 0; ks < kDK; ++ks) asm volatile("" : "+v"(opf[ks]));
-    start(0, st0, pb0, copy_src(1, niter > 1), st1);
+    start(0, st0, pb0, copy_src(1, nloc > 1), st1);
     sync();
   }
   // Step t: the dS wave finishes tile t (with its dP, still in a1) and then starts tile t+1; the P
@@ -1068,11 +1096,11 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     constexpr bool PW = decltype(pw)::value;
     auto step = [&](int t, const char* sc, const char* pc, const char* sn, char* pn, char* sx) __attribute__((always_inline)) {
       if constexpr (PW) {
-        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
+        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < nloc), sx);
         finish(sc, pc);
       } else {
         finish(sc, pc);
-        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < niter), sx);
+        start(t + 1, sn, pn, copy_src(t + 2, t + 2 < nloc), sx);
       }
       sync();
     };
@@ -1086,17 +1114,56 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
   else run(std::false_type{});
 
   if (kvalid) {
-    bf16_t* o = (pwave ? dv : dk) + (krow + kj) * DH;
     const float mul = pwave ? 1.f : scale;
+    if (nsplit == 1) {
+      bf16_t* o = (pwave ? dv : dk) + (krow + kj) * DH;
 #pragma unroll
-    for (int db = 0; db < kDB; ++db)
+      for (int db = 0; db < kDB; ++db)
 #pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        *reinterpret_cast<u32x2*>(o + d) = u32x2{pack_bf16x2(acc[db][4 * rq] * mul, acc[db][4 * rq + 1] * mul),
-                                                 pack_bf16x2(acc[db][4 * rq + 2] * mul, acc[db][4 * rq + 3] * mul)};
-      }
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d = 32 * db + 8 * rq + 4 * hf;
+          *reinterpret_cast<u32x2*>(o + d) = u32x2{pack_bf16x2(acc[db][4 * rq] * mul, acc[db][4 * rq + 1] * mul),
+                                                   pack_bf16x2(acc[db][4 * rq + 2] * mul, acc[db][4 * rq + 3] * mul)};
+        }
+    } else {
+      // fp32 partial of this split: part[split][dk | dv][b][kv head][key][d], summed by
+      // attn_dkv_reduce_kernel.
+      const long plane = (long)B * Hkv * S * DH;
+      float* o = part + (2L * split + (pwave ? 1 : 0)) * plane + (krow + kj) * DH;
+#pragma unroll
+      for (int db = 0; db < kDB; ++db)
+#pragma unroll
+        for (int rq = 0; rq < 4; ++rq) {
+          const int d = 32 * db + 8 * rq + 4 * hf;
+          *reinterpret_cast<f32x4*>(o + d) = f32x4{acc[db][4 * rq] * mul, acc[db][4 * rq + 1] * mul,
+                                                   acc[db][4 * rq + 2] * mul, acc[db][4 * rq + 3] * mul};
+        }
+    }
   }
+}
+
+// dK, dV = the sum of the nsplit fp32 partials of the split dK/dV kernel, rounded to bf16 once. Each
+// thread sums 8 consecutive elements of one plane (blockIdx.y: 0 dK, 1 dV) over the splits in split
+// order, so the result does not depend on scheduling. plane (B Hkv S DH) is a multiple of 8.
+__global__ __launch_bounds__(256) void attn_dkv_reduce_kernel(const float* __restrict__ part, int nsplit, long plane,
+                                                              bf16_t* __restrict__ dk, bf16_t* __restrict__ dv) {
+  const long e = ((long)blockIdx.x * 256 + threadIdx.x) * 8;
+  const int which = blockIdx.y;
+  if (e >= plane) return;
+  float acc[8] = {};
+  for (int sp = 0; sp < nsplit; ++sp) {
+    const float* src = part + (2L * sp + which) * plane + e;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(src);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(src + 4);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc[u] += a[u];
+      acc[4 + u] += b[u];
+    }
+  }
+  bf16_t* dst = (which ? dv : dk) + e;
+  *reinterpret_cast<u32x4*>(dst) = u32x4{pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                                          pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7])};
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1468,6 +1535,40 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 // ------------------------------------------------------------------------------------------
 // Launchers
 // ------------------------------------------------------------------------------------------
+// Work items of the dK/dV kernels (every head_dim): one per (query head of the group, 64-query tile)
+// seen by a 128-key block. Under the causal mask key block kb sees the tiles from 128 kb on, so
+// block 0 holds the most; without it every block holds ceil(S / 64). The kernel runs one 8-wave
+// workgroup per CU. When the heaviest block holds more than ~1.15x a CU's share of all items, or
+// there are fewer blocks than CUs, the CUs given light blocks idle while the heaviest runs: the
+// block's items are then split over nsplit workgroups (1, 2, 4 or 8: the smallest that brings the
+// heaviest workgroup under the share), whose fp32 partials attn_dkv_reduce_kernel sums. At B = 1,
+// Hkv = 8 causal this gives 8 splits at S <= 1024, 4 at 2048, 2 at 4096 and 1 from 8192 on.
+int attn_dkv_nsplit(int b, int hq, int hkv, int s, int dh, int causal) {
+  if (b < 1 || hkv < 1 || s < 1 || hq % hkv) return 1;
+  const long G = hq / hkv;
+  const long nkb = (s + 127) / 128;
+  const long heaviest = G * ((s + 63) / 64);
+  long total = 0;
+  for (long kb = 0; kb < nkb; ++kb) total += G * (causal ? (s - 128 * kb + 63) / 64 : (s + 63) / 64);
+  total *= (long)b * hkv;
+  for (int ns = 1; ns < 8; ns *= 2)
+    if (heaviest * kNumCU * 100 <= 115L * total * ns) return ns;
+  return 8;
+}
+
+size_t attn_dvec_bytes(int b, int hq, int s) {
+  // D (fp32 per query row), rounded up to 256 B so the partials that follow it stay aligned.
+  return ((size_t)b * hq * s * sizeof(float) + 255) / 256 * 256;
+}
+
+size_t attn_bwd_workspace(int b, int hq, int hkv, int s, int dh) {
+  // D plus, when either mode splits, the fp32 dK/dV partials of the larger split.
+  const int ns = attn_dkv_nsplit(b, hq, hkv, s, dh, 1) > attn_dkv_nsplit(b, hq, hkv, s, dh, 0)
+                     ? attn_dkv_nsplit(b, hq, hkv, s, dh, 1) : attn_dkv_nsplit(b, hq, hkv, s, dh, 0);
+  if (ns == 1) return (size_t)b * hq * s * sizeof(float);
+  return attn_dvec_bytes(b, hq, s) + (size_t)ns * 2 * (size_t)b * hkv * s * dh * sizeof(float);
+}
+
 namespace {
 int fwd_grid(const AttnShape& sh) {
   const int G = sh.hq / sh.hkv;
@@ -1515,14 +1616,22 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   }
   e = hipGetLastError();
   if (e != hipSuccess) return e;
-  dim3 kgrid(((sh.s + 127) / 128) * sh.b * sh.hkv);
+  // Split key blocks write fp32 partials after the D vector in the workspace; the reduce sums them.
+  const int ns = attn_dkv_nsplit(sh.b, sh.hq, sh.hkv, sh.s, DH, sh.causal);
+  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(dvec) + attn_dvec_bytes(sh.b, sh.hq, sh.s));
+  dim3 sgrid(((sh.s + 127) / 128) * sh.b * sh.hkv * ns);
   if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), kgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-    return hipGetLastError();
+    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
+    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
+  } else {
+    if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), sgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
+    else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), sgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
   }
-  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), kgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  e = hipGetLastError();
+  if (e != hipSuccess || ns == 1) return e;
+  const long plane = (long)sh.b * sh.hkv * sh.s * DH;
+  dim3 rgrid((unsigned)((plane / 8 + 255) / 256), 2);
+  hipLaunchKernelGGL(attn_dkv_reduce_kernel, rgrid, dim3(256), 0, st, part, ns, plane, dk, dv);
   return hipGetLastError();
 }
 }  // namespace

@@ -258,10 +258,13 @@ int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t
 }
 
 size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh) {
-  (void)hkv;
-  (void)dh;
-  if (b < 1 || hq < 1 || s < 1) return 0;
-  return (size_t)b * (size_t)hq * (size_t)s * sizeof(float);
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1 || hq % hkv || b * hq * s > kMaxDim) return 0;
+  return mtp::attn_bwd_workspace((int)b, (int)hq, (int)hkv, (int)s, (int)dh);
+}
+
+int mtp_attn_bwd_dkv_splits(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh, int32_t causal) {
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1 || hq % hkv || b * hq * s > kMaxDim) return 0;
+  return mtp::attn_dkv_nsplit((int)b, (int)hq, (int)hkv, (int)s, (int)dh, causal ? 1 : 0);
 }
 
 int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, const float* lse, const void* d_o,

@@ -44,6 +44,11 @@ struct AttnShape {
   int causal;  // 1: key j visible to query i iff j <= i (and, packed, same segment); 0: every key
 };
 
+// Splits of each key block's work in the head_dim-128 dK/dV kernel (1 = none), and the backward
+// workspace: D plus the fp32 dK/dV partials when either mode splits.
+int attn_dkv_nsplit(int b, int hq, int hkv, int s, int dh, int causal);
+size_t attn_bwd_workspace(int b, int hq, int hkv, int s, int dh);
+
 hipError_t launch_attn_fwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v,
                            const int32_t* seg_id, const int32_t* seg_start, bf16_t* o, float* lse,
                            hipStream_t stream);

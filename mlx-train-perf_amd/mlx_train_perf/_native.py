@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_attn_fwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                     _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "mtp_attn_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "mtp_attn_bwd_dkv_splits": (ctypes.c_int, [_i64, _i64, _i64, _i64, _i64, _i32]),
     "mtp_bench_mfma_ceiling": (ctypes.c_int, [ctypes.c_int, ctypes.c_int, _c_void_p, _c_void_p]),
     "mtp_attn_bwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _i64, _i64, _i64, _i64, _i64, _f32, _i32, _c_void_p, _c_void_p,

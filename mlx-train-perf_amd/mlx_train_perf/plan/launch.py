@@ -99,16 +99,50 @@ def attn_heads_per_workgroup(hq: int, hkv: int) -> int:
     return 4 if g % 4 == 0 else (2 if g % 2 == 0 else 1)
 
 
+def attn_dkv_splits(*, b: int, hq: int, hkv: int, s: int, dh: int = 128, causal: bool = True) -> int:
+    """Workgroups per 128-key block of the dK/dV pass (every head_dim; `dh` only sizes the workspace): the size table of the launch
+    plan (the MI355X counterpart of the reference's tile selection by sequence bucket,
+    attention/kernel/dispatch.py:46-133), mirroring attn_dkv_nsplit in csrc/attn_kernels.hip.
+
+    A key block's work is one item per (query head of its group, 64-query tile it sees): under the
+    causal mask block kb sees the tiles from 128 kb on. One 8-wave workgroup runs per CU, so when
+    the heaviest block exceeds ~1.15x a CU's share of all items (or blocks are fewer than CUs) the
+    light CUs idle behind it; the block is then split over 2, 4 or 8 workgroups, the smallest count
+    that brings the heaviest workgroup under the share, and their fp32 partials are summed."""
+    if b < 1 or hkv < 1 or s < 1 or hq % hkv:
+        return 1
+    g = hq // hkv
+    nkb = -(-s // 128)
+    heaviest = g * -(-s // 64)
+    total = b * hkv * sum(g * (-(-(s - 128 * kb) // 64) if causal else -(-s // 64)) for kb in range(nkb))
+    for ns in (1, 2, 4):
+        if heaviest * NUM_CU * 100 <= 115 * total * ns:
+            return ns
+    return 8
+
+
+def attn_bwd_workspace_bytes(*, b: int, hq: int, hkv: int, s: int, dh: int = 128) -> int:
+    """D (fp32 per query row) plus the fp32 dK/dV partials of the larger split of the two masks."""
+    ns = max(attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=True),
+             attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=False))
+    if ns == 1:
+        return b * hq * s * 4
+    return -(-(b * hq * s * 4) // 256) * 256 + ns * 2 * b * hkv * s * dh * 4   # D padded to 256 B, partials
+
+
 @dataclass(frozen=True)
 class AttnPlan:
     heads_per_workgroup: int
     fwd_workgroups: int
+    dkv_splits: int
     dkv_workgroups: int
     bwd_workspace_bytes: int
 
 
-def attn_plan(*, b: int, hq: int, hkv: int, s: int) -> AttnPlan:
+def attn_plan(*, b: int, hq: int, hkv: int, s: int, dh: int = 128, causal: bool = True) -> AttnPlan:
     hpw = attn_heads_per_workgroup(hq, hkv)
     p = 32 * (4 // hpw)
-    return AttnPlan(heads_per_workgroup=hpw, fwd_workgroups=-(-s // p) * b * (hq // hpw),
-                    dkv_workgroups=-(-s // 128) * b * hkv, bwd_workspace_bytes=b * hq * s * 4)
+    ns = attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=causal)
+    return AttnPlan(heads_per_workgroup=hpw, fwd_workgroups=-(-s // p) * b * (hq // hpw), dkv_splits=ns,
+                    dkv_workgroups=-(-s // 128) * b * hkv * ns,
+                    bwd_workspace_bytes=attn_bwd_workspace_bytes(b=b, hq=hq, hkv=hkv, s=s, dh=dh))

@@ -44,6 +44,19 @@ def test_plans_agree_with_python_planner(n, d, v):
     assert lib.mtp_attn_bwd_workspace_bytes(1, 32, 8, 8192, 128) == plan.attn_plan(b=1, hq=32, hkv=8, s=8192).bwd_workspace_bytes
 
 
+def test_dkv_split_table_agrees_with_python_planner():
+    lib = _native.load()
+    for b in (1, 2, 4):
+        for hq, hkv in ((32, 8), (8, 2), (4, 1), (6, 3), (64, 8)):
+            for s in (1, 61, 300, 1024, 1100, 2048, 4096, 5000, 8192, 16384):
+                for dh in (64, 96, 128):
+                    for causal in (0, 1):
+                        assert lib.mtp_attn_bwd_dkv_splits(b, hq, hkv, s, dh, causal) == plan.attn_dkv_splits(
+                            b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=bool(causal)), (b, hq, hkv, s, dh, causal)
+                    assert lib.mtp_attn_bwd_workspace_bytes(b, hq, hkv, s, dh) == plan.attn_bwd_workspace_bytes(
+                        b=b, hq=hq, hkv=hkv, s=s, dh=dh)
+
+
 FAKE = 0x100000  # aligned, never dereferenced: every call below fails validation first
 
 

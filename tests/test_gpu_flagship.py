@@ -222,3 +222,34 @@ def test_c5_flagship_packed_attention():
         l_max = max(l_max, float((lse[:, :, ps].double() - ol).abs().max()))
         a += n
     _assert_attn(stats, o_max, o_peak, l_max)
+
+
+@pytest.mark.parametrize(("s", "d"), [(2048, 128), (4096, 128), (2048, 64), (4096, 96)])
+def test_causal_attention_split_dkv_sizes(s, d):
+    """The sizes where the dK/dV pass splits its key blocks (4 splits at 2048, 2 at 4096 for B=1,
+    Hq=32, Hkv=8, any head_dim): fp32 partials summed by the reduce kernel, same bars as C4."""
+    from mlx_train_perf.plan.launch import attn_dkv_splits
+
+    b, hq, hkv = 1, 32, 8
+    ns = attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s)
+    print(f"[attn causal split dK/dV] s={s} d={d} splits={ns}", flush=True)
+    assert ns == {2048: 4, 4096: 2}[s]
+    scale = 1.0 / math.sqrt(d)
+    q, k, v, do = _attn_gpu_inputs(b, hq, hkv, s, d, seed=s + d)
+    o, lse, dq, dk, dv = _kernel_attn(q, k, v, do, scale)
+    grp = hq // hkv
+    stats = {n: _RelL2() for n in ("O", "dQ", "dK", "dV")}
+    o_max = l_max = o_peak = 0.0
+    for kvh in range(hkv):
+        hs, ks = slice(kvh * grp, (kvh + 1) * grp), slice(kvh, kvh + 1)
+        oo, ol = oatt.attention_forward(q[:, hs], k[:, ks], v[:, ks], scale=scale, dtype=torch.float64)
+        gq, gk, gv = oatt.attention_backward(q[:, hs], k[:, ks], v[:, ks], oo, ol, do[:, hs], scale=scale,
+                                             dtype=torch.float64)
+        stats["O"].add(o[:, hs], oo)
+        stats["dQ"].add(dq[:, hs], gq)
+        stats["dK"].add(dk[:, ks], gk)
+        stats["dV"].add(dv[:, ks], gv)
+        o_max = max(o_max, float((o[:, hs].double() - oo).abs().max()))
+        o_peak = max(o_peak, float(oo.abs().max()))
+        l_max = max(l_max, float((lse[:, hs].double() - ol).abs().max()))
+    _assert_attn(stats, o_max, o_peak, l_max)

@@ -99,7 +99,11 @@ def test_batch_rows_with_different_layouts(d, hq, hkv):
     assert float((lse.double() - ol).abs().max()) <= 2e-3
     for got, want in ((dq, gq), (dk, gk), (dv, gv)):
         assert rel_l2(got, want) <= 1e-2
-    # each row alone (B=1) gives the same bits as inside the batch
+    # each row alone (B=1) gives the same bits as inside the batch (when the dK/dV size table picks
+    # the same split for B=1 as for B: the split sets the fp32 summation grouping of dK/dV)
+    from mlx_train_perf.plan.launch import attn_dkv_splits
+
+    assert attn_dkv_splits(b=1, hq=hq, hkv=hkv, s=s, dh=d) == attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=d)
     for r in range(b):
         one = _run(q[r:r + 1], k[r:r + 1], v[r:r + 1], do[r:r + 1], scale, sid[r:r + 1], sst[r:r + 1])
         for x, y in zip(one, (o, lse, dq, dk, dv)):

@@ -57,8 +57,47 @@ def test_attention_plan():
     p = plan.attn_plan(b=1, hq=32, hkv=8, s=8192)
     assert p.heads_per_workgroup == 4
     assert p.fwd_workgroups == (8192 // 32) * 8
-    assert p.dkv_workgroups == 64 * 8
+    assert p.dkv_splits == 1 and p.dkv_workgroups == 64 * 8
+    assert p.bwd_workspace_bytes == 32 * 8192 * 4          # D only: no split at the flagship
     assert plan.attn_heads_per_workgroup(6, 3) == 2 and plan.attn_heads_per_workgroup(3, 1) == 1
+
+
+def _dkv_items(b, hq, hkv, s, causal):
+    """Brute force: the (head, 64-query tile) items each 128-key block of the dK/dV pass visits."""
+    g = hq // hkv
+    blocks = []
+    for kb in range(-(-s // 128)):
+        tiles = [t for t in range(-(-s // 64)) if not causal or (t + 1) * 64 - 1 >= kb * 128]
+        blocks.append(g * len(tiles))
+    return [x for x in blocks for _ in range(b * hkv)]
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_dkv_split_table(causal):
+    """The dK/dV size table: known entries at B=1, Hq=32, Hkv=8 (8 splits at S<=1024, 4 at 2048, 2 at
+    4096, 1 from 8192), and for every shape the chosen count is the smallest of 1/2/4/8 that brings the
+    heaviest workgroup (brute-force item counts) to <= 1.15x a CU's share, the split work adds up to
+    the unsplit work, and the workspace holds D plus the partials."""
+    if causal:
+        assert [plan.attn_dkv_splits(b=1, hq=32, hkv=8, s=s) for s in (512, 1024, 2048, 4096, 8192, 16384)] == \
+            [8, 8, 4, 2, 1, 1]
+    for b, hq, hkv, s in [(1, 32, 8, 2048), (1, 32, 8, 4096), (2, 32, 8, 2048), (4, 32, 8, 2048), (1, 8, 2, 300),
+                          (1, 4, 1, 1100), (1, 32, 8, 8192), (1, 64, 8, 3000), (3, 16, 4, 777)]:
+        items = _dkv_items(b, hq, hkv, s, causal)
+        share = sum(items) / plan.NUM_CU
+        ns = plan.attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, causal=causal)
+        assert ns in (1, 2, 4, 8)
+        fits = [k for k in (1, 2, 4, 8) if max(items) / k <= 1.15 * share]
+        assert ns == (fits[0] if fits else 8), (b, hq, hkv, s, ns)
+        # the kernel's split of a block of n items: [n * i // ns, n * (i + 1) // ns) for i < ns
+        for n in set(items):
+            parts = [n * (i + 1) // ns - n * i // ns for i in range(ns)]
+            assert sum(parts) == n and max(parts) - min(parts) <= 1
+    assert plan.attn_dkv_splits(b=1, hq=32, hkv=8, s=2048, dh=64) == 4   # the same table for head_dim 64/96
+    ws = plan.attn_bwd_workspace_bytes(b=1, hq=32, hkv=8, s=2048)
+    assert ws == 32 * 2048 * 4 + 4 * 2 * 8 * 2048 * 128 * 4
+    # D padded to 256 bytes before the partials (their 16-byte stores stay aligned)
+    assert plan.attn_bwd_workspace_bytes(b=1, hq=1, hkv=1, s=61) == 256 + 8 * 2 * 61 * 128 * 4
 
 
 def test_memory_planner_terms():
