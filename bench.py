@@ -234,7 +234,8 @@ def bench_lce(steps, warmup, head_kind="dense"):
             "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),
             "fwd_kernel_launches": len(fwd_ms),
             "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_marginal_peak_gb": bwd_peak / 1e9,
-            "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks,
+            "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_row_block": p.bwd_row_block,
+            "bwd_row_blocks": p.bwd_row_blocks, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks,
             "transposed_head_cache_gb": head_t / 1e9,
             "bwd_footprint_gb": (bwd_peak + head_t) / 1e9}
 

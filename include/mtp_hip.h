@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTP_ABI_VERSION 1
+#define MTP_ABI_VERSION 2
 
 /* Error codes; the Python layer maps them onto the reference's typed exceptions
  * (src/mlx_train_perf/errors.py:1-76). */
@@ -83,13 +83,23 @@ int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, 
                         void* stream);
 size_t mtp_lce_fwd_noalloc_max_workspace_bytes(void);
 
-/* Vocab columns per backward chunk for a workspace budget (bytes); a multiple of 256. */
+/* Rows per backward block for a workspace budget (bytes): n when the whole padded vocab's gradient
+ * tiles for all rows fit the budget; else a multiple of 256 (n split in 2 or 4 blocks) whose
+ * whole-vocab gradient tiles fit it while the dH product keeps >= 256 output tiles per block;
+ * else n (the vocab is chunked instead). Replaces the reference's chunk budgeting
+ * (core/kernel/launch.py:63-72), which bounds the per-dispatch size. */
+int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
+
+/* Vocab columns per backward chunk, a multiple of 256, when all n rows form one block (a trainable
+ * head, or mtp_lce_bwd_row_block(...) == n) for a workspace budget (bytes). With a smaller row block
+ * the chunk is the whole padded vocab, round_up(v, 256). */
 int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
-/* Workspace bytes needed by mtp_lce_bwd at a given chunk: the bf16 gradient tile buffer
- * [n][chunk + 64] (the row pitch is padded off a power of two) plus, when more than one chunk is
- * needed, an fp32 [n][d] dH accumulator. */
-size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk);
+/* Workspace bytes needed by mtp_lce_bwd at a given chunk and row block (0 or >= n: all rows): the
+ * bf16 gradient tile buffer [row_block][chunk + 64] (the row pitch is padded off a power of two)
+ * plus, when more than one chunk is needed, an fp32 [row_block][d] dH accumulator. */
+size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
+                                   int64_t row_block);
 
 /* Row pitch (elements) of the transposed dense head used by mtp_lce_bwd: round_up(v, 256) + 64. */
 int64_t mtp_lce_head_t_ld(int64_t v);
@@ -109,6 +119,8 @@ int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scale
  * is frozen and must pass d_w = NULL. lse is the forward's saved output (no recompute of the forward).
  * w_t (optional) is the head transposed by mtp_lce_head_transpose; it must hold the values the
  * kernels use for the head and only changes how the dH product reads it (faster when given).
+ * row_block (0 = all rows; else a multiple of 256) processes the rows in blocks that reuse one
+ * gradient buffer; d_w requires all rows in one block.
  * Replaces: the kernel-path vjps _ce_vjp / _ce_frozen_vjp / quantized _ce_vjp
  * (core/loss.py:242-298,322-349) that call chunked_backward (core/chunked.py:52-90, d_w at :90);
  * design of the fused 2-GEMM backward K4 (core/kernel/source.py:475-611) and of the d_w kernel K5
@@ -116,8 +128,8 @@ int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scale
 int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32_t* w_q,
                 const void* scales, const void* biases, const int64_t* targets, int64_t n, int64_t d,
                 int64_t v, int32_t head_kind, int64_t ignore_index, const float* lse,
-                const float* d_nll, void* d_hidden, void* d_w, int64_t chunk, void* workspace,
-                size_t workspace_bytes, void* stream);
+                const float* d_nll, void* d_hidden, void* d_w, int64_t chunk, int64_t row_block,
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------------
  * (B) Flash attention. Layouts (attention/reference.py:22-25): q [b][hq][s][dh],

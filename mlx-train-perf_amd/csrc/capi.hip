@@ -169,11 +169,27 @@ int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, 
   return ok();
 }
 
+int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+  if (n < 1 || d < 1 || v < 1) return 0;
+  const int64_t vpad = round_up(v, kTile);
+  const size_t row_bytes = (size_t)(vpad + mtp::kGPitchPad) * 2;  // one row of gradient tiles
+  if ((size_t)n * row_bytes <= budget_bytes) return n;
+  // Split the rows in 2 or 4 blocks while each block's whole-vocab G fits the budget and its dH
+  // product keeps at least one 256 x 256 output tile per CU; otherwise chunk the vocab instead.
+  for (int64_t parts = 2; parts <= 4; parts *= 2) {
+    const int64_t rows = round_up((n + parts - 1) / parts, kTile);
+    if ((rows / kTile) * ((d + kTile - 1) / kTile) < mtp::kNumCU) break;
+    if ((size_t)rows * row_bytes <= budget_bytes) return rows;
+  }
+  return n;
+}
+
 int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
   if (n < 1 || d < 1 || v < 1) return 0;
   const int64_t vpad = round_up(v, kTile);
-  // One chunk if the whole padded vocab fits the budget; otherwise the budget also carries the
-  // fp32 dH accumulator. Gradient-tile rows are chunk + kGPitchPad elements apart.
+  // All n rows in one block: one chunk if the whole padded vocab fits the budget; otherwise the
+  // budget also carries the fp32 dH accumulator. Gradient-tile rows are chunk + kGPitchPad
+  // elements apart.
   if ((size_t)n * (size_t)(vpad + mtp::kGPitchPad) * 2 <= budget_bytes) return vpad;
   const size_t acc = (size_t)n * (size_t)d * 4;
   const size_t rest = budget_bytes > acc ? budget_bytes - acc : 0;
@@ -183,12 +199,14 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) 
   return c;
 }
 
-size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk) {
+size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
+                                   int64_t row_block) {
   (void)head_kind;
   if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
+  if (row_block < 1 || row_block > n) row_block = n;
   const int64_t nchunks = (v + chunk - 1) / chunk;
-  size_t bytes = (size_t)n * (size_t)(chunk + mtp::kGPitchPad) * 2;
-  if (nchunks > 1) bytes += (size_t)n * (size_t)d * 4;
+  size_t bytes = (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2;
+  if (nchunks > 1) bytes += (size_t)row_block * (size_t)d * 4;
   return bytes;
 }
 
@@ -218,7 +236,7 @@ int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scale
 int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32_t* w_q, const void* scales,
                 const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind,
                 int64_t ignore_index, const float* lse, const float* d_nll, void* d_hidden, void* d_w, int64_t chunk,
-                void* workspace, size_t workspace_bytes, void* stream) {
+                int64_t row_block, void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
   if (rc) return rc;
   if (w_t && !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w_t must be 16-byte aligned");
@@ -226,16 +244,22 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
-  const size_t need = mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk);
+  if (row_block == 0 || row_block > n) row_block = n;
+  if (row_block < n && (row_block < 0 || row_block % kTile))
+    return fail(MTP_ERR_INPUT, "row_block must be 0, >= n, or a positive multiple of 256 (got %lld)", (long long)row_block);
+  if (d_w && row_block < n)
+    return fail(MTP_ERR_INPUT, "a trainable head (d_w) sums over every row: row_block must cover all n=%lld rows", (long long)n);
+  const size_t need = mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk, row_block);
   if (!workspace || workspace_bytes < need)
-    return fail(MTP_ERR_WORKSPACE, "lce backward needs a workspace of %zu bytes at chunk=%lld (got %zu)", need, (long long)chunk, workspace ? workspace_bytes : (size_t)0);
+    return fail(MTP_ERR_WORKSPACE, "lce backward needs a workspace of %zu bytes at chunk=%lld, row_block=%lld (got %zu)", need, (long long)chunk, (long long)row_block, workspace ? workspace_bytes : (size_t)0);
   if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
   mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
-  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)n * (size_t)(chunk + mtp::kGPitchPad) * 2);
+  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2);
   mtp::LceHead head = make_head(w, w_q, scales, biases, head_kind);
   head.wt = static_cast<const mtp::bf16_t*>(w_t);
   hipError_t e = mtp::launch_lce_bwd(head, static_cast<const mtp::bf16_t*>(hidden),
                                      targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
+                                     (int)row_block,
                                      static_cast<mtp::bf16_t*>(d_hidden), static_cast<mtp::bf16_t*>(d_w), gbuf, acc32,
                                      static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce backward launch failed: %s", hipGetErrorString(e));

@@ -1451,9 +1451,10 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
   return hipGetLastError();
 }
 
-hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
-                          const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
-                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
+// One block of rows [0, N) of the backward (all its vocab chunks).
+static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
+                               const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
+                               bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   const int nchunks = (V + chunk - 1) / chunk;
@@ -1506,6 +1507,23 @@ hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targ
       e = hipGetLastError();
       if (e != hipSuccess) return e;
     }
+  }
+  return hipSuccess;
+}
+
+// The backward in blocks of row_block rows (a multiple of 256): each block's gradient tiles reuse
+// the one G buffer, and its dH rows are final after its last vocab chunk. A trainable head (dW)
+// sums over every row, so it takes a single block.
+hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
+                          const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
+  if (dW != nullptr || row_block >= N)
+    return lce_bwd_rows(h, H, targets, lse, dnll, N, D, V, ignore_index, chunk, dH, dW, Gbuf, acc32, stream);
+  for (int r0 = 0; r0 < N; r0 += row_block) {
+    const int rows = (N - r0 < row_block) ? N - r0 : row_block;
+    hipError_t e = lce_bwd_rows(h, H + (long)r0 * D, targets + r0, lse + r0, dnll + r0, rows, D, V, ignore_index,
+                                chunk, dH + (long)r0 * D, nullptr, Gbuf, acc32, stream);
+    if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -35,7 +35,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
                           hipStream_t stream);
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
-                          const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
+                          const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
                           bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream);
 
 struct AttnShape {

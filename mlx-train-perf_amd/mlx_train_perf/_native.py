@@ -31,6 +31,7 @@ from mlx_train_perf.errors import (
 LIB_NAME = "libmtp_hip.so"
 LIB_PATH = Path(os.environ.get("MTP_HIP_LIB", str(Path(__file__).resolve().parent / LIB_NAME)))
 
+ABI_VERSION = 2
 MTP_OK = 0
 MTP_ERR_INPUT = -1
 MTP_ERR_UNSUPPORTED = -2
@@ -58,14 +59,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
                                            _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
                                            _c_void_p]),
     "mtp_lce_fwd_noalloc_max_workspace_bytes": (_size, []),
+    "mtp_lce_bwd_row_block": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_chunk": (_i64, [_i64, _i64, _i64, _size]),
-    "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64]),
+    "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64, _i64]),
     "mtp_lce_head_t_ld": (_i64, [_i64]),
     "mtp_lce_head_transpose": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,
                                               _c_void_p, _c_void_p]),
     "mtp_lce_bwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
-                                   _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+                                   _c_void_p, _i64, _i64, _c_void_p, _size, _c_void_p]),
     "mtp_attn_fwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
                                     _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
     "mtp_attn_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
@@ -98,8 +100,9 @@ def load() -> ctypes.CDLL:
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.mtp_abi_version() != 1:
-            raise MissingDependencyError(f"{LIB_PATH} has ABI version {lib.mtp_abi_version()}, expected 1")
+        if lib.mtp_abi_version() != ABI_VERSION:
+            raise MissingDependencyError(f"{LIB_PATH} has ABI version {lib.mtp_abi_version()}, expected "
+                                         f"{ABI_VERSION}; rebuild it")
         _lib = lib
         return lib
 

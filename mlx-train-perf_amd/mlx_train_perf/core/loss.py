@@ -317,18 +317,24 @@ class _KernelLCE(torch.autograd.Function):
         hidden2, targets2, lse = ctx.saved_tensors
         w, w_q, scales, biases, head_kind, v = ctx.head
         n, d = hidden2.shape
-        chunk = ctx.bwd_chunk or lib.mtp_lce_bwd_chunk(n, d, v, _plan.lce_bwd_budget_bytes())
-        chunk = min(max(256, (chunk + 255) // 256 * 256), (v + 255) // 256 * 256)
-        ws_bytes = lib.mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk)
+        d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
+        vpad = (v + 255) // 256 * 256
+        if ctx.bwd_chunk:   # an explicit vocab chunk: all rows in one block
+            chunk, rows = min(max(256, (ctx.bwd_chunk + 255) // 256 * 256), vpad), n
+        else:
+            # Row blocks reuse one gradient buffer (a trainable head's dL/dW needs every row at once).
+            budget = _plan.lce_bwd_budget_bytes()
+            rows = n if d_w is not None else lib.mtp_lce_bwd_row_block(n, d, v, budget)
+            chunk = vpad if rows < n else lib.mtp_lce_bwd_chunk(n, d, v, budget)
+        ws_bytes = lib.mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk, rows)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
         d_hidden = torch.empty_like(hidden2)
-        d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
         w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
         ct = d_nll.to(torch.float32).contiguous()
         rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),
                              _native.ptr(scales), _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind,
                              ctx.ignore_index, lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(),
-                             _native.ptr(d_w), chunk, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
+                             _native.ptr(d_w), chunk, rows, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         return d_hidden, None, d_w, None, None, None, None, None, None, None
 

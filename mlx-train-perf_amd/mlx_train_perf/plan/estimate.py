@@ -45,8 +45,11 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
     eb = dtype_bytes(dtype)
     if impl == "kernel":
         fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)
-        c = chunk or _launch.lce_bwd_chunk(n, d, v, bwd_budget or _launch.lce_bwd_budget_bytes())
-        bwd = _launch.lce_bwd_workspace_bytes(n, d, v, c) + n * 4
+        if chunk:
+            bwd = _launch.lce_bwd_workspace_bytes(n, d, v, chunk) + n * 4
+        else:
+            p = _launch.lce_plan(n=n, v=v, d=d, budget=bwd_budget or _launch.lce_bwd_budget_bytes())
+            bwd = p.bwd_workspace_bytes + n * 4
     elif impl == "chunked":
         c = chunk or 8192
         fwd = 3 * n * min(c, v) * 4 + 2 * n * 4

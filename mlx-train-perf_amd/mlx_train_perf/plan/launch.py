@@ -5,7 +5,8 @@ The reference plans Metal dispatches against a GPU-watchdog time budget
 watchdog on compute queues, so every op is one launch sequence and the planner's job is geometry and
 workspace: how many vocab splits the LCE forward uses, how wide a backward vocab chunk may be for a
 workspace budget, and the attention grid. The integer formulas here mirror the C-ABI's
-(mlx-train-perf_amd/csrc/lce_kernels.hip lce_fwd_nsplit; capi.hip mtp_lce_bwd_chunk) so that plans
+(mlx-train-perf_amd/csrc/lce_kernels.hip lce_fwd_nsplit; capi.hip mtp_lce_bwd_row_block, mtp_lce_bwd_chunk;
+attn_kernels.hip attn_dkv_nsplit) so that plans
 can be checked and sized on the CPU; a GPU test asserts they agree with the library.
 """
 from __future__ import annotations
@@ -16,11 +17,11 @@ from dataclasses import dataclass
 NUM_CU = 256        # MI355X compute units (8 XCDs x 32)
 TILE = 256          # LCE workgroup tile edge (rows and vocab columns)
 ATTN_TILE = 64      # attention key/query tile
-# Bytes of backward workspace (bf16 gradient chunk + fp32 dH when chunked). 3 GiB holds the whole
-# padded vocab of a 151936-entry head at 8192 tokens (2.49 GB), so the flagship backward runs as
-# one chunk: no fp32 dH read-modify-write and two launches instead of six (1.6% faster than three
-# chunks at 1 GiB). Small next to the 288 GB of HBM; MTP_LCE_BWD_BUDGET overrides it.
-DEFAULT_LCE_BWD_BUDGET = 3 << 30
+# Bytes of backward workspace (bf16 gradient tiles + fp32 dH when the vocab is chunked). 1.5 GiB
+# holds the whole padded vocab of a 151936-entry head for half of 8192 tokens (1.25 GB), so the
+# flagship backward runs as two row blocks of one vocab chunk each: G never holds the full (N, V)
+# matrix, and there is no fp32 dH read-modify-write. MTP_LCE_BWD_BUDGET overrides it.
+DEFAULT_LCE_BWD_BUDGET = 3 << 29
 
 
 # Gradient-tile rows are chunk + 64 elements apart: a pitch that is a multiple of a large power of
@@ -60,6 +61,23 @@ def lce_fwd_workspace_bytes(n: int, v: int) -> int:
     return 2 * lce_fwd_splits(n, v) * n * 4
 
 
+def lce_bwd_row_block(n: int, d: int, v: int, budget: int) -> int:
+    """Rows per backward block (mirror of mtp_lce_bwd_row_block): all n when the whole padded
+    vocab's gradient tiles fit the budget; else n split in 2 or 4 blocks (a multiple of 256 rows)
+    whose whole-vocab tiles fit it while the dH product keeps >= NUM_CU output tiles; else n."""
+    vpad = -(-v // TILE) * TILE
+    row_bytes = (vpad + G_PITCH_PAD) * 2
+    if n * row_bytes <= budget:
+        return n
+    for parts in (2, 4):
+        rows = -(-(-(-n // parts)) // TILE) * TILE
+        if (rows // TILE) * -(-d // TILE) < NUM_CU:
+            break
+        if rows * row_bytes <= budget:
+            return rows
+    return n
+
+
 def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
     """Vocab columns per backward chunk (multiple of 256) for a workspace budget in bytes."""
     vpad = -(-v // TILE) * TILE
@@ -71,27 +89,33 @@ def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
     return min(max(c, TILE), vpad)
 
 
-def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int) -> int:
-    """bf16 gradient tiles [n][chunk + G_PITCH_PAD] plus the fp32 dH accumulator when >1 chunk."""
+def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int | None = None) -> int:
+    """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD] plus the fp32 dH accumulator when >1 chunk."""
+    rows = n if not row_block or row_block > n else row_block
     nchunks = -(-v // chunk)
-    return n * (chunk + G_PITCH_PAD) * 2 + (n * d * 4 if nchunks > 1 else 0)
+    return rows * (chunk + G_PITCH_PAD) * 2 + (rows * d * 4 if nchunks > 1 else 0)
 
 
 @dataclass(frozen=True)
 class LcePlan:
     fwd_splits: int
     fwd_workspace_bytes: int
+    bwd_row_block: int
+    bwd_row_blocks: int
     bwd_chunk: int
     bwd_chunks: int
     bwd_workspace_bytes: int
 
 
-def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None) -> LcePlan:
+def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None, trainable: bool = False) -> LcePlan:
+    """Forward splits and backward geometry. A trainable head's dL/dW sums over every row, so its
+    backward takes all rows in one block (the vocab is chunked instead when they do not fit)."""
     b = lce_bwd_budget_bytes() if budget is None else budget
-    chunk = lce_bwd_chunk(n, d, v, b)
+    rows = n if trainable else lce_bwd_row_block(n, d, v, b)
+    chunk = -(-v // TILE) * TILE if rows < n else lce_bwd_chunk(n, d, v, b)
     return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=lce_fwd_workspace_bytes(n, v),
-                   bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
-                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk))
+                   bwd_row_block=rows, bwd_row_blocks=-(-n // rows), bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
+                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows))
 
 
 def attn_heads_per_workgroup(hq: int, hkv: int) -> int:

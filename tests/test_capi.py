@@ -29,18 +29,24 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(_native.SIGNATURES) >= declared - set()  # every export has a Python signature
-    assert lib.mtp_abi_version() == 1
+    assert lib.mtp_abi_version() == _native.ABI_VERSION == 2
 
 
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1)])
 def test_plans_agree_with_python_planner(n, d, v):
     lib = _native.load()
     assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, 0) == plan.lce_fwd_workspace_bytes(n, v)
-    for budget in (1 << 20, 1 << 26, 1 << 30, 1 << 34):
+    for budget in (1 << 20, 1 << 26, 1 << 30, 3 << 29, 1 << 34):
         c = lib.mtp_lce_bwd_chunk(n, d, v, budget)
         assert c == plan.lce_bwd_chunk(n, d, v, budget)
         assert c % 256 == 0 and c >= 256
-        assert lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, c) == plan.lce_bwd_workspace_bytes(n, d, v, c)
+        rb = lib.mtp_lce_bwd_row_block(n, d, v, budget)
+        assert rb == plan.lce_bwd_row_block(n, d, v, budget)
+        for rows in (0, n, rb):
+            assert lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, c, rows) == plan.lce_bwd_workspace_bytes(n, d, v, c, rows)
+        p = plan.lce_plan(n=n, v=v, d=d, budget=budget)
+        assert p.bwd_row_block == rb
+        assert p.bwd_workspace_bytes == lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, p.bwd_chunk, rb)
     assert lib.mtp_attn_bwd_workspace_bytes(1, 32, 8, 8192, 128) == plan.attn_plan(b=1, hq=32, hkv=8, s=8192).bwd_workspace_bytes
 
 
@@ -79,12 +85,17 @@ def test_lce_refusals():
     assert _lce_fwd(ws_bytes=8) == _native.MTP_ERR_WORKSPACE
     assert "workspace" in _native.last_error()
     lib = _native.load()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100, FAKE, 1 << 20, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100, 0, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_INPUT and "multiple of 256" in _native.last_error()
-    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, FAKE, 16, None)
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, 0, FAKE, 16, None)
     assert rc == _native.MTP_ERR_WORKSPACE
-    rc = lib.mtp_lce_bwd(FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, FAKE, 1 << 20, None)
+    rc = lib.mtp_lce_bwd(FAKE, None, None, FAKE, FAKE, FAKE, FAKE, 16, 64, 100, 1, -100, FAKE, FAKE, FAKE, FAKE, 256, 0, FAKE, 1 << 20, None)
     assert rc == _native.MTP_ERR_UNSUPPORTED and "frozen" in _native.last_error()
+    # row blocks: a multiple of 256 below n, and never with a trainable head's d_w
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 1024, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 256, 300, FAKE, 1 << 30, None)
+    assert rc == _native.MTP_ERR_INPUT and "row_block" in _native.last_error()
+    rc = lib.mtp_lce_bwd(FAKE, FAKE, None, None, None, None, FAKE, 1024, 64, 100, 0, -100, FAKE, FAKE, FAKE, FAKE, 256, 512, FAKE, 1 << 30, None)
+    assert rc == _native.MTP_ERR_INPUT and "trainable" in _native.last_error()
     assert lib.mtp_lce_head_t_ld(151936) == 152064 + 64 and lib.mtp_lce_head_t_ld(1) == 256 + 64
     assert lib.mtp_lce_head_transpose(FAKE, None, None, None, 100, 36, 0, FAKE, None) == _native.MTP_ERR_UNSUPPORTED
     assert lib.mtp_lce_head_transpose(None, None, None, None, 100, 64, 0, FAKE, None) == _native.MTP_ERR_INPUT

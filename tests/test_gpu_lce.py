@@ -251,3 +251,48 @@ def test_transposed_head_cache_keeps_two_heads():
     gc.collect()
     grad(0)
     assert L.transposed_head_cache_bytes() == per_head
+
+
+@pytest.mark.parametrize(("n", "d", "v", "row_block", "head"), [(1000, 256, 3000, 256, "dense"), (700, 128, 2100, 512, "dense"),
+                                                                (600, 128, 1500, 256, "q4")])
+def test_backward_row_blocks_match_all_rows(n, d, v, row_block, head):
+    """mtp_lce_bwd in row blocks (one gradient buffer reused per block) gives dH bitwise equal to one
+    all-rows block: every G element and every dH tile is computed the same way either way."""
+    from mlx_train_perf import _native
+
+    print(f"[lce bwd row blocks] n={n} d={d} v={v} row_block={row_block} head={head}", flush=True)
+    lib = _native.load()
+    h, w, t = lce_inputs(n, d, v, seed=n + row_block)
+    hd, td = h.cuda(), t.cuda()
+    if head == "dense":
+        kind, wd = _native.HEAD_DENSE, w.cuda()
+        ptrs, keep = (wd.data_ptr(), None, None, None), (wd,)
+    else:
+        kind = _native.HEAD_Q4
+        keep = tuple(x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))
+        ptrs = (None, keep[0].data_ptr(), keep[1].data_ptr(), keep[2].data_ptr())
+    fws = lib.mtp_lce_fwd_workspace_bytes(n, d, v, kind)
+    ws = torch.empty(fws, dtype=torch.uint8, device="cuda")
+    nll, lse, tgt = (torch.empty(n, device="cuda") for _ in range(3))
+    stream = torch.cuda.current_stream().cuda_stream
+    _native.check(lib.mtp_lce_fwd(hd.data_ptr(), *ptrs, td.data_ptr(), n, d, v, kind, IGN, nll.data_ptr(),
+                                  lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), fws, stream), domain="loss")
+    ct = _cotangent(t).cuda()
+    chunk = (v + 255) // 256 * 256
+    outs = []
+    for rb in (0, row_block):
+        bws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, kind, chunk, rb)
+        assert rb == 0 or bws < lib.mtp_lce_bwd_workspace_bytes(n, d, v, kind, chunk, 0)
+        bw = torch.empty(bws, dtype=torch.uint8, device="cuda")
+        dh = torch.full((n, d), 7.0, dtype=torch.bfloat16, device="cuda")
+        w_ptr, wq_ptr, sc_ptr, bi_ptr = ptrs
+        _native.check(lib.mtp_lce_bwd(hd.data_ptr(), w_ptr, None, wq_ptr, sc_ptr, bi_ptr, td.data_ptr(), n, d, v,
+                                      kind, IGN, lse.data_ptr(), ct.data_ptr(), dh.data_ptr(), None, chunk, rb,
+                                      bw.data_ptr(), bws, stream), domain="loss")
+        torch.cuda.synchronize()
+        outs.append(dh.cpu())
+    assert torch.equal(outs[0], outs[1])
+    wf = w if head == "dense" else oquant.dequantize_affine(*(x.cpu() for x in keep), dtype=torch.float32)
+    _, olse, _ = olce.forward(h, wf, t, ignore_index=IGN)
+    odh = olce.backward(h, wf, t, olse, ct.cpu(), ignore_index=IGN, dtype=torch.float64)
+    assert rel_l2(outs[1], odh) <= 1e-2

@@ -53,6 +53,27 @@ def test_backward_chunk_fits_budget_when_possible(budget):
         assert -(-v // c) == 1 and ws == n * (c + 64) * 2
 
 
+def test_backward_row_blocks():
+    """The default budget (1.5 GiB) runs the flagship backward as two row blocks of one whole-vocab
+    chunk each: G holds half the (N, V) gradient, there is no fp32 dH accumulator, and each block's
+    dH product still has one 256 x 256 output tile per CU. A trainable head keeps one block."""
+    n, d, v = 8192, 4096, 151936
+    p = plan.lce_plan(n=n, v=v, d=d)
+    assert plan.DEFAULT_LCE_BWD_BUDGET == 3 << 29
+    assert (p.bwd_row_block, p.bwd_row_blocks, p.bwd_chunks) == (4096, 2, 1)
+    assert p.bwd_workspace_bytes == 4096 * (152064 + 64) * 2 <= plan.DEFAULT_LCE_BWD_BUDGET
+    assert (4096 // 256) * (4096 // 256) >= plan.NUM_CU
+    t = plan.lce_plan(n=n, v=v, d=d, trainable=True)
+    assert t.bwd_row_block == n and t.bwd_chunks > 1 and t.bwd_workspace_bytes <= plan.DEFAULT_LCE_BWD_BUDGET
+    # row blocks never leave fewer dH tiles than CUs: at d=1024 the flagship falls back to vocab chunks
+    assert plan.lce_bwd_row_block(n, 1024, v, 3 << 29) == n
+    # every block but the last is whole; blocks cover the rows
+    for nn in (8192, 8200, 12000):
+        rb = plan.lce_bwd_row_block(nn, d, v, 3 << 29)
+        assert rb % 256 == 0 or rb == nn
+        assert -(-nn // rb) * rb >= nn
+
+
 def test_attention_plan():
     p = plan.attn_plan(b=1, hq=32, hkv=8, s=8192)
     assert p.heads_per_workgroup == 4
