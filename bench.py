@@ -345,7 +345,40 @@ def bench_attention(steps, warmup, mode="causal", s=None):
            "fwd_marginal_peak_gb": fwd_peak / 1e9, "fwdbwd_marginal_peak_gb": fb_peak / 1e9}
     if mode == "packed":
         out["segments"] = len(lens)
+        out["tile_efficiency"] = attention_tile_efficiency(lens, s)
+    elif mode == "causal":
+        out["tile_efficiency"] = attention_tile_efficiency(None, s)
     return out
+
+
+def attention_tile_efficiency(lens: list[int] | None, s: int) -> dict:
+    """Visible (query, key) pairs / pairs in the tiles the head_dim-128 kernels visit, per head, for
+    a packed layout (`lens`) or the causal mask (None). Forward and dQ: a 32-query wave block visits
+    the 64-key tiles from its workgroup's first segment start (rounded down to 64) up to its last
+    query. dK/dV: a 128-key block visits the 64-query tiles from its first key (rounded down) up to
+    the end of its last key's segment."""
+    import bisect
+
+    if lens is None:
+        lens = [s]
+    starts, pos = [], 0
+    for n in lens:
+        starts += [pos] * n
+        pos += n
+    visible = sum(n * (n + 1) // 2 for n in lens)
+    fwd = 0
+    for q0 in range(0, s, 32):
+        q1 = min(q0 + 32, s)
+        kv0 = starts[q0] // 64 * 64
+        fwd += 32 * 64 * (-(-(q1 - kv0) // 64))
+    dkv = 0
+    for k0 in range(0, s, 128):
+        klast = min(k0 + 127, s - 1)
+        q_end = bisect.bisect_right(starts, klast)   # first position whose segment starts past klast
+        q_begin = k0 // 64 * 64
+        dkv += 128 * 64 * max(0, -(-(q_end - q_begin) // 64))
+    return {"visible_pairs": visible, "fwd_dq_visited_pairs": fwd, "dkv_visited_pairs": dkv,
+            "fwd_dq_efficiency": visible / fwd, "dkv_efficiency": visible / dkv}
 
 
 def attention_ladder(steps, warmup):
