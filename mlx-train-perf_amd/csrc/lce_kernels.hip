@@ -680,6 +680,20 @@ __device__ __forceinline__ bool xcd_rows_tile(int mtiles, int ntiles, int& m, in
   return n < ntiles;
 }
 
+// One resident round of exactly 8 x 32 workgroups (one per CU) over an M x N tile grid with
+// M % 4 == 0, N % 8 == 0 and (M / 4) (N / 8) == 8: XCD x (workgroup g runs on XCD g % 8) takes the
+// 4 x 8 rectangle (M group x % (M / 4), N group x / (M / 4)), so its 32 workgroups share 4 M-operand
+// and 8 N-operand slabs per stage in its L2. With M / 8 = 2 (a 16-tile row block) the row-grouped
+// orders give each XCD 2 x 16 tiles instead: 18 slabs per stage, and each XCD streams the whole
+// N operand. Returns false when the grid is not of this form (use the other orders then).
+__device__ __forceinline__ bool xcd_rect_tile(int mtiles, int ntiles, int& m, int& n) {
+  if (mtiles % 4 != 0 || ntiles % 8 != 0 || (mtiles / 4) * (ntiles / 8) != 8) return false;
+  const int nmg = mtiles / 4, x = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  m = 4 * (x % nmg) + (slot & 3);
+  n = 8 * (x / nmg) + (slot >> 2);
+  return true;
+}
+
 // ------------------------------------------------------------------------------------------
 // Forward: per (row tile, vocab split) workgroup, running per-token (max, sum exp2) partials.
 // A operand = head rows (vocab), B operand = hidden rows (tokens): every lane then owns whole
@@ -699,7 +713,8 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   const int g = blockIdx.x;
   const int rtiles = (N + kTile - 1) / kTile;
   int split, rt;
-  if (rtiles % 8 == 0 && nsplit % 8 == 0) {
+  if (xcd_rect_tile(rtiles, nsplit, rt, split)) {
+  } else if (rtiles % 8 == 0 && nsplit % 8 == 0) {
     const int rpx = rtiles / 8, slot = g >> 3;
     rt = (g & 7) * rpx + slot % rpx;
     split = slot / rpx;
@@ -1058,7 +1073,8 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
   const int g = blockIdx.x;
   const int rtiles = (N + kTile - 1) / kTile;
   int split, rt;
-  if (rtiles % 8 == 0 && nsplit % 8 == 0) {
+  if (xcd_rect_tile(rtiles, nsplit, rt, split)) {
+  } else if (rtiles % 8 == 0 && nsplit % 8 == 0) {
     const int rpx = rtiles / 8, slot = g >> 3;
     rt = (g & 7) * rpx + slot % rpx;
     split = slot / rpx;
@@ -1198,7 +1214,8 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   int rt, dt;
-  if (rtiles % 8 == 0) {
+  if (xcd_rect_tile(rtiles, dtiles, rt, dt)) {
+  } else if (rtiles % 8 == 0) {
     if (!xcd_rows_tile(rtiles, dtiles, rt, dt)) return;
   } else if (!xcd_tile(rtiles, dtiles, rt, dt)) {
     return;
