@@ -267,17 +267,40 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, uint32_t voff, c
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, voff, 0, 0, 0);
 }
 
-// K-contiguous operand: tile row r, k in [64 kt, 64 kt + 64) of a row-major [rows][ld] matrix.
-// LDS rows are 128 B with the swizzle of lds_off(); fragments are single ds_read_b128.
-struct DmaRowOp {
+// Swizzle of the DMA-fed row tiles (128 B LDS rows): chunk c of row r sits in chunk slot
+// c ^ swz32(r). Any 16 consecutive rows read at one chunk (the rows of an MFMA fragment) hit
+// distinct banks, as with swz(), and the pattern repeats every 32 rows: the four 32-row blocks of
+// a wave's fragments share one lane offset (block b adds 4096 b), and the copies of a partner wave
+// 32 rows on use the same lane offsets.
+__device__ __forceinline__ int swz32(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
+
+// Fragment reads of a K-contiguous row tile: one ds_read_b128 per fragment, at the lane's offset
+// XOR the k-step's chunk bits plus the block's 4096 b.
+struct RowFrags {
   static constexpr int kReads = 1;
-  static constexpr bool kProduce = false;  // the copies land in the stage as they are
+  int xo;  // lane offset of block 0, k-step 0: row (first_row + lane % 32), chunk lane / 32
+
+  template <int NB>
+  __device__ __forceinline__ void setup(int first_row) {
+    const int lane = threadIdx.x & 63;
+    const int row = first_row + (lane & 31);
+    xo = row * 128 + (((lane >> 5) ^ swz32(row)) << 4);
+  }
+  // Chunk 2 ks + lane / 32 of the row: (2 ks + h) ^ s = (h ^ s) ^ 2 ks, i.e. bits 5-6 of the offset.
+  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
+    return as_bf16x8(lds_read16(st, (xo ^ (ks << 5)) + 4096 * b));
+  }
+};
+
+// K-contiguous operand: tile row r, k in [64 kt, 64 kt + 64) of a row-major [rows][ld] matrix,
+// copied global -> LDS by buffer_load ... lds.
+struct DmaRowOp : RowFrags {
+  static constexpr bool kInline = false;
   static constexpr bool kPartner = true;   // issue2 available
   const char* base;    // tile row 0, k = 0
   long bytes;          // readable bytes from base (the tile's nrows rows)
   long row32;          // bytes of 32 rows
   uint32_t voff[4];    // per-lane byte offsets of this wave's four 1 KiB copies
-  int lo[4], sx[4];    // per-lane fragment row offsets and swizzle (per 32-row block)
 
   __device__ __forceinline__ void init(const bf16_t* b, int ld, int nrows) {
     base = reinterpret_cast<const char*>(b);
@@ -287,17 +310,16 @@ struct DmaRowOp {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int row = 64 * i + 8 * w + (L >> 3);  // copy 8 i + w covers rows 8 (8 i + w) .. +7
-      const int c = (L & 7) ^ swz(row);
+      const int c = (L & 7) ^ swz32(row);
       const int src = row < nrows ? row : nrows - 1;
       voff[i] = 2u * (uint32_t)(src * ld + 8 * c);
     }
   }
   __device__ __forceinline__ void issue(int kt, char* dst, bool live = true) const { issue_at(0, kt, dst, live); }
   // Waves 0-3 only: this wave's four copies and those of wave w + 4, whose rows are 32 further on.
-  // Their swizzle differs in chunk bit 2 (swz(r + 32) = swz(r) ^ 4 for r % 64 < 32), and with ld a
-  // multiple of 64 the chunk index sits in offset bits 4-6, so their lane offsets are voff ^ 64
-  // from a descriptor 32 rows further on. Rows past the operand's end read zeros (their results
-  // are discarded like those of the clamped rows).
+  // swz32 repeats every 32 rows, so their lane offsets are voff from a descriptor 32 rows further
+  // on. Rows past the operand's end read zeros (their results are discarded like those of the
+  // clamped rows).
   __device__ __forceinline__ void issue2(int kt, char* dst, int w, bool live = true) const {
     issue2_at(0, kt, dst, w, live);
   }
@@ -309,7 +331,7 @@ struct DmaRowOp {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       dma16(r, voff[i], dst + 1024 * (8 * i + w));
-      dma16(r2, voff[i] ^ 64u, dst + 1024 * (8 * i + w + 4));
+      dma16(r2, voff[i], dst + 1024 * (8 * i + w + 4));
     }
   }
   // Copy from the tile `shift` bytes further on with the same per-lane offsets (valid when both
@@ -322,20 +344,6 @@ struct DmaRowOp {
 #pragma unroll
     for (int i = 0; i < 4; ++i) dma16(r, voff[i], dst + 1024 * (8 * i + w));
   }
-  template <int NB>
-  __device__ __forceinline__ void setup(int first_row) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int row = first_row + 32 * b + (lane & 31);
-      lo[b] = row * 128;
-      sx[b] = swz(row) ^ (lane >> 5);
-    }
-  }
-  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
-    return as_bf16x8(lds_read16(st, lo[b] + (((2 * ks) ^ sx[b]) << 4)));
-  }
-  __device__ __forceinline__ void produce(int, char*) {}
 };
 
 // K-major operand: element (k, col) at base[k * ld + col]; the tile holds 64 k-rows x 256
@@ -346,7 +354,7 @@ struct DmaRowOp {
 // row kvalid - 1; columns at or past ncols re-read the last 8 columns.
 struct DmaTransOp {
   static constexpr int kReads = 2;
-  static constexpr bool kProduce = false;
+  static constexpr bool kInline = false;
   static constexpr bool kPartner = false;  // issue2 is never selected (kept so that calls compile)
   const char* base;    // k = 0, column 0 of the tile
   long ldb;            // row pitch in bytes
@@ -400,68 +408,69 @@ struct DmaTransOp {
     const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
     return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
   }
-  __device__ __forceinline__ void produce(int, char*) {}
 };
 
-// 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16): the packed
-// words of each 64-deep slab are copied global -> a 2 x 8 KiB LDS staging area (rows of 32 B), and
-// `produce` dequantizes them, bf16(scale * q + bias) in fp32, into the stage's bf16 A tile (the
-// DmaRowOp layout, read the same way). Thread t produces half a row: row t >> 1, k 32 (t & 1) ..
-// +31; its scale and bias are loaded one slab ahead into registers.
-constexpr int kQ4Stage = 8192;
-struct DmaQ4Op : DmaRowOp {
-  static constexpr bool kProduce = true;
-  static constexpr bool kPartner = false;
-  const char* qbase;   // packed words of tile row 0
-  long qbytes;         // readable bytes from qbase
-  const bf16_t* sc;    // scales / biases of tile row 0
-  const bf16_t* bi;
-  int D, nrows;
-  uint32_t qoff;       // lane byte offset of its 16-byte copy (row 32 w + L / 2, half L & 1)
-  char* stg;           // staging base (2 x kQ4Stage)
-  float s_n, b_n;      // scale / bias of this thread's row for the next slab to produce
+// 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16), dequantized
+// in registers. Thread t owns half a tile row: row t >> 1, k 32 (t & 1) .. +31 of each 64-deep slab,
+// i.e. 4 packed words. It loads them and the row's scale and bias for the slab straight into
+// registers (buffer loads, one stage ahead: `qn`), and while the MFMAs of stage kt run it
+// dequantizes slab kt + 1 (`qc`), bf16(scale * q + bias) in fp32, into the next stage's A tile,
+// one 16-byte LDS write per word in the row layout that RowFrags reads. The packed words never pass
+// through LDS, and the stage loop's copies are the B operand's only.
+struct RegQ4Op : RowFrags {
+  static constexpr bool kInline = true;
+  static constexpr bool kPartner = true;  // no copies of its own
+  __amdgpu_buffer_rsrc_t rq, rs, rb;      // packed words, scales, biases of the tile's rows
+  uint32_t qo, so;                        // this thread's byte offsets in them (row clamped to the last)
+  uint32_t wo;                            // LDS byte offset of its first 16-byte chunk (word 0)
+  int last;                               // index of the last slab
+  u32x4 qc, qn;
+  float sc, bc;
+  uint32_t sn, bn;  // raw bf16 bits of the next slab's scale and bias, converted by shift()
 
-  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D_, int nrows_,
-                                       char* stg_) {
-    qbase = reinterpret_cast<const char*>(wq);
-    qbytes = 4L * nrows_ * (D_ >> 3);
-    sc = sc_;
-    bi = bi_;
-    D = D_;
-    nrows = nrows_;
-    stg = stg_;
-    const int w = threadIdx.x >> 6, L = threadIdx.x & 63;
-    const int row = 32 * w + (L >> 1);
-    const int src = row < nrows ? row : nrows - 1;
-    qoff = 4u * (uint32_t)(src * (D >> 3) + 4 * (L & 1));
-  }
-  // Next tile, `rows` further on, with the same lane offsets (both tiles whole).
-  __device__ __forceinline__ void advance(int rows) {
-    qbase += 4L * rows * (D >> 3);
-    sc += (long)rows * (D >> 6);
-    bi += (long)rows * (D >> 6);
-  }
-  __device__ __forceinline__ void issue(int kt, char*, bool live = true) const {
-    const int w = threadIdx.x >> 6;
-    const __amdgpu_buffer_rsrc_t r = dma_rsrc(qbase + kt * 32, live ? qbytes - kt * 32 : 0);
-    dma16(r, qoff, stg + (kt & 1) * kQ4Stage + 1024 * w);
-  }
-  __device__ __forceinline__ void load_sb(int kt) {
-    const int row = threadIdx.x >> 1;
-    const int last = (D >> 6) - 1;  // past the last slab: reload it (branch-free; unused)
-    const long g = (long)(row < nrows ? row : nrows - 1) * (D >> 6) + (kt < last ? kt : last);
-    s_n = bf16_to_f32(sc[g]);
-    b_n = bf16_to_f32(bi[g]);
-  }
-  // Dequantize slab kt (its copies have landed) into the A tile at `stage`, then fetch the next
-  // slab's scale and bias.
-  __device__ __forceinline__ void produce(int kt, char* stage) {
+  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D, int nrows) {
     const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
-    const u32x4 q = lds_read16(stg + (kt & 1) * kQ4Stage, row * 32 + 16 * h);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) lds_write16(stage, lds_off(row, 4 * h + c), dequant8(q[c], s_n, b_n));
-    load_sb(kt + 1);
+    const int src = row < nrows ? row : nrows - 1;
+    rq = dma_rsrc(reinterpret_cast<const char*>(wq), 4L * nrows * (D >> 3));
+    rs = dma_rsrc(reinterpret_cast<const char*>(sc_), 2L * nrows * (D >> 6));
+    rb = dma_rsrc(reinterpret_cast<const char*>(bi_), 2L * nrows * (D >> 6));
+    qo = 4u * (uint32_t)(src * (D >> 3) + 4 * h);
+    so = 2u * (uint32_t)(src * (D >> 6));
+    // chunk 4 h + c of the row: (4 h + c) ^ swz32(row) = ((4 h) ^ swz32(row)) ^ c, so word c's
+    // chunk is wo ^ (c << 4) (the row offset is a multiple of 128).
+    wo = (uint32_t)(row * 128 + (((4 * h) ^ swz32(row)) << 4));
+    last = (D >> 6) - 1;
   }
+  // Packed words, scale and bias of slab kt (clamped to the last slab: the loads past the end are
+  // never used) into qc (CUR) or qn.
+  template <bool CUR>
+  __device__ __forceinline__ void load(int kt) {
+    const int k = kt < last ? kt : last;
+    const u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 32 * k, 0));
+    const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 2 * k, 0);
+    const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(rb, so, 2 * k, 0);
+    if constexpr (CUR) {
+      qc = q;
+      sc = __uint_as_float(s << 16);
+      bc = __uint_as_float(b << 16);
+    } else {
+      // Kept raw: converting here would make the wave wait for the loads at once.
+      qn = q;
+      sn = s;
+      bn = b;
+    }
+  }
+  __device__ __forceinline__ void shift() {
+    qc = qn;
+    sc = __uint_as_float(sn << 16);
+    bc = __uint_as_float(bn << 16);
+  }
+  template <int C>
+  __device__ __forceinline__ void produce_word(char* stage) const {
+    lds_write16(stage, (int)(wo ^ (C << 4)), dequant8(qc[C], sc, bc));
+  }
+  __device__ __forceinline__ void issue(int, char*, bool = true) const {}
+  __device__ __forceinline__ void issue2(int, char*, int, bool = true) const {}
 };
 
 template <class OA, class OB>
@@ -510,6 +519,25 @@ __device__ __forceinline__ void dma_sched_mix() {
   }
 }
 
+// A k-step of a 4-bit stage (RegQ4Op): its 8 MFMAs with the NR fragment reads packed into the
+// first kDmaFront as in dma_sched, and the NW dequantized words of the next stage (about 24 VALU
+// instructions and one 16-byte LDS write each) spread over the MFMAs, each write after its word's
+// arithmetic.
+template <int NR, int NW, int S = 0>
+__device__ __forceinline__ void dma_sched_q4() {
+  if constexpr (S < 8) {
+    constexpr int F = kDmaFront;
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    constexpr int r = S < F ? NR * (S + 1) / F - NR * S / F : 0;
+    if constexpr (r > 0) __builtin_amdgcn_sched_group_barrier(0x100, r, 0);
+    constexpr int v = 24 * NW * (S + 1) / 8 - 24 * NW * S / 8;
+    __builtin_amdgcn_sched_group_barrier(0x002, v, 0);
+    constexpr int wr = NW * (S + 1) / 8 - NW * S / 8;
+    if constexpr (wr > 0) __builtin_amdgcn_sched_group_barrier(0x200, wr, 0);
+    dma_sched_q4<NR, NW, S + 1>();
+  }
+}
+
 // Last k-step of a stage: its 8 MFMAs interleaved with the 8 copies of the stage after next and
 // the NR reads of the next stage's first fragments.
 template <int NR, int S = 0>
@@ -547,7 +575,10 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   if (!pre) {
-    if constexpr (OA::kProduce) oa.load_sb(0);
+    if constexpr (OA::kInline) {
+      oa.template load<true>(0);
+      oa.template load<false>(1);
+    }
     oa.issue(0, lds);
     ob.issue(0, lds + 32768);
     if (nk > 1) {
@@ -555,9 +586,15 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       ob.issue(1, lds + kDmaStage + 32768);
     }
   }
-  if constexpr (OA::kProduce) {
+  if constexpr (OA::kInline) {
+    // Stage 0's A tile is dequantized here, with nothing to overlap; each later one during the
+    // k-steps of the stage before it.
     if (pre) wait_vmcnt<PRE_VM>(); else wait_vmcnt<0>();
-    oa.produce(0, lds);
+    oa.template produce_word<0>(lds);
+    oa.template produce_word<1>(lds);
+    oa.template produce_word<2>(lds);
+    oa.template produce_word<3>(lds);
+    oa.shift();
     wait_lgkmcnt0();
   } else {
     if (pre) wait_vmcnt<PRE_VM>();
@@ -579,22 +616,38 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     for (int kt = 0; kt + 1 < nk; ++kt) {
       char* cur = lds + ((kt & 1) ? kDmaStage : 0);
       char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
-      dma_read_frags(oa, ob, cur, 1, ga, gb);
-      dma_mfma(fa, fb, acc);
-      dma_sched<NR>();
-      dma_read_frags(oa, ob, cur, 2, fa, fb);
-      dma_mfma(ga, gb, acc);
-      dma_sched<NR>();
-      dma_read_frags(oa, ob, cur, 3, ga, gb);
-      dma_mfma(fa, fb, acc);
-      dma_sched<NR>();
+      if constexpr (OA::kInline) {
+        // 4-bit A: load slab kt + 2 into qn, and dequantize slab kt + 1 (qc) into the next stage's
+        // A tile (free since the last barrier) between this stage's MFMAs.
+        oa.template load<false>(kt + 2);
+        dma_read_frags(oa, ob, cur, 1, ga, gb);
+        dma_mfma(fa, fb, acc);
+        oa.template produce_word<0>(nxt);
+        oa.template produce_word<1>(nxt);
+        dma_sched_q4<NR, 2>();
+        dma_read_frags(oa, ob, cur, 2, fa, fb);
+        dma_mfma(ga, gb, acc);
+        oa.template produce_word<2>(nxt);
+        dma_sched_q4<NR, 1>();
+        dma_read_frags(oa, ob, cur, 3, ga, gb);
+        dma_mfma(fa, fb, acc);
+        oa.template produce_word<3>(nxt);
+        dma_sched_q4<NR, 1>();
+      } else {
+        dma_read_frags(oa, ob, cur, 1, ga, gb);
+        dma_mfma(fa, fb, acc);
+        dma_sched<NR>();
+        dma_read_frags(oa, ob, cur, 2, fa, fb);
+        dma_mfma(ga, gb, acc);
+        dma_sched<NR>();
+        dma_read_frags(oa, ob, cur, 3, ga, gb);
+        dma_mfma(fa, fb, acc);
+        dma_sched<NR>();
+      }
       wait_lgkmcnt0();
       wait_vmcnt<0>();
-      if constexpr (OA::kProduce) {
-        oa.produce(kt + 1, nxt);
-        wait_lgkmcnt0();
-      }
       raw_barrier();
+      if constexpr (OA::kInline) oa.shift();
       const bool live = kt + 2 < nk;
       if constexpr (R == 0) {
         oa.issue(kt + 2, cur, live);
@@ -705,7 +758,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                     const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
                     float* __restrict__ part_m, float* __restrict__ part_s) {
-  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   // Workgroup g runs on XCD g % 8. When the row tiles divide into 8 groups, XCD x owns row tiles
   // [x R/8, (x+1) R/8) for every split, walked split-major: the ~32 workgroups resident on one XCD
   // then cover R/8 row tiles x 32/(R/8) splits (4 x 8 at the flagship), whose hidden and head
@@ -814,29 +867,28 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     }
     raw_barrier();
   } else if (Q4) {
-    // 4-bit head (D % 64 == 0): packed words copied to LDS and dequantized there (DmaQ4Op).
+    // 4-bit head (D % 64 == 0): packed words loaded into registers and dequantized into the A
+    // tile between the MFMAs (RegQ4Op).
     DmaRowOp ob;
     ob.init(H + (long)t0 * D, D, N - t0);
-    DmaQ4Op oa;
+    RegQ4Op oa;
     const int vb0 = vt_begin * kTile;
-    oa.init(Wq + (long)vb0 * (D >> 3), Sc + (long)vb0 * (D >> 6), Bi + (long)vb0 * (D >> 6), D, V - vb0,
-            lds + kLdsBytes);
+    oa.init(Wq + (long)vb0 * (D >> 3), Sc + (long)vb0 * (D >> 6), Bi + (long)vb0 * (D >> 6), D, V - vb0);
     bool pre = false;
     for (int vt = vt_begin; vt < vt_end; ++vt) {
       const int v0 = vt * kTile;
       const bool has_next = vt + 1 < vt_end;
       // After the last barrier of this tile `oa` is only needed for the next tile: move it there
-      // and start its first two stages.
+      // and load its first two slabs; waves 0-3 copy the first two hidden stages (theirs and their
+      // SIMD partner's, as in the stage loop).
       auto next = [&]() {
         const int v1 = v0 + kTile;
-        if (v1 + kTile <= V) oa.advance(kTile);
-        else oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, V - v1,
-                     lds + kLdsBytes);
-        oa.load_sb(0);
-        oa.issue(0, lds);
-        if (nk > 1) oa.issue(1, lds);
-        ob.issue(0, lds + 32768);
-        if (nk > 1) ob.issue(1, lds + kDmaStage + 32768);
+        oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, V - v1);
+        oa.template load<true>(0);
+        oa.template load<false>(1);
+        if (wsc >= 4) return;
+        ob.issue2(0, lds + 32768, wsc);
+        if (nk > 1) ob.issue2(1, lds + kDmaStage + 32768, wsc);
       };
       f32x16 acc[4][kNJ];
       gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next);
@@ -1068,7 +1120,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
                               const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
                               int N, int D, int V, int v_begin, int v_end, int ctiles, int nsplit, int ldg,
                               bf16_t* __restrict__ G) {
-  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + 2 * kQ4Stage : kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
 
   const int g = blockIdx.x;
   const int rtiles = (N + kTile - 1) / kTile;
@@ -1122,12 +1174,11 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
 
   DmaRowOp ob;
   ob.init(H + (long)t0 * D, D, N - t0);
-  typedef typename std::conditional<Q4 != 0, DmaQ4Op, DmaRowOp>::type OpA;
+  typedef typename std::conditional<Q4 != 0, RegQ4Op, DmaRowOp>::type OpA;
   OpA oa;
   auto init_a = [&](int v1) {
     if constexpr (Q4) {
-      oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1,
-              lds + kLdsBytes);
+      oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1);
     } else {
       oa.init(W + (long)v1 * D, D, vlim - v1);
     }
@@ -1141,12 +1192,9 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
     const bool next_whole = v0 + 2 * kTile <= vlim;
     auto next = [&]() {
       if constexpr (Q4) {
-        const int v1 = v0 + kTile;
-        if (next_whole) oa.advance(kTile);
-        else init_a(v1);
-        oa.load_sb(0);
-        oa.issue(0, lds);
-        oa.issue(1, lds);
+        init_a(v0 + kTile);
+        oa.template load<true>(0);
+        oa.template load<false>(1);
       } else {
         // Every wave copies here (with only waves 0-3 copying, as in the forward, this kernel
         // measured 0.2% slower).

@@ -74,12 +74,18 @@ __device__ __forceinline__ void transpose8x8(const u32x4 (&x)[8], u32x4 (&y)[8])
 
 // Dequantize one packed word (8 four-bit values, low nibble first) with an affine
 // scale/bias into 8 bf16 values (w = scale * q + bias, computed in fp32).
+// The even nibbles are spread into the bytes of one word and the odd ones into another, so each
+// value converts with a single byte-to-float (v_cvt_f32_ubyte0..3).
 __device__ __forceinline__ u32x4 dequant8(uint32_t q, float s, float b) {
+  uint32_t ev = q & 0x0F0F0F0Fu, od = (q >> 4) & 0x0F0F0F0Fu;
+  // Hide the masks from the compiler, which would otherwise narrow each conversion to a 4-bit
+  // field extract plus a byte-0 conversion (two instructions instead of one).
+  asm("" : "+v"(ev), "+v"(od));
   u32x4 r;
 #pragma unroll
   for (int p = 0; p < 4; ++p) {
-    const float lo = __builtin_fmaf(s, (float)((q >> (8 * p)) & 0xFu), b);
-    const float hi = __builtin_fmaf(s, (float)((q >> (8 * p + 4)) & 0xFu), b);
+    const float lo = __builtin_fmaf(s, (float)((ev >> (8 * p)) & 0xFFu), b);
+    const float hi = __builtin_fmaf(s, (float)((od >> (8 * p)) & 0xFFu), b);
     r[p] = pack_bf16x2(lo, hi);
   }
   return r;
