@@ -412,62 +412,84 @@ struct DmaTransOp {
 
 // 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16), dequantized
 // in registers. Thread t owns half a tile row: row t >> 1, k 32 (t & 1) .. +31 of each 64-deep slab,
-// i.e. 4 packed words. It loads them and the row's scale and bias for the slab straight into
-// registers (buffer loads, one stage ahead: `qn`), and while the MFMAs of stage kt run it
-// dequantizes slab kt + 1 (`qc`), bf16(scale * q + bias) in fp32, into the next stage's A tile,
-// one 16-byte LDS write per word in the row layout that RowFrags reads. The packed words never pass
-// through LDS, and the stage loop's copies are the B operand's only.
+// i.e. 4 packed words, which it loads straight into registers one stage ahead (`qn`). While the
+// MFMAs of stage kt run it dequantizes slab kt + 1 (`qc`), bf16(scale * q + bias) in fp32, into
+// the next stage's A tile, one 16-byte LDS write per word in the row layout that RowFrags reads.
+// The scales and biases go through LDS: the copier threads (waves 0-3, thread t for row t) load
+// those of slab kt + 2 during stage kt and store them packed (scale | bias << 16) into a two-slot
+// ring before the barrier; after it every thread reads its row's pair. So the non-copier waves
+// issue one vector-memory load per stage.
+constexpr int kQ4SbBytes = 2 * 256 * 4;  // the scale/bias ring, after the four operand tiles
 struct RegQ4Op : RowFrags {
   static constexpr bool kInline = true;
   static constexpr bool kPartner = true;  // no copies of its own
   __amdgpu_buffer_rsrc_t rq, rs, rb;      // packed words, scales, biases of the tile's rows
-  uint32_t qo, so;                        // this thread's byte offsets in them (row clamped to the last)
+  uint32_t qo;                            // this thread's byte offset in the packed words
+  uint32_t so;                            // copier thread t: byte offset of row t's scale and bias
   uint32_t wo;                            // LDS byte offset of its first 16-byte chunk (word 0)
   int last;                               // index of the last slab
+  char* ring;                             // the scale/bias ring (2 slots x 256 rows x 4 B)
   u32x4 qc, qn;
-  float sc, bc;
-  uint32_t sn, bn;  // raw bf16 bits of the next slab's scale and bias, converted by shift()
+  uint32_t sb;                            // packed raw scale and bias of the slab being dequantized
+  uint32_t s0, b0, s1, b1;                // copier threads: raw scale / bias of slabs in flight
 
-  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D, int nrows) {
-    const int row = threadIdx.x >> 1, h = threadIdx.x & 1;
+  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D, int nrows,
+                                       char* ring_) {
+    const int t = threadIdx.x, row = t >> 1, h = t & 1;
     const int src = row < nrows ? row : nrows - 1;
+    const int srow = (t & 255) < nrows ? (t & 255) : nrows - 1;
     rq = dma_rsrc(reinterpret_cast<const char*>(wq), 4L * nrows * (D >> 3));
     rs = dma_rsrc(reinterpret_cast<const char*>(sc_), 2L * nrows * (D >> 6));
     rb = dma_rsrc(reinterpret_cast<const char*>(bi_), 2L * nrows * (D >> 6));
     qo = 4u * (uint32_t)(src * (D >> 3) + 4 * h);
-    so = 2u * (uint32_t)(src * (D >> 6));
+    so = 2u * (uint32_t)(srow * (D >> 6));
     // chunk 4 h + c of the row: (4 h + c) ^ swz32(row) = ((4 h) ^ swz32(row)) ^ c, so word c's
     // chunk is wo ^ (c << 4) (the row offset is a multiple of 128).
     wo = (uint32_t)(row * 128 + (((4 * h) ^ swz32(row)) << 4));
     last = (D >> 6) - 1;
+    ring = ring_;
   }
-  // Packed words, scale and bias of slab kt (clamped to the last slab: the loads past the end are
-  // never used) into qc (CUR) or qn.
+  // Packed words of slab kt (clamped to the last slab: loads past the end are never used) into qc
+  // (CUR) or qn.
   template <bool CUR>
-  __device__ __forceinline__ void load(int kt) {
+  __device__ __forceinline__ void load_q(int kt) {
     const int k = kt < last ? kt : last;
     const u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, qo, 32 * k, 0));
-    const uint32_t s = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 2 * k, 0);
-    const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(rb, so, 2 * k, 0);
-    if constexpr (CUR) {
-      qc = q;
-      sc = __uint_as_float(s << 16);
-      bc = __uint_as_float(b << 16);
+    if constexpr (CUR) qc = q; else qn = q;
+  }
+  // Copier threads: raw scale and bias of slab kt into (s0, b0) (SECOND: (s1, b1)).
+  template <bool SECOND>
+  __device__ __forceinline__ void load_sb(int kt) {
+    const int k = kt < last ? kt : last;
+    const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, so, 2 * k, 0);
+    const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(rb, so, 2 * k, 0);
+    if constexpr (SECOND) {
+      s1 = sv;
+      b1 = bv;
     } else {
-      // Kept raw: converting here would make the wave wait for the loads at once.
-      qn = q;
-      sn = s;
-      bn = b;
+      s0 = sv;
+      b0 = bv;
     }
   }
+  // Copier threads, once the loads have landed: store the pair of slab kt into its ring slot.
+  template <bool SECOND>
+  __device__ __forceinline__ void put_sb(int kt) const {
+    const uint32_t v = SECOND ? (s1 | (b1 << 16)) : (s0 | (b0 << 16));
+    *reinterpret_cast<uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x & 255)) = v;
+  }
+  // Every thread, after the barrier that follows put_sb(kt): its row's pair of slab kt.
+  __device__ __forceinline__ void get_sb(int kt) {
+    sb = *reinterpret_cast<const uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x >> 1));
+  }
+  // qc = qn where it stands: left to itself the compiler sinks the copy to the loop's top and puts
+  // a wait for the load before it there, after the next stage's copies, which it then waits for too.
   __device__ __forceinline__ void shift() {
     qc = qn;
-    sc = __uint_as_float(sn << 16);
-    bc = __uint_as_float(bn << 16);
+    asm volatile("" : "+v"(qc));
   }
   template <int C>
   __device__ __forceinline__ void produce_word(char* stage) const {
-    lds_write16(stage, (int)(wo ^ (C << 4)), dequant8(qc[C], sc, bc));
+    lds_write16(stage, (int)(wo ^ (C << 4)), dequant8(qc[C], __uint_as_float(sb << 16), __uint_as_float(sb & 0xffff0000u)));
   }
   __device__ __forceinline__ void issue(int, char*, bool = true) const {}
   __device__ __forceinline__ void issue2(int, char*, int, bool = true) const {}
@@ -576,8 +598,12 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
 
   if (!pre) {
     if constexpr (OA::kInline) {
-      oa.template load<true>(0);
-      oa.template load<false>(1);
+      oa.template load_q<true>(0);
+      oa.template load_q<false>(1);
+      if (wsc < 4) {
+        oa.template load_sb<false>(0);
+        oa.template load_sb<true>(1);
+      }
     }
     oa.issue(0, lds);
     ob.issue(0, lds + 32768);
@@ -590,11 +616,22 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     // Stage 0's A tile is dequantized here, with nothing to overlap; each later one during the
     // k-steps of the stage before it.
     if (pre) wait_vmcnt<PRE_VM>(); else wait_vmcnt<0>();
+    if (wsc < 4) {
+      oa.template put_sb<false>(0);
+      oa.template put_sb<true>(1);
+    }
+    wait_lgkmcnt0();
+    raw_barrier();
+    oa.get_sb(0);
     oa.template produce_word<0>(lds);
     oa.template produce_word<1>(lds);
     oa.template produce_word<2>(lds);
     oa.template produce_word<3>(lds);
+    oa.get_sb(1);
     oa.shift();
+    // Slab 2: the stage loop loads slab kt + 3 after its barrier, ahead of the copies.
+    oa.template load_q<false>(2);
+    if (wsc < 4) oa.template load_sb<false>(2);
     wait_lgkmcnt0();
   } else {
     if (pre) wait_vmcnt<PRE_VM>();
@@ -617,9 +654,8 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       char* cur = lds + ((kt & 1) ? kDmaStage : 0);
       char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
       if constexpr (OA::kInline) {
-        // 4-bit A: load slab kt + 2 into qn, and dequantize slab kt + 1 (qc) into the next stage's
-        // A tile (free since the last barrier) between this stage's MFMAs.
-        oa.template load<false>(kt + 2);
+        // 4-bit A: dequantize slab kt + 1 (qc) into the next stage's A tile (free since the last
+        // barrier) between this stage's MFMAs.
         dma_read_frags(oa, ob, cur, 1, ga, gb);
         dma_mfma(fa, fb, acc);
         oa.template produce_word<0>(nxt);
@@ -646,8 +682,21 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       }
       wait_lgkmcnt0();
       wait_vmcnt<0>();
+      if constexpr (OA::kInline) {
+        oa.shift();
+        if constexpr (R != 2) {
+          oa.template put_sb<false>(kt + 2);
+          wait_lgkmcnt0();
+        }
+      }
       raw_barrier();
-      if constexpr (OA::kInline) oa.shift();
+      if constexpr (OA::kInline) {
+        // Slab kt + 3 (the copiers: also its scales and biases), issued before the stage's copies
+        // so that it does not queue behind them; it has until the next barrier to land.
+        oa.get_sb(kt + 2);
+        oa.template load_q<false>(kt + 3);
+        if constexpr (R != 2) oa.template load_sb<false>(kt + 3);
+      }
       const bool live = kt + 2 < nk;
       if constexpr (R == 0) {
         oa.issue(kt + 2, cur, live);
@@ -758,7 +807,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
                     const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
                     float* __restrict__ part_m, float* __restrict__ part_s) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + kQ4SbBytes : kLdsBytes];
   // Workgroup g runs on XCD g % 8. When the row tiles divide into 8 groups, XCD x owns row tiles
   // [x R/8, (x+1) R/8) for every split, walked split-major: the ~32 workgroups resident on one XCD
   // then cover R/8 row tiles x 32/(R/8) splits (4 x 8 at the flagship), whose hidden and head
@@ -873,7 +922,8 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     ob.init(H + (long)t0 * D, D, N - t0);
     RegQ4Op oa;
     const int vb0 = vt_begin * kTile;
-    oa.init(Wq + (long)vb0 * (D >> 3), Sc + (long)vb0 * (D >> 6), Bi + (long)vb0 * (D >> 6), D, V - vb0);
+    oa.init(Wq + (long)vb0 * (D >> 3), Sc + (long)vb0 * (D >> 6), Bi + (long)vb0 * (D >> 6), D, V - vb0,
+            lds + kLdsBytes);
     bool pre = false;
     for (int vt = vt_begin; vt < vt_end; ++vt) {
       const int v0 = vt * kTile;
@@ -883,10 +933,13 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       // SIMD partner's, as in the stage loop).
       auto next = [&]() {
         const int v1 = v0 + kTile;
-        oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, V - v1);
-        oa.template load<true>(0);
-        oa.template load<false>(1);
+        oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, V - v1,
+                lds + kLdsBytes);
+        oa.template load_q<true>(0);
+        oa.template load_q<false>(1);
         if (wsc >= 4) return;
+        oa.template load_sb<false>(0);
+        oa.template load_sb<true>(1);
         ob.issue2(0, lds + 32768, wsc);
         if (nk > 1) ob.issue2(1, lds + kDmaStage + 32768, wsc);
       };
@@ -1120,7 +1173,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
                               const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
                               int N, int D, int V, int v_begin, int v_end, int ctiles, int nsplit, int ldg,
                               bf16_t* __restrict__ G) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + kQ4SbBytes : kLdsBytes];
 
   const int g = blockIdx.x;
   const int rtiles = (N + kTile - 1) / kTile;
@@ -1178,7 +1231,8 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
   OpA oa;
   auto init_a = [&](int v1) {
     if constexpr (Q4) {
-      oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1);
+      oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1,
+              lds + kLdsBytes);
     } else {
       oa.init(W + (long)v1 * D, D, vlim - v1);
     }
@@ -1193,8 +1247,12 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
     auto next = [&]() {
       if constexpr (Q4) {
         init_a(v0 + kTile);
-        oa.template load<true>(0);
-        oa.template load<false>(1);
+        oa.template load_q<true>(0);
+        oa.template load_q<false>(1);
+        if (__builtin_amdgcn_readfirstlane(w) < 4) {
+          oa.template load_sb<false>(0);
+          oa.template load_sb<true>(1);
+        }
       } else {
         // Every wave copies here (with only waves 0-3 copying, as in the forward, this kernel
         // measured 0.2% slower).
