@@ -1335,8 +1335,8 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     if (qvalid && hf == 0) dvec[qrow + qi] = dq_row;
   }
 
-  // Tile t from stage cur; the copies of tile t+1 go to stage nxt (free since the barrier that ended
-  // tile t-1).
+  // dQ pass, tile t from stage cur; the copies of tile t+1 go to stage nxt (free since the barrier
+  // that ended tile t-1).
   auto body = [&](int t, const char* cur, char* nxt) __attribute__((always_inline)) {
     const int kv0 = kv_begin + t * kKT;
     const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
@@ -1352,24 +1352,23 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         a1[db] = b + (uint32_t)(t1_ ^ (db << 6));
       }
     };
-    // S^T = K Q^T (and dP^T = V dO^T): row fragments two k16 steps ahead, the two 32-key
-    // accumulator chains interleaved.
-    f32x16 sacc[2], pacc[DQ ? 2 : 1];
+    // S^T = K Q^T and dP^T = V dO^T: row fragments one k16 step ahead, the two 32-key accumulator
+    // chains interleaved.
+    f32x16 sacc[2], pacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         sacc[kb][r] = 0.f;
-        if constexpr (DQ) pacc[kb][r] = 0.f;
+        pacc[kb][r] = 0.f;
       }
-    // Read-ahead distance in k16 steps (the dQ pass holds twice the fragments per step).
-    constexpr int RA = DQ ? 1 : 2;
-    bf16x8 rk[RA + 1][2], rv[DQ ? RA + 1 : 1][2];
+    constexpr int RA = 1;
+    bf16x8 rk[RA + 1][2], rv[RA + 1][2];
     auto rd = [&](int ks) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         rk[ks % (RA + 1)][kb] = as_bf16x8(lds_read16(kt, 32 * kb * kRowB + (kb_ ^ (ks << 5))));
-        if constexpr (DQ) rv[ks % (RA + 1)][kb] = as_bf16x8(lds_read16(vt, 32 * kb * kRowB + (kb_ ^ (ks << 5))));
+        rv[ks % (RA + 1)][kb] = as_bf16x8(lds_read16(vt, 32 * kb * kRowB + (kb_ ^ (ks << 5))));
       }
     };
 #pragma unroll
@@ -1380,7 +1379,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         sacc[kb] = mfma32(rk[ks % (RA + 1)][kb], qf[ks], sacc[kb]);
-        if constexpr (DQ) pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
+        pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
       }
       if (ks < 2 * kLd) issue_one(t + 1, nxt, ks);
       // Keep each k16 step's reads, products and copy load together (the scheduler would
@@ -1390,17 +1389,9 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     // The products above run for every wave, as they carry the copies; the rest only for a wave
     // with keys of this tile to attend to (the others meet them at the barrier either way).
     if (!skip) {
-      // Transposed fragments of the second product's tile: in flight during the softmax (forward);
-      // the dQ pass issues them after dS, when the score registers are free.
+      // Transposed fragments of K (the dQ^T products' operand), read after dS, when the score
+      // registers are free.
       bf16x8 tf[4][4];
-      if constexpr (!DQ) {
-        uint32_t a0[4], a1[4];
-        taddr(vt, a0, a1);
-        tr_slab<0>(a0, a1, tf);
-        tr_slab<1>(a0, a1, tf);
-        tr_slab<2>(a0, a1, tf);
-        tr_slab<3>(a0, a1, tf);
-      }
       // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
       // c <= thr (causal and tail bounds) and, packed, c >= lo (at or after the row's segment
       // start). Only tiles that cross the wave's diagonal, the sequence end or (packed) a segment
@@ -1422,81 +1413,183 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
           for (int r = 0; r < 16; ++r) sacc[kb][r] = visible(kb, r) ? sacc[kb][r] : kNegInf;
       }
       bf16x8 pf[4];
-      if constexpr (DQ) {
-        // dS = P (dP - D), P = exp2(scale log2(e) S - L log2(e)).
+      // dS = P (dP - D), P = exp2(scale log2(e) S - L log2(e)).
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const float p = fast_exp2(__builtin_fmaf(sacc[kb][r], scale_log2, -l2q));
-            pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
-          }
-      } else {
-        // Online softmax in the log2 domain against a reference maximum m that a row raises only
-        // when its tile maximum exceeds m by more than kRescaleLog2: its O and l are then rescaled
-        // together, otherwise probabilities up to 2^kRescaleLog2 accumulate against the old m.
-        // O / l and L = m + log2(l) are the same either way. The branch is taken by the whole wave
-        // when any row needs it (most tiles skip it), but each row decides for itself and the
-        // others multiply by exactly 1: a row's arithmetic depends only on its own scores, so rows
-        // of other packed segments sharing the wave come out bitwise the same whatever this row's
-        // keys hold.
-        {
-          float mx = kNegInf;
+        for (int r = 0; r < 16; ++r) {
+          const float p = fast_exp2(__builtin_fmaf(sacc[kb][r], scale_log2, -l2q));
+          pf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
+        }
+      // dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
+      // The K^T fragments are read only now (the score registers are free after dS): slab by
+      // slab, each slab's products issued as soon as its reads have returned while the reads of
+      // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
+      uint32_t a0[4], a1[4];
+      taddr(kt, a0, a1);
+      tr_slab<0>(a0, a1, tf);
+      tr_slab<1>(a0, a1, tf);
+      slab_wait<8>(tf[0]);
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+      for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], pf[0], acc[db]);
+      tr_slab<2>(a0, a1, tf);
+      slab_wait<8>(tf[1]);
 #pragma unroll
-            for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, sacc[kb][r]), sacc[kb][r + 1]);
-          mx = max_xhalf(mx);
-          const float mt = mx * scale_log2;  // scale_log2 > 0: the max of the scaled scores
-          const bool up = mt > m + kRescaleLog2;  // false while mt = -inf (all keys hidden)
-          if (__builtin_amdgcn_ballot_w64(up) != 0) {
-            const float alpha = up ? fast_exp2(m - mt) : 1.f;  // m = -inf: alpha = 0 (O, l are 0)
-            m = up ? mt : m;
-            l *= alpha;
+      for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], pf[1], acc[db]);
+      tr_slab<3>(a0, a1, tf);
+      slab_wait<8>(tf[2]);
 #pragma unroll
-            for (int db = 0; db < kDB; ++db)
+      for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], pf[2], acc[db]);
+      slab_wait<0>(tf[3]);
 #pragma unroll
-              for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
-          }
-          // m = -inf only while every key seen by this row is masked; then p = exp2(-inf) = 0.
-          const float nb = (m == kNegInf) ? 0.f : -m;
+      for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], pf[3], acc[db]);
+    }
+    // This wave's copies of tile t+1 landed; after the barrier nobody reads `cur`, which takes t+2.
+    vm_wait0();
+    lgkm_wait0();
+    asm volatile("s_barrier" ::: "memory");
+  };
+  // Forward tile t from stage cur, the copies of tile t+1 into stage nxt. S^T = K Q^T is formed per
+  // 32-key half: chain 0 (keys kv0 .. +31) carries the copies, and half 0's probabilities are formed
+  // while chain 1's products run, half 1's while half 0's O^T products run, so the exps sit in MFMA
+  // shadows instead of between the two products. Half 0 is formed against the running maximum m
+  // before the tile's maximum is known; the one wave-uniform check after chain 1 raises m (and
+  // recomputes half 0) in the rare tile whose maximum exceeds m by kRescaleLog2, exactly as the
+  // single-pass online softmax would.
+  auto fwd_body = [&](int t, const char* cur, char* nxt) __attribute__((always_inline)) {
+    const int kv0 = kv_begin + t * kKT;
+    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
+    const char* kt = cur;
+    const char* vt = cur + kTile;
+    int kb_ = kbase, t0_ = tbase0, t1_ = tbase1;
+    asm volatile("" : "+v"(kb_), "+v"(t0_), "+v"(t1_));
+    const uint32_t vb = lds_addr(vt);
+    uint32_t a0[4], a1[4];
 #pragma unroll
-          for (int kb = 0; kb < 2; ++kb)
+    for (int db = 0; db < kDB; ++db) {
+      a0[db] = vb + (uint32_t)(t0_ ^ (db << 6));
+      a1[db] = vb + (uint32_t)(t1_ ^ (db << 6));
+    }
+    f32x16 s0, s1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s0[r] = 0.f;
+      s1[r] = 0.f;
+    }
+    // Step i of the 16 products: chain i / 8, k16 step i % 8; row fragments two steps ahead.
+    constexpr int RA = 2;
+    bf16x8 rk[RA + 1];
+    auto rd = [&](int i) {
+      rk[i % (RA + 1)] = as_bf16x8(lds_read16(kt, 32 * (i >> 3) * kRowB + (kb_ ^ ((i & 7) << 5))));
+    };
+    rd(0);
+    rd(1);
+#pragma unroll
+    for (int i = 0; i < kDK; ++i) {
+      rd(i + RA);
+      s0 = mfma32(rk[i % (RA + 1)], qf[i], s0);
+      if (i < 2 * kLd) issue_one(t + 1, nxt, i);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // Chain 0 runs for every wave, as it carries the copies; the rest only for a wave with keys of
+    // this tile to attend to (the others meet them at the barrier either way).
+    if (!skip) {
+      // Key kv0 + 4 hf + c (c = 32 kb + 8 (r >> 2) + (r & 3)) is visible to this lane's query iff
+      // c <= thr (causal and tail bounds) and, packed, c >= lo (at or after the row's segment
+      // start). Only tiles that cross the wave's diagonal, the sequence end or (packed) a segment
+      // start are masked (scores of hidden keys set to -inf, so their probabilities are 0); the
+      // test is per wave, a scalar branch before each half's softmax.
+      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
+      const int thr = qvalid ? ((causal && qi < S - 1 ? qi : S - 1) - kv0 - 4 * hf) : -1;
+      const int lo = my_sst - kv0 - 4 * hf;
+      {
+        auto mask = [&](f32x16& sc, int kb) {
+          if (need_mask) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const float p = fast_exp2(__builtin_fmaf(sacc[kb][r], scale_log2, nb));
-              l += p;
-              pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
+              const int c = 32 * kb + 8 * (r >> 2) + (r & 3);
+              bool ok = c <= thr;
+              if (PACKED) ok = ok && (c >= lo);
+              sc[r] = ok ? sc[r] : kNegInf;
             }
+          }
+        };
+        // Probability r of half kb against the row bias nb into pf[2 kb + r / 8]; returns it.
+        bf16x8 pf[4];
+        auto prob = [&](const f32x16& sc, int kb, int r, float nb) {
+          const float p = fast_exp2(__builtin_fmaf(sc[r], scale_log2, nb));
+          pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
+          return p;
+        };
+        // m = -inf only while every key seen by this row is masked; then p = exp2(-inf) = 0.
+        float nb = (m == kNegInf) ? 0.f : -m;
+        mask(s0, 0);
+        // Chain 1, each product followed by two of half 0's probabilities (written in this order:
+        // the scheduler does not move them across the wave exchange below).
+        float l0 = 0.f;
+#pragma unroll
+        for (int i = kDK; i < 2 * kDK; ++i) {
+          if (i + RA < 2 * kDK) rd(i + RA);
+          s1 = mfma32(rk[i % (RA + 1)], qf[i - kDK], s1);
+          l0 += prob(s0, 0, 2 * (i - kDK), nb);
+          l0 += prob(s0, 0, 2 * (i - kDK) + 1, nb);
         }
-      }
-      // O^T += V^T P^T (forward) or dQ^T += K^T dS^T: contraction over the 64 keys in 16-key slabs.
-      if constexpr (DQ) {
-        // The K^T fragments are read only now (the score registers are free after dS): slab by
-        // slab, each slab's products issued as soon as its reads have returned while the reads of
-        // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
-        uint32_t a0[4], a1[4];
-        taddr(kt, a0, a1);
+        // Half 0's speculative values are needed here, not only past the branches below (the mask
+        // of half 1, the rescale that may replace them): otherwise the compiler sinks them out of
+        // chain 1's shadows.
+        asm volatile("" ::"v"(l0), "v"(pf[0]), "v"(pf[1]));
+        // Transposed fragments of V (the O^T products' operand) for half 0, after chain 1's row
+        // fragments; half 1's go out once these have returned.
+        bf16x8 tf[4][4];
         tr_slab<0>(a0, a1, tf);
         tr_slab<1>(a0, a1, tf);
-        slab_wait<8>(tf[0]);
+        mask(s1, 1);
+        float mx = kNegInf;
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], pf[0], acc[db]);
+        for (int r = 0; r < 16; r += 2) mx = fmaxf(fmaxf(mx, s0[r]), fmaxf(s1[r], fmaxf(s0[r + 1], s1[r + 1])));
+        const float mt = max_xhalf(mx) * scale_log2;  // scale_log2 > 0: the max of the scaled scores
+        // A row raises m only when the tile maximum exceeds it by more than kRescaleLog2: its O and
+        // l are then rescaled together and half 0 recomputed; otherwise probabilities up to
+        // 2^kRescaleLog2 accumulate against the old m. O / l and L = m + log2(l) are the same
+        // either way. The branch is taken by the whole wave when any row needs it (most tiles
+        // skip it), but each row decides for itself and the others keep their values bitwise (alpha
+        // 1, half 0 recomputed identically): a row's arithmetic depends only on its own scores, so
+        // rows of other packed segments sharing the wave come out bitwise the same whatever this
+        // row's keys hold.
+        const bool up = mt > m + kRescaleLog2;  // false while mt = -inf (all keys hidden)
+        if (__builtin_amdgcn_ballot_w64(up) != 0) {
+          const float alpha = up ? fast_exp2(m - mt) : 1.f;  // m = -inf: alpha = 0 (O, l are 0)
+          m = up ? mt : m;
+          l *= alpha;
+#pragma unroll
+          for (int db = 0; db < kDB; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[db][r] *= alpha;
+          nb = (m == kNegInf) ? 0.f : -m;
+          l0 = 0.f;
+#pragma unroll
+          for (int r = 0; r < 16; ++r) l0 += prob(s0, 0, r, nb);
+        }
+        l += l0;
+        // O^T += V^T P^T: half 0's two 16-key slabs, each product followed by two of half 1's
+        // probabilities, then half 1's slabs.
+        slab_wait<0>(tf[0]);
+        slab_wait<0>(tf[1]);
         tr_slab<2>(a0, a1, tf);
-        slab_wait<8>(tf[1]);
-#pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], pf[1], acc[db]);
         tr_slab<3>(a0, a1, tf);
-        slab_wait<8>(tf[2]);
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], pf[2], acc[db]);
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int db = 0; db < kDB; ++db) {
+            acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
+            const int r = 2 * (kDB * ks + db);
+            l += prob(s1, 1, r, nb);
+            l += prob(s1, 1, r + 1, nb);
+          }
+        slab_wait<0>(tf[2]);
         slab_wait<0>(tf[3]);
 #pragma unroll
-        for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], pf[3], acc[db]);
-      } else {
-        tr_wait(tf);
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks)
+        for (int ks = 2; ks < 4; ++ks)
 #pragma unroll
           for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
       }
@@ -1507,8 +1600,13 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     asm volatile("s_barrier" ::: "memory");
   };
   for (int t = 0; t < ntiles; t += 2) {
-    body(t, lds0, lds1);
-    if (t + 1 < ntiles) body(t + 1, lds1, lds0);
+    if constexpr (DQ) {
+      body(t, lds0, lds1);
+      if (t + 1 < ntiles) body(t + 1, lds1, lds0);
+    } else {
+      fwd_body(t, lds0, lds1);
+      if (t + 1 < ntiles) fwd_body(t + 1, lds1, lds0);
+    }
   }
 
   float mul = scale, lt = 0.f;
