@@ -8,20 +8,22 @@
 // Packed mode: key j is visible to query i iff seg_id[i] == seg_id[j] and j <= i
 // (attention/segments.py:22-29); seg_start (non-decreasing, gapless layout) only bounds loops.
 //
-// Kernel structure (all MFMA 32x32x16 bf16, fp32 accumulate, 4 waves per workgroup):
-//   attn_fwd:     a wave owns 32 queries of one head; a workgroup holds up to 4 heads of one GQA
-//                 group so every K/V tile staged in LDS feeds 128 query rows. Scores are computed
-//                 transposed (keys x queries) so each lane owns one query column: the online
-//                 softmax is lane-local plus one exchange with lane^32, and the probability tile
-//                 feeds the P.V MFMA directly from registers.
-//   attn_bwd_dq:  same ownership as the forward; recomputes S^T and dP^T per key tile and
-//                 accumulates dQ^T in registers (rows are owned, no atomics).
-//   attn_bwd_dkv: a wave owns 32 keys of one kv head; the workgroup sweeps every query tile of
-//                 every head in the group and accumulates dK^T, dV^T in registers (no atomics).
-// Operand tiles in LDS: "natural" tiles keep 64 rows x head_dim with a 16-byte row pad;
-// "transposed" tiles keep head_dim rows x 64 positions in the 128-byte swizzled layout, with the
-// middle two 4-position quads of every 16-position group swapped so that one 16-byte read yields
-// the MFMA contraction slots that match the accumulator layout of the preceding product.
+// Kernel structure (all MFMA 32x32x16 bf16, fp32 accumulate):
+//   attn_kv_kernel<DH, PACKED, DQ> (forward, and the dQ pass, which also forms D): a wave owns 32
+//                 queries of one head; a workgroup holds up to 4 heads of one GQA group so every
+//                 K/V tile staged in LDS (copied global -> LDS, two stages) feeds 128 query rows.
+//                 Scores are computed transposed (keys x queries) so each lane owns one query
+//                 column: the online softmax is lane-local plus one exchange with lane^32, and the
+//                 probability (or dS) tile feeds the next product directly from registers.
+//   attn_bwd_dkv128_ab_kernel (head_dim 128): 8 waves per 128-key block, operand-split P waves
+//                 and dS waves (below).
+//   attn_bwd_dkv_kernel (head_dim 64, 96): a wave owns 32 keys of one kv head; the workgroup
+//                 sweeps every query tile of every head in the group and accumulates dK^T, dV^T in
+//                 registers (no atomics). Its tiles are register-staged: "natural" tiles keep
+//                 64 rows x head_dim with a 16-byte row pad; "transposed" tiles keep head_dim rows
+//                 x 64 positions in the 128-byte swizzled layout, with the middle two 4-position
+//                 quads of every 16-position group swapped so that one 16-byte read yields the
+//                 MFMA contraction slots that match the accumulator layout of the preceding product.
 #include <type_traits>
 
 #include "mtp_common.hpp"
@@ -61,11 +63,18 @@ __device__ __forceinline__ u32x2 tr16_asm(uint32_t a) {
 __device__ __forceinline__ bf16x8 tr_pair(u32x2 lo, u32x2 hi) {
   return __builtin_bit_cast(bf16x8, u32x4{lo[0], lo[1], hi[0], hi[1]});
 }
-// Waits until at most N LDS reads are outstanding and marks one slab's 4 fragments as produced here.
-template <int N>
+// Waits until at most N LDS reads are outstanding and marks one slab's NDB fragments as produced here.
+template <int N, int NDB = 4>
 __device__ __forceinline__ void slab_wait(bf16x8 (&f)[4]) {
   static_assert(N >= 0 && N <= 15, "lgkmcnt is a 4-bit field");
-  asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) : "n"(N));
+  if constexpr (NDB == 4) {
+    asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]), "+v"(f[3]) : "n"(N));
+  } else if constexpr (NDB == 3) {
+    asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(f[0]), "+v"(f[1]), "+v"(f[2]) : "n"(N));
+  } else {
+    static_assert(NDB == 2, "head_dim 64, 96 or 128");
+    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(f[0]), "+v"(f[1]) : "n"(N));
+  }
 }
 // max(x of lane l, x of lane l ^ 32): the two lane halves hold the two key halves of one query
 // column. v_permlane32_swap exchanges the upper half of one register with the lower half of the
@@ -96,16 +105,15 @@ __device__ __forceinline__ void lds_copy4(const float* src, int bytes, char* dst
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4, voff, 0, 0, 0);
 }
 
-// Transposed fragments f[KS][db] of slab KS (rows 16 KS.. of a swizzled 256-byte-row tile): head_dim
-// block db (32 columns) in the MFMA accumulator-row order (4 hf + 0..3, 4 hf + 8..11), from the
-// LDS addresses a0/a1[db] of reads 0 and 1 (16-row slab 0). Asm reads: slab_wait before use.
-template <int KS>
+// Transposed fragments f[KS][db] of slab KS (rows 16 KS.. of a swizzled tile of ROWB-byte rows):
+// head_dim block db < NDB (32 columns) in the MFMA accumulator-row order (4 hf + 0..3,
+// 4 hf + 8..11), from the LDS addresses a0/a1[db] of reads 0 and 1 (16-row slab 0). Asm reads:
+// slab_wait before use.
+template <int KS, int NDB = 4, int ROWB = 256>
 __device__ __forceinline__ void tr_slab(const uint32_t (&a0)[4], const uint32_t (&a1)[4], bf16x8 (&f)[4][4]) {
-  constexpr int off = KS * 16 * 256;
-  f[KS][0] = tr_pair(tr16_asm<off>(a0[0]), tr16_asm<off>(a1[0]));
-  f[KS][1] = tr_pair(tr16_asm<off>(a0[1]), tr16_asm<off>(a1[1]));
-  f[KS][2] = tr_pair(tr16_asm<off>(a0[2]), tr16_asm<off>(a1[2]));
-  f[KS][3] = tr_pair(tr16_asm<off>(a0[3]), tr16_asm<off>(a1[3]));
+  constexpr int off = KS * 16 * ROWB;
+#pragma unroll
+  for (int db = 0; db < NDB; ++db) f[KS][db] = tr_pair(tr16_asm<off>(a0[db]), tr16_asm<off>(a1[db]));
 }
 // Waits for every LDS read issued so far and marks the 16 fragments as produced here.
 __device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
@@ -187,368 +195,6 @@ __device__ __forceinline__ bf16x8 t_frag(const char* tile, int row, int ks, int 
 }
 
 __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1); }
-
-// ------------------------------------------------------------------------------------------
-// Forward
-// ------------------------------------------------------------------------------------------
-template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_fwd_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                     const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
-                     bf16_t* __restrict__ o, float* __restrict__ lse, int B, int Hq, int Hkv, int S,
-                     float scale_log2, int causal) {
-  using C = AttnCfg<DH>;
-  constexpr int kStage = C::kNatBytes + C::kTBytes + 256;
-  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
-
-  const int G = Hq / Hkv;
-  const int hpw = heads_per_wg(G);
-  const int P = 32 * (4 / hpw);
-  const int npb = (S + P - 1) / P;
-  const int hgb = Hq / hpw;  // head groups per batch entry
-  const int nhg = B * hgb;
-  const int g = blockIdx.x;
-  const int hg = g % nhg;
-  const int pb = npb - 1 - g / nhg;  // heaviest (latest) query blocks first
-  const int bidx = hg / hgb;
-  const int h0 = (hg % hgb) * hpw;
-  const int kvh = h0 / G;
-
-  const int tid = threadIdx.x;
-  // The wave index is read as a scalar so that every per-wave bound below (and the decisions built
-  // on them) is a scalar branch, not a per-lane select.
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hf = lane >> 5, col = lane & 31;
-  const int head = h0 + (w % hpw);
-  const int qw0 = pb * P + 32 * (w / hpw);
-  const int qi = qw0 + col;
-  const bool qvalid = qi < S;
-  const bool wave_has = qw0 < S;
-  const int wq_last = wave_has ? ((qw0 + 31 < S) ? qw0 + 31 : S - 1) : 0;
-
-  const bf16_t* qh = q + (long)(bidx * Hq + head) * S * DH;
-  const bf16_t* kh = k + (long)(bidx * Hkv + kvh) * S * DH;
-  const bf16_t* vh = v + (long)(bidx * Hkv + kvh) * S * DH;
-  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
-  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
-
-  bf16x8 qf[C::kDK];
-#pragma unroll
-  for (int ks = 0; ks < C::kDK; ++ks)
-    qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(qh + (long)qi * DH + 16 * ks + 8 * hf))
-                    : as_bf16x8(zero4());
-
-  const int wg_q0 = pb * P;
-  const int wg_q1 = (causal && wg_q0 + P < S) ? wg_q0 + P : S;  // non-causal: every key
-  int kv_begin = 0;
-  if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
-  const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
-
-  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
-  if (PACKED) {
-    my_seg = qvalid ? sid[qi] : -2;
-    w_sst_first = __builtin_amdgcn_readfirstlane(wave_has ? sst[qw0] : 0);
-    w_sst_last = __builtin_amdgcn_readfirstlane(wave_has ? sst[wq_last] : 0);
-  }
-
-  float m = kNegInf, l = 0.f;
-  f32x16 oacc[C::kDB];
-#pragma unroll
-  for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) oacc[db][r] = 0.f;
-
-  const bool isV = tid >= 128;
-  BlockLoad<DH> bl;
-  bl.init(isV ? tid - 128 : tid);
-  int seg_reg = 0;
-
-  auto load_tile = [&](int t) {
-    const int kv0 = kv_begin + t * kKT;
-    bl.load((isV ? vh : kh) + (long)kv0 * DH, S - kv0);
-    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
-  };
-  auto store_tile = [&](char* st) {
-    if (isV) bl.store_t(st + C::kNatBytes);
-    else bl.store_nat(st);
-    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + C::kNatBytes + C::kTBytes)[tid] = seg_reg;
-  };
-
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(lds);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const char* cur = lds + (t & 1) * kStage;
-    const int kv0 = kv_begin + t * kKT;
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1);
-    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
-    if (!skip) {
-      f32x16 sacc[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) sacc[kb][r] = 0.f;
-#pragma unroll
-        for (int ks = 0; ks < C::kDK; ++ks) sacc[kb] = mfma32(nat_frag<DH>(cur, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
-      }
-      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
-      const int* segs = reinterpret_cast<const int*>(cur + C::kNatBytes + C::kTBytes);
-      float mt = kNegInf;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float x = sacc[kb][r] * scale_log2;
-          if (need_mask) {
-            const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const int j = kv0 + jl;
-            bool ok = (!causal || j <= qi) && (j < S) && qvalid;
-            if (PACKED) ok = ok && (segs[jl] == my_seg);
-            if (!ok) x = kNegInf;
-          }
-          sacc[kb][r] = x;
-          mt = fmaxf(mt, x);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float mn = fmaxf(m, mt);
-      const float base = (mn == kNegInf) ? 0.f : mn;
-      const float alpha = fast_exp2(m - base);
-      m = mn;
-      l *= alpha;
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) oacc[db][r] *= alpha;
-      bf16x8 pf[4];
-      float ls = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = fast_exp2(sacc[kb][r] - base);
-          ls += p;
-          pf[2 * kb + (r >> 3)][r & 7] = (__bf16)p;
-        }
-      l += ls;
-      const char* vt = cur + C::kNatBytes;
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) oacc[db] = mfma32(t_frag(vt, 32 * db + col, ks, hf), pf[ks], oacc[db]);
-    }
-    if (more) store_tile(lds + ((t + 1) & 1) * kStage);
-    __syncthreads();
-  }
-
-  const float lt = l + __shfl_xor(l, 32, 64);
-  const float inv = (lt > 0.f) ? 1.f / lt : 0.f;
-  if (qvalid) {
-    bf16_t* oh = o + ((long)(bidx * Hq + head) * S + qi) * DH;
-#pragma unroll
-    for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        const u32x2 pk{pack_bf16x2(oacc[db][4 * rq] * inv, oacc[db][4 * rq + 1] * inv),
-                       pack_bf16x2(oacc[db][4 * rq + 2] * inv, oacc[db][4 * rq + 3] * inv)};
-        *reinterpret_cast<u32x2*>(oh + d) = pk;
-      }
-    if (hf == 0) lse[(long)(bidx * Hq + head) * S + qi] = (m + fast_log2(lt)) * kLn2;
-  }
-}
-
-// ------------------------------------------------------------------------------------------
-// Backward pre-pass for head_dim 64 and 96: D[row] = sum_d dO[row][d] * O[row][d] (fp32), 8 lanes
-// per row. For head_dim 128 the dQ pass (attn_kv128_kernel<., true>) forms D itself.
-// ------------------------------------------------------------------------------------------
-template <int DH>
-__global__ __launch_bounds__(256) void attn_bwd_dvec_kernel(const bf16_t* __restrict__ o, const bf16_t* __restrict__ d_o,
-                                                            float* __restrict__ dvec, long rows) {
-  const long row = (long)blockIdx.x * 32 + (threadIdx.x >> 3);
-  const int sub = threadIdx.x & 7;
-  float acc = 0.f;
-  if (row < rows) {
-    for (int c = sub; c < DH / 8; c += 8) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(o + row * DH + 8 * c);
-      const u32x4 b = *reinterpret_cast<const u32x4*>(d_o + row * DH + 8 * c);
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        acc = __builtin_fmaf(bf16lo(a[p]), bf16lo(b[p]), acc);
-        acc = __builtin_fmaf(bf16hi(a[p]), bf16hi(b[p]), acc);
-      }
-    }
-  }
-  acc += __shfl_xor(acc, 4, 64);
-  acc += __shfl_xor(acc, 2, 64);
-  acc += __shfl_xor(acc, 1, 64);
-  if (row < rows && sub == 0) dvec[row] = acc;
-}
-
-// ------------------------------------------------------------------------------------------
-// Backward dQ (query-row owners; no atomics).
-// ------------------------------------------------------------------------------------------
-template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_bwd_dq_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                        const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
-                        const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
-                        bf16_t* __restrict__ dq, int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
-  using C = AttnCfg<DH>;
-  constexpr int kStage = 2 * C::kNatBytes + C::kTBytes + 256;  // K, V natural; K^T; key segment ids
-  __shared__ __attribute__((aligned(16))) char lds[kStage];
-
-  const int G = Hq / Hkv;
-  const int hpw = heads_per_wg(G);
-  const int P = 32 * (4 / hpw);
-  const int npb = (S + P - 1) / P;
-  const int hgb = Hq / hpw;
-  const int nhg = B * hgb;
-  const int g = blockIdx.x;
-  const int hg = g % nhg;
-  const int pb = npb - 1 - g / nhg;
-  const int bidx = hg / hgb;
-  const int h0 = (hg % hgb) * hpw;
-  const int kvh = h0 / G;
-
-  const int tid = threadIdx.x;
-  // The wave index is read as a scalar so that every per-wave bound below (and the decisions built
-  // on them) is a scalar branch, not a per-lane select.
-  const int lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int hf = lane >> 5, col = lane & 31;
-  const int head = h0 + (w % hpw);
-  const int qw0 = pb * P + 32 * (w / hpw);
-  const int qi = qw0 + col;
-  const bool qvalid = qi < S;
-  const bool wave_has = qw0 < S;
-  const int wq_last = wave_has ? ((qw0 + 31 < S) ? qw0 + 31 : S - 1) : 0;
-
-  const long qrow = (long)(bidx * Hq + head) * S;
-  const bf16_t* qh = q + qrow * DH;
-  const bf16_t* doh = d_o + qrow * DH;
-  const bf16_t* kh = k + (long)(bidx * Hkv + kvh) * S * DH;
-  const bf16_t* vh = v + (long)(bidx * Hkv + kvh) * S * DH;
-  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
-  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
-
-  bf16x8 qf[C::kDK], df[C::kDK];
-#pragma unroll
-  for (int ks = 0; ks < C::kDK; ++ks) {
-    qf[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(qh + (long)qi * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-    df[ks] = qvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(doh + (long)qi * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-  }
-  const float l2q = qvalid ? lse[qrow + qi] * kLog2e : 0.f;
-  const float dq_row = qvalid ? dvec[qrow + qi] : 0.f;
-
-  const int wg_q0 = pb * P;
-  const int wg_q1 = (causal && wg_q0 + P < S) ? wg_q0 + P : S;  // non-causal: every key
-  int kv_begin = 0;
-  if (PACKED) kv_begin = (sst[wg_q0] / kKT) * kKT;
-  const int ntiles = (wg_q1 - kv_begin + kKT - 1) / kKT;
-
-  int my_seg = 0, w_sst_first = 0, w_sst_last = 0;
-  if (PACKED) {
-    my_seg = qvalid ? sid[qi] : -2;
-    w_sst_first = __builtin_amdgcn_readfirstlane(wave_has ? sst[qw0] : 0);
-    w_sst_last = __builtin_amdgcn_readfirstlane(wave_has ? sst[wq_last] : 0);
-  }
-
-  f32x16 acc[C::kDB];
-#pragma unroll
-  for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
-
-  const bool isV = tid >= 128;
-  BlockLoad<DH> bl;
-  bl.init(isV ? tid - 128 : tid);
-  int seg_reg = 0;
-  auto load_tile = [&](int t) {
-    const int kv0 = kv_begin + t * kKT;
-    bl.load((isV ? vh : kh) + (long)kv0 * DH, S - kv0);
-    if (PACKED && tid < kKT) seg_reg = (kv0 + tid < S) ? sid[kv0 + tid] : -1;
-  };
-  auto store_tile = [&](char* st) {
-    if (isV) {
-      bl.store_nat(st + C::kNatBytes);
-    } else {
-      bl.store_nat(st);
-      bl.store_t(st + 2 * C::kNatBytes);
-    }
-    if (PACKED && tid < kKT) reinterpret_cast<int*>(st + 2 * C::kNatBytes + C::kTBytes)[tid] = seg_reg;
-  };
-
-  if (ntiles > 0) {
-    load_tile(0);
-    store_tile(lds);
-  }
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    const char* cur = lds;
-    const int kv0 = kv_begin + t * kKT;
-    const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1);
-    const bool skip = !wave_has || (causal && kv0 > wq_last) || (PACKED && kv0 + kKT - 1 < w_sst_first);
-    if (!skip) {
-      f32x16 sacc[2], pacc[2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[kb][r] = 0.f;
-          pacc[kb][r] = 0.f;
-        }
-#pragma unroll
-        for (int ks = 0; ks < C::kDK; ++ks) {
-          sacc[kb] = mfma32(nat_frag<DH>(cur, 32 * kb + col, ks, hf), qf[ks], sacc[kb]);
-          pacc[kb] = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * kb + col, ks, hf), df[ks], pacc[kb]);
-        }
-      }
-      const bool need_mask = (causal && kv0 + kKT - 1 > qw0) || (kv0 + kKT > S) || (PACKED && kv0 < w_sst_last);
-      const int* segs = reinterpret_cast<const int*>(cur + 2 * C::kNatBytes + C::kTBytes);
-      bf16x8 sf[4];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          float p = fast_exp2(sacc[kb][r] * scale_log2 - l2q);
-          if (need_mask) {
-            const int jl = 32 * kb + 8 * (r >> 2) + 4 * hf + (r & 3);
-            const int j = kv0 + jl;
-            bool ok = (!causal || j <= qi) && (j < S) && qvalid;
-            if (PACKED) ok = ok && (segs[jl] == my_seg);
-            if (!ok) p = 0.f;
-          }
-          sf[2 * kb + (r >> 3)][r & 7] = (__bf16)(p * (pacc[kb][r] - dq_row));
-        }
-      const char* kt = cur + 2 * C::kNatBytes;
-#pragma unroll
-      for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc[db] = mfma32(t_frag(kt, 32 * db + col, ks, hf), sf[ks], acc[db]);
-    }
-    __syncthreads();
-    if (more) {
-      store_tile(lds);
-      __syncthreads();
-    }
-  }
-
-  if (qvalid) {
-    bf16_t* out = dq + (qrow + qi) * DH;
-#pragma unroll
-    for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        const u32x2 pk{pack_bf16x2(acc[db][4 * rq] * scale, acc[db][4 * rq + 1] * scale),
-                       pack_bf16x2(acc[db][4 * rq + 2] * scale, acc[db][4 * rq + 3] * scale)};
-        *reinterpret_cast<u32x2*>(out + d) = pk;
-      }
-  }
-}
 
 // ------------------------------------------------------------------------------------------
 // Backward dK, dV (key-row owners, GQA group summed in registers; no atomics).
@@ -1167,47 +813,61 @@ __global__ __launch_bounds__(256) void attn_dkv_reduce_kernel(const float* __res
 }
 
 // ------------------------------------------------------------------------------------------
-// Forward and dQ for head_dim 128, DMA-fed. Same ownership and math as attn_fwd_kernel /
-// attn_bwd_dq_kernel. Each 64-key K and V tile is copied global -> LDS (rows past S read as
-// zeros) in the swizzled 256 B-row layout of the dK/dV kernel; S^T = K Q^T and dP^T = V dO^T read
-// row fragments, O^T += V^T P^T and dQ^T += K^T dS^T read transposed fragments of the same tiles.
-// Two LDS stages, one barrier per key tile.
+// Forward and dQ, DMA-fed, for head_dim 64, 96 and 128 (query-row owners; no atomics). Each 64-key K
+// and V tile is copied global -> LDS (rows past S read as zeros) in a swizzled row layout (kvdma
+// below); S^T = K Q^T and dP^T = V dO^T read row fragments, O^T += V^T P^T and dQ^T += K^T dS^T
+// read transposed fragments of the same tiles. Two LDS stages, one barrier per key tile.
 // ------------------------------------------------------------------------------------------
-namespace kv128 {
-constexpr int kRowB = 256;
-constexpr int kTile = kKT * kRowB;            // 16 KiB
-constexpr int kStage = 2 * kTile;             // K, V
-__device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+namespace kvdma {
+// LDS layout of a 64-position K/V tile for head_dim DH: rows of kRowB bytes, 16-byte chunk c of row r
+// at slot c ^ sw(r). head_dim 64 packs a row into 128 B; 96 and 128 use 256 B rows (96 leaves chunks
+// 12-15 empty: their copies read nothing and write zeros). Both swizzles keep every row-fragment
+// read (ds_read_b128, 16 rows at one chunk per 16 lanes) and every transposed read
+// (ds_read_b64_tr_b16, 4 rows x 2 chunks per 16 lanes) on distinct banks, and repeat every 16 rows.
+template <int DH>
+struct Lay {
+  static constexpr int kRowB = DH == 64 ? 128 : 256;
+  static constexpr int kChunks = kRowB / 16;
+  static constexpr int kTile = kKT * kRowB;
+  static constexpr int kStage = 2 * kTile;  // K, V
+  static __device__ __forceinline__ int sw(int r) {
+    if constexpr (DH == 64) return ((r & 2) << 1) | ((r >> 2) & 3);
+    else return ((r & 3) << 2) | ((r >> 2) & 3);
+  }
+};
 
 // Per-lane constants: row-fragment swizzle and the transposed-read offsets tro[t] of read t (0, 1)
 // of head_dim block 0 within a 16-row slab (block db adds db << 6 by XOR: 4 db only touches chunk
-// bits 2-3 of the swizzled 16-byte chunk index).
+// bits 2 and up of the swizzled 16-byte chunk index).
+template <int DH>
 struct Lanes {
   int sw_r;
   int tro[2];
   __device__ __forceinline__ void init() {
+    using L = Lay<DH>;
     const int lane = threadIdx.x & 63;
     const int hf = lane >> 5, col = lane & 31;
-    sw_r = sw(col & 15);
+    sw_r = L::sw(col & 15);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
       const int c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-      tro[t] = rl * kRowB + ((c0 ^ sw(rl)) << 4) + 8 * (lane & 1);
+      tro[t] = rl * L::kRowB + ((c0 ^ L::sw(rl)) << 4) + 8 * (lane & 1);
     }
   }
 };
-}  // namespace kv128
+}  // namespace kvdma
 
-template <bool PACKED, bool DQ>
+template <int DH, bool PACKED, bool DQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                       const bf16_t* __restrict__ d_o, const bf16_t* __restrict__ o_in, const float* __restrict__ lse_in,
-                       float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
-                       const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
-                       int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
-  using namespace kv128;
-  constexpr int DH = 128;
+void attn_kv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+                    const bf16_t* __restrict__ d_o, const bf16_t* __restrict__ o_in, const float* __restrict__ lse_in,
+                    float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
+                    const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
+                    int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
+  using L = kvdma::Lay<DH>;
+  constexpr int kRowB = L::kRowB, kTile = L::kTile, kStage = L::kStage;
+  auto sw = [](int r) { return L::sw(r); };
   constexpr int kDK = DH / 16, kDB = DH / 32;
   __shared__ __attribute__((aligned(1024))) char lds0[kStage];
   __shared__ __attribute__((aligned(1024))) char lds1[kStage];
@@ -1281,7 +941,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-  Lanes ln;
+  kvdma::Lanes<DH> ln;
   ln.init();
   // Row-fragment offset of rows 32 kb + col, k16 step ks: 32 kb kRowB + (kbase ^ (ks << 5)) (the
   // chunk index 2 ks + hf is XOR-swizzled with the row's pattern and 2 ks touches chunk bits 1-3
@@ -1290,26 +950,34 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
   // instead of 32 offsets per lane (two stages) being held in registers across the loop.
   const int kbase = col * kRowB + ((hf ^ ln.sw_r) << 4);
   const int tbase0 = ln.tro[0], tbase1 = ln.tro[1];
-  // Copies of tile t into stage st: this wave's load j (0-3 K rows, 4-7 V rows); each wave copies
-  // kLd 1 KiB pieces of each 16 KiB tile, rows 4 (NW jj + w) .. +3 of piece jj. The copies of the
-  // next tile are issued during the current one, one per k16 step of its first product: a copy
-  // load holds its wave at issue while the CU's load path (~64 B/clk) serves the other waves'
-  // copies, and issued between products that wait overlaps MFMA work. Past the last tile the loads
-  // get an empty buffer range (no memory access; zeros into a stage nobody reads), so no branch
-  // splits the product loop.
-  constexpr int kLd = 16 / NW;
+  // Copies of tile t into stage st: this wave's load j (0 .. kLd-1 K rows, kLd .. 2 kLd-1 V rows);
+  // each wave copies kLd 1 KiB pieces of each tile, piece NW jj + w holding rows kRpp (NW jj + w)
+  // .. + kRpp - 1. A lane's source is the logical chunk its LDS slot holds (chunks past head_dim
+  // point beyond the buffer and read zeros). The copies of the next tile are issued during the
+  // current one, spread over the k16 steps of its first product: a copy load holds its wave at
+  // issue while the CU's load path (~64 B/clk) serves the other waves' copies, and issued between
+  // products that wait overlaps MFMA work. Past the last tile the loads get an empty buffer range
+  // (no memory access; zeros into a stage nobody reads), so no branch splits the product loop.
+  constexpr int kLd = kTile / 1024 / NW;
+  constexpr int kLpr = L::kChunks, kRpp = 64 / kLpr;  // lanes per LDS row, rows per 1 KiB piece
   uint32_t coff[kLd];
 #pragma unroll
   for (int jj = 0; jj < kLd; ++jj) {
-    const int row = 4 * (NW * jj + w) + (lane >> 4);
-    coff[jj] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+    const int row = kRpp * (NW * jj + w) + lane / kLpr;
+    const int c = (lane % kLpr) ^ sw(row);
+    coff[jj] = 16 * c < 2 * DH ? (uint32_t)(row * 2 * DH + 16 * c) : 0x7ffffff0u;
   }
   auto issue_one = [&](int t, char* st, int j) __attribute__((always_inline)) {
     const bool ok = t < ntiles;
     const int kv0 = kv_begin + t * kKT;
     const int jj = j % kLd;
-    lds_copy16((j < kLd ? kh : vh) + (ok ? (long)kv0 * DH : 0), ok ? (S - kv0) * kRowB : 0,
+    lds_copy16((j < kLd ? kh : vh) + (ok ? (long)kv0 * DH : 0), ok ? (S - kv0) * 2 * DH : 0,
                st + (j < kLd ? 0 : kTile) + 1024 * (NW * jj + w), coff[jj]);
+  };
+  // Copies j of tile t+1 issued in k16 step i of the first product: an even share of the 2 kLd.
+  auto issue_step = [&](int t, char* nxt, int i) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = (2 * kLd) * i / kDK; j < (2 * kLd) * (i + 1) / kDK; ++j) issue_one(t + 1, nxt, j);
   };
 
 #pragma unroll
@@ -1381,7 +1049,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         sacc[kb] = mfma32(rk[ks % (RA + 1)][kb], qf[ks], sacc[kb]);
         pacc[kb] = mfma32(rv[ks % (RA + 1)][kb], df[ks], pacc[kb]);
       }
-      if (ks < 2 * kLd) issue_one(t + 1, nxt, ks);
+      issue_step(t, nxt, ks);
       // Keep each k16 step's reads, products and copy load together (the scheduler would
       // otherwise bunch the copies and hoist the transposed reads into this loop).
       __builtin_amdgcn_sched_barrier(0);
@@ -1427,20 +1095,20 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
       // the slab after next are in flight (lgkmcnt counts LDS reads in issue order).
       uint32_t a0[4], a1[4];
       taddr(kt, a0, a1);
-      tr_slab<0>(a0, a1, tf);
-      tr_slab<1>(a0, a1, tf);
-      slab_wait<8>(tf[0]);
+      tr_slab<0, kDB, kRowB>(a0, a1, tf);
+      tr_slab<1, kDB, kRowB>(a0, a1, tf);
+      slab_wait<2 * kDB, kDB>(tf[0]);
 #pragma unroll
       for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], pf[0], acc[db]);
-      tr_slab<2>(a0, a1, tf);
-      slab_wait<8>(tf[1]);
+      tr_slab<2, kDB, kRowB>(a0, a1, tf);
+      slab_wait<2 * kDB, kDB>(tf[1]);
 #pragma unroll
       for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], pf[1], acc[db]);
-      tr_slab<3>(a0, a1, tf);
-      slab_wait<8>(tf[2]);
+      tr_slab<3, kDB, kRowB>(a0, a1, tf);
+      slab_wait<2 * kDB, kDB>(tf[2]);
 #pragma unroll
       for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], pf[2], acc[db]);
-      slab_wait<0>(tf[3]);
+      slab_wait<0, kDB>(tf[3]);
 #pragma unroll
       for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], pf[3], acc[db]);
     }
@@ -1476,11 +1144,11 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
       s0[r] = 0.f;
       s1[r] = 0.f;
     }
-    // Step i of the 16 products: chain i / 8, k16 step i % 8; row fragments two steps ahead.
+    // Step i of the 2 kDK products: chain i / kDK, k16 step i % kDK; row fragments two steps ahead.
     constexpr int RA = 2;
     bf16x8 rk[RA + 1];
     auto rd = [&](int i) {
-      rk[i % (RA + 1)] = as_bf16x8(lds_read16(kt, 32 * (i >> 3) * kRowB + (kb_ ^ ((i & 7) << 5))));
+      rk[i % (RA + 1)] = as_bf16x8(lds_read16(kt, 32 * (i / kDK) * kRowB + (kb_ ^ ((i % kDK) << 5))));
     };
     rd(0);
     rd(1);
@@ -1488,7 +1156,7 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
     for (int i = 0; i < kDK; ++i) {
       rd(i + RA);
       s0 = mfma32(rk[i % (RA + 1)], qf[i], s0);
-      if (i < 2 * kLd) issue_one(t + 1, nxt, i);
+      issue_step(t, nxt, i);
       __builtin_amdgcn_sched_barrier(0);
     }
     // Chain 0 runs for every wave, as it carries the copies; the rest only for a wave with keys of
@@ -1524,15 +1192,15 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         // m = -inf only while every key seen by this row is masked; then p = exp2(-inf) = 0.
         float nb = (m == kNegInf) ? 0.f : -m;
         mask(s0, 0);
-        // Chain 1, each product followed by two of half 0's probabilities (written in this order:
-        // the scheduler does not move them across the wave exchange below).
+        // Chain 1, each product followed by an even share of half 0's 16 probabilities (written in
+        // this order: the scheduler does not move them across the wave exchange below).
         float l0 = 0.f;
 #pragma unroll
         for (int i = kDK; i < 2 * kDK; ++i) {
           if (i + RA < 2 * kDK) rd(i + RA);
           s1 = mfma32(rk[i % (RA + 1)], qf[i - kDK], s1);
-          l0 += prob(s0, 0, 2 * (i - kDK), nb);
-          l0 += prob(s0, 0, 2 * (i - kDK) + 1, nb);
+#pragma unroll
+          for (int r = 16 * (i - kDK) / kDK; r < 16 * (i - kDK + 1) / kDK; ++r) l0 += prob(s0, 0, r, nb);
         }
         // Half 0's speculative values are needed here, not only past the branches below (the mask
         // of half 1, the rescale that may replace them): otherwise the compiler sinks them out of
@@ -1541,8 +1209,8 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
         // Transposed fragments of V (the O^T products' operand) for half 0, after chain 1's row
         // fragments; half 1's go out once these have returned.
         bf16x8 tf[4][4];
-        tr_slab<0>(a0, a1, tf);
-        tr_slab<1>(a0, a1, tf);
+        tr_slab<0, kDB, kRowB>(a0, a1, tf);
+        tr_slab<1, kDB, kRowB>(a0, a1, tf);
         mask(s1, 1);
         float mx = kNegInf;
 #pragma unroll
@@ -1571,23 +1239,23 @@ void attn_kv128_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ 
           for (int r = 0; r < 16; ++r) l0 += prob(s0, 0, r, nb);
         }
         l += l0;
-        // O^T += V^T P^T: half 0's two 16-key slabs, each product followed by two of half 1's
-        // probabilities, then half 1's slabs.
-        slab_wait<0>(tf[0]);
-        slab_wait<0>(tf[1]);
-        tr_slab<2>(a0, a1, tf);
-        tr_slab<3>(a0, a1, tf);
+        // O^T += V^T P^T: half 0's two 16-key slabs, each product followed by an even share of half
+        // 1's probabilities, then half 1's slabs.
+        slab_wait<0, kDB>(tf[0]);
+        slab_wait<0, kDB>(tf[1]);
+        tr_slab<2, kDB, kRowB>(a0, a1, tf);
+        tr_slab<3, kDB, kRowB>(a0, a1, tf);
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
           for (int db = 0; db < kDB; ++db) {
             acc[db] = mfma32(tf[ks][db], pf[ks], acc[db]);
-            const int r = 2 * (kDB * ks + db);
-            l += prob(s1, 1, r, nb);
-            l += prob(s1, 1, r + 1, nb);
+            const int u = kDB * ks + db;
+#pragma unroll
+            for (int r = 8 * u / kDB; r < 8 * (u + 1) / kDB; ++r) l += prob(s1, 1, r, nb);
           }
-        slab_wait<0>(tf[2]);
-        slab_wait<0>(tf[3]);
+        slab_wait<0, kDB>(tf[2]);
+        slab_wait<0, kDB>(tf[3]);
 #pragma unroll
         for (int ks = 2; ks < 4; ++ks)
 #pragma unroll
@@ -1680,13 +1348,8 @@ hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
                   const int32_t* sst, bf16_t* o, float* lse, hipStream_t st) {
   const float sl2 = sh.scale * kLog2e;
   dim3 grid(fwd_grid(sh)), block(256);
-  if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-    return hipGetLastError();
-  }
-  if (sid) hipLaunchKernelGGL((attn_fwd_kernel<DH, true>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.causal);
-  else hipLaunchKernelGGL((attn_fwd_kernel<DH, false>), grid, block, 0, st, q, k, v, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.causal);
+  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
   return hipGetLastError();
 }
 
@@ -1694,24 +1357,13 @@ template <int DH>
 hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const bf16_t* v, const bf16_t* o,
                   const float* lse, const bf16_t* d_o, const int32_t* sid, const int32_t* sst, bf16_t* dq,
                   bf16_t* dk, bf16_t* dv, float* dvec, hipStream_t st) {
-  const long rows = (long)sh.b * sh.hq * sh.s;
   dim3 block(256);
   hipError_t e = hipSuccess;
-  // head_dim 128: the dQ pass forms D itself (and writes it for dK/dV).
-  if constexpr (DH != 128) {
-    hipLaunchKernelGGL(attn_bwd_dvec_kernel<DH>, dim3((unsigned)((rows + 31) / 32)), block, 0, st, o, d_o, dvec, rows);
-    e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
+  // The dQ pass forms D = rowsum(dO o O) itself and writes it for the dK/dV pass.
   const float sl2 = sh.scale * kLog2e;
   dim3 qgrid(fwd_grid(sh));
-  if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_kv128_kernel<true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-    else hipLaunchKernelGGL((attn_kv128_kernel<false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  } else {
-  if (sid) hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, true>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  else hipLaunchKernelGGL((attn_bwd_dq_kernel<DH, false>), qgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dq, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  }
+  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // Split key blocks write fp32 partials after the D vector in the workspace; the reduce sums them.
