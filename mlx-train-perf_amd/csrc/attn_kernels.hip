@@ -15,15 +15,8 @@
 //                 Scores are computed transposed (keys x queries) so each lane owns one query
 //                 column: the online softmax is lane-local plus one exchange with lane^32, and the
 //                 probability (or dS) tile feeds the next product directly from registers.
-//   attn_bwd_dkv128_ab_kernel (head_dim 128): 8 waves per 128-key block, operand-split P waves
-//                 and dS waves (below).
-//   attn_bwd_dkv_kernel (head_dim 64, 96): a wave owns 32 keys of one kv head; the workgroup
-//                 sweeps every query tile of every head in the group and accumulates dK^T, dV^T in
-//                 registers (no atomics). Its tiles are register-staged: "natural" tiles keep
-//                 64 rows x head_dim with a 16-byte row pad; "transposed" tiles keep head_dim rows
-//                 x 64 positions in the 128-byte swizzled layout, with the middle two 4-position
-//                 quads of every 16-position group swapped so that one 16-byte read yields the
-//                 MFMA contraction slots that match the accumulator layout of the preceding product.
+//   attn_bwd_dkv_ab_kernel<DH, PACKED>: 8 waves per 128-key block, operand-split P waves and dS
+//                 waves (below); dK^T and dV^T accumulate in registers (no atomics).
 #include <type_traits>
 
 #include "mtp_common.hpp"
@@ -31,9 +24,6 @@
 
 namespace mtp {
 
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
-typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kKT = 64;  // positions (keys or queries) per LDS tile
 // Online softmax: the running maximum (log2 domain) is raised, and O and l rescaled, only when a
@@ -53,7 +43,7 @@ __device__ __forceinline__ uint32_t lds_addr(const char* p) {
 // ds_read_b64_tr_b16 (gfx950 LDS transpose read) of LDS byte address a + OFF, as inline asm. The
 // builtin form is treated by the compiler's wait insertion as a possible reader of every LDS DMA
 // in flight, so each tile would wait for the copies of the tile after next before its transposed
-// product; the asm form is invisible to it, and callers wait for the results (tr_wait) before use.
+// product; the asm form is invisible to it, and callers wait for the results (slab_wait) before use.
 template <int OFF>
 __device__ __forceinline__ u32x2 tr16_asm(uint32_t a) {
   u32x2 r;
@@ -115,318 +105,49 @@ __device__ __forceinline__ void tr_slab(const uint32_t (&a0)[4], const uint32_t 
 #pragma unroll
   for (int db = 0; db < NDB; ++db) f[KS][db] = tr_pair(tr16_asm<off>(a0[db]), tr16_asm<off>(a1[db]));
 }
-// Waits for every LDS read issued so far and marks the 16 fragments as produced here.
-__device__ __forceinline__ void tr_wait(bf16x8 (&f)[4][4]) {
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(f[0][0]), "+v"(f[0][1]), "+v"(f[0][2]), "+v"(f[0][3]), "+v"(f[1][0]), "+v"(f[1][1]),
-                 "+v"(f[1][2]), "+v"(f[1][3]), "+v"(f[2][0]), "+v"(f[2][1]), "+v"(f[2][2]), "+v"(f[2][3]),
-                 "+v"(f[3][0]), "+v"(f[3][1]), "+v"(f[3][2]), "+v"(f[3][3]));
-}
-
-// The dQ kernel (head_dim 64 and 96) stages one K/V tile in LDS and prefetches the next into
-// registers, so two workgroups (8 waves) share a CU. The dK/dV kernel processes each 64-query tile
-// as two 32-query halves (fewer live registers).
-
-template <int DH>
-struct AttnCfg {
-  static constexpr int kNatStride = DH * 2 + 16;
-  static constexpr int kNatBytes = kKT * kNatStride;
-  static constexpr int kTBytes = DH * 128;
-  static constexpr int kDK = DH / 16;  // MFMA contraction steps over head_dim
-  static constexpr int kDB = DH / 32;  // 32-row output blocks over head_dim
-};
-
-// Stored quad of logical quad q (4 positions) inside a transposed row.
-__device__ __forceinline__ int quad_pos(int q) {
-  const int ql = q & 3;
-  return (q & ~3) | (ql == 1 ? 2 : (ql == 2 ? 1 : ql));
-}
-__device__ __forceinline__ int t_off(int d, int sq) { return lds_off(d, sq >> 1) + ((sq & 1) << 3); }
-
-// One thread's 8-row x 8-column block of a 64-row tile with DH columns (row stride DH elements).
-template <int DH>
-struct BlockLoad {
-  u32x4 x[8];
-  int rb, cb;
-  bool active;
-
-  __device__ __forceinline__ void init(int b) {
-    active = b < DH;
-    rb = b / (DH / 8);
-    cb = b % (DH / 8);
-  }
-  __device__ __forceinline__ void load(const bf16_t* base, int rows_valid) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int r = 8 * rb + i;
-      if (active && r < rows_valid) {
-        x[i] = *reinterpret_cast<const u32x4*>(base + (long)r * DH + 8 * cb);
-      } else {
-        x[i] = zero4();
-      }
-    }
-  }
-  __device__ __forceinline__ void store_nat(char* lds) const {
-    if (!active) return;
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-      *reinterpret_cast<u32x4*>(lds + (8 * rb + i) * AttnCfg<DH>::kNatStride + 16 * cb) = x[i];
-  }
-  __device__ __forceinline__ void store_t(char* lds) const {
-    if (!active) return;
-    u32x4 y[8];
-    transpose8x8(x, y);
-    const int q0 = quad_pos(2 * rb), q1 = quad_pos(2 * rb + 1);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int d = 8 * cb + j;
-      *reinterpret_cast<u32x2*>(lds + t_off(d, q0)) = u32x2{y[j][0], y[j][1]};
-      *reinterpret_cast<u32x2*>(lds + t_off(d, q1)) = u32x2{y[j][2], y[j][3]};
-    }
-  }
-};
-
-template <int DH>
-__device__ __forceinline__ bf16x8 nat_frag(const char* tile, int row, int ks, int h) {
-  return as_bf16x8(*reinterpret_cast<const u32x4*>(tile + row * AttnCfg<DH>::kNatStride + 32 * ks + 16 * h));
-}
-__device__ __forceinline__ bf16x8 t_frag(const char* tile, int row, int ks, int h) {
-  return as_bf16x8(lds_read16(tile, lds_off(row, 2 * ks + h)));
-}
 
 __device__ __forceinline__ int heads_per_wg(int G) { return (G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1); }
 
-// ------------------------------------------------------------------------------------------
-// Backward dK, dV (key-row owners, GQA group summed in registers; no atomics).
-// ------------------------------------------------------------------------------------------
-__device__ __forceinline__ int upper_bound_i32(const int32_t* a, int n, int x) {
-  int lo = 0, hi = n;  // first index with a[i] > x
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (a[mid] > x) hi = mid;
-    else lo = mid + 1;
+namespace kvdma {
+// LDS layout of a 64-position K/V tile for head_dim DH: rows of kRowB bytes, 16-byte chunk c of row r
+// at slot c ^ sw(r). head_dim 64 packs a row into 128 B; 96 and 128 use 256 B rows (96 leaves chunks
+// 12-15 empty: their copies read nothing and write zeros). Both swizzles keep every row-fragment
+// read (ds_read_b128, 16 rows at one chunk per 16 lanes) and every transposed read
+// (ds_read_b64_tr_b16, 4 rows x 2 chunks per 16 lanes) on distinct banks, and repeat every 16 rows.
+template <int DH>
+struct Lay {
+  static constexpr int kRowB = DH == 64 ? 128 : 256;
+  static constexpr int kChunks = kRowB / 16;
+  static constexpr int kTile = kKT * kRowB;
+  static constexpr int kStage = 2 * kTile;  // K, V
+  static __device__ __forceinline__ int sw(int r) {
+    if constexpr (DH == 64) return ((r & 2) << 1) | ((r >> 2) & 3);
+    else return ((r & 3) << 2) | ((r >> 2) & 3);
   }
-  return lo;
-}
+};
 
-template <int DH, bool PACKED>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attn_bwd_dkv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
-                         const bf16_t* __restrict__ d_o, const float* __restrict__ lse, const float* __restrict__ dvec,
-                         const int32_t* __restrict__ seg_id, const int32_t* __restrict__ seg_start,
-                         bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
-                         float scale_log2, float scale, int causal, int nsplit, float* __restrict__ part) {
-  using C = AttnCfg<DH>;
-  // Q, dO natural; Q^T, dO^T; then L*log2e, D and segment ids of the 64 queries.
-  constexpr int kStage = 2 * C::kNatBytes + 2 * C::kTBytes + 3 * 256;
-  __shared__ __attribute__((aligned(16))) char lds[2 * kStage];
-
-  const int G = Hq / Hkv;
-  const int nkv = B * Hkv;
-  // Block g: split g % nsplit of key block (g / nsplit) / nkv of kv head (g / nsplit) % nkv; the
-  // earliest keys (most work under the causal mask) first.
-  const int g = blockIdx.x;
-  const int split = g % nsplit;
-  const int kvi = (g / nsplit) % nkv;
-  const int kt = (g / nsplit) / nkv;
-  const int bidx = kvi / Hkv;
-  const int kvh = kvi % Hkv;
-  const int k0 = kt * 128;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63, w = tid >> 6;
-  const int hf = lane >> 5, col = lane & 31;
-  const int kw0 = k0 + 32 * w;
-  const int kj = kw0 + col;
-  const bool kvalid = kj < S;
-  const bool wave_has = kw0 < S;
-
-  const long krow = (long)(bidx * Hkv + kvh) * S;
-  const bf16_t* kh = k + krow * DH;
-  const bf16_t* vh = v + krow * DH;
-  const int32_t* sid = PACKED ? seg_id + (long)bidx * S : nullptr;
-  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
-
-  bf16x8 kf[C::kDK], vf[C::kDK];
+// Per-lane constants: row-fragment swizzle and the transposed-read offsets tro[t] of read t (0, 1)
+// of head_dim block 0 within a 16-row slab (block db adds db << 6 by XOR: 4 db only touches chunk
+// bits 2 and up of the swizzled 16-byte chunk index).
+template <int DH>
+struct Lanes {
+  int sw_r;
+  int tro[2];
+  __device__ __forceinline__ void init() {
+    using L = Lay<DH>;
+    const int lane = threadIdx.x & 63;
+    const int hf = lane >> 5, col = lane & 31;
+    sw_r = L::sw(col & 15);
 #pragma unroll
-  for (int ks = 0; ks < C::kDK; ++ks) {
-    kf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(kh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-    vf[ks] = kvalid ? as_bf16x8(*reinterpret_cast<const u32x4*>(vh + (long)kj * DH + 16 * ks + 8 * hf)) : as_bf16x8(zero4());
-  }
-  const int my_seg = (PACKED && kvalid) ? sid[kj] : -3;
-
-  const int q_begin = causal ? (k0 / kKT) * kKT : 0;  // non-causal: every query
-  int q_end = S;
-  if (PACKED) {
-    const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
-    q_end = upper_bound_i32(sst, S, klast);
-  }
-  const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
-  const int niter = G * ntq;
-  // This workgroup's share of the key block's (head, query tile) items: [it0, it1).
-  const int it0 = (int)((long)niter * split / nsplit);
-  const int it1 = (int)((long)niter * (split + 1) / nsplit);
-
-  f32x16 dka[C::kDB], dva[C::kDB];
-#pragma unroll
-  for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      dka[db][r] = 0.f;
-      dva[db][r] = 0.f;
+    for (int t = 0; t < 2; ++t) {
+      const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
+      const int c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+      tro[t] = rl * L::kRowB + ((c0 ^ L::sw(rl)) << 4) + 8 * (lane & 1);
     }
-
-  const bool isD = tid >= 128;
-  BlockLoad<DH> bl;
-  bl.init(isD ? tid - 128 : tid);
-  float l2_reg = 0.f, d_reg = 0.f;
-  int seg_reg = 0;
-  auto load_tile = [&](int it) {
-    const int hh = it / ntq, tq = it % ntq;
-    const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
-    const int q0 = q_begin + tq * kKT;
-    bl.load((isD ? d_o : q) + (qrow + q0) * DH, S - q0);
-    if (tid < kKT) {
-      const int qq = q0 + tid;
-      const bool ok = qq < S;
-      l2_reg = ok ? lse[qrow + qq] * kLog2e : 0.f;
-      d_reg = ok ? dvec[qrow + qq] : 0.f;
-      if (PACKED) seg_reg = ok ? sid[qq] : -1;
-    }
-  };
-  auto store_tile = [&](char* st) {
-    const int off = isD ? C::kNatBytes : 0;
-    bl.store_nat(st + off);
-    bl.store_t(st + 2 * C::kNatBytes + (isD ? C::kTBytes : 0));
-    if (tid < kKT) {
-      float* sc = reinterpret_cast<float*>(st + 2 * C::kNatBytes + 2 * C::kTBytes);
-      sc[tid] = l2_reg;
-      sc[64 + tid] = d_reg;
-      reinterpret_cast<int*>(sc + 128)[tid] = seg_reg;
-    }
-  };
-
-  if (it1 > it0) {
-    load_tile(it0);
-    store_tile(lds);
   }
-  __syncthreads();
-  for (int it = it0; it < it1; ++it) {
-    const char* cur = lds + ((it - it0) & 1) * kStage;
-    const int q0 = q_begin + (it % ntq) * kKT;
-    const bool more = it + 1 < it1;
-    if (more) load_tile(it + 1);
-    bool skip = !wave_has || (causal && q0 + kKT - 1 < kw0);
-    int sst_last = 0;
-    if (PACKED && !skip) {
-      skip = sst[q0] > kw0 + 31;
-      sst_last = sst[(q0 + kKT - 1 < S) ? q0 + kKT - 1 : S - 1];
-    }
-    if (!skip) {
-      const bool need_mask = (causal && q0 < kw0 + 31) || (q0 + kKT > S) || (PACKED && sst_last > kw0);
-      const float* l2s = reinterpret_cast<const float*>(cur + 2 * C::kNatBytes + 2 * C::kTBytes);
-      const float* ds_ = l2s + 64;
-      const int* segs = reinterpret_cast<const int*>(l2s + 128);
-      const char* qt = cur + 2 * C::kNatBytes;
-      const char* dt = qt + C::kTBytes;
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        f32x16 sacc, pacc;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          sacc[r] = 0.f;
-          pacc[r] = 0.f;
-        }
-#pragma unroll
-        for (int ks = 0; ks < C::kDK; ++ks) {
-          sacc = mfma32(nat_frag<DH>(cur, 32 * qb + col, ks, hf), kf[ks], sacc);
-          pacc = mfma32(nat_frag<DH>(cur + C::kNatBytes, 32 * qb + col, ks, hf), vf[ks], pacc);
-        }
-        bf16x8 pf[2], sf[2];
-#pragma unroll
-        for (int rq = 0; rq < 4; ++rq) {
-          const int ql0 = 32 * qb + 8 * rq + 4 * hf;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(l2s + ql0);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(ds_ + ql0);
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int r = 4 * rq + u;
-            float p = fast_exp2(sacc[r] * scale_log2 - l4[u]);
-            if (need_mask) {
-              const int qq = q0 + ql0 + u;
-              bool ok = (!causal || kj <= qq) && (qq < S) && kvalid;
-              if (PACKED) ok = ok && (segs[ql0 + u] == my_seg);
-              if (!ok) p = 0.f;
-            }
-            pf[r >> 3][r & 7] = (__bf16)p;
-            sf[r >> 3][r & 7] = (__bf16)(p * (pacc[r] - d4[u]));
-          }
-        }
-#pragma unroll
-        for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) {
-            dva[db] = mfma32(t_frag(dt, 32 * db + col, 2 * qb + kk, hf), pf[kk], dva[db]);
-            dka[db] = mfma32(t_frag(qt, 32 * db + col, 2 * qb + kk, hf), sf[kk], dka[db]);
-          }
-      }
-    }
-    if (more) store_tile(lds + ((it + 1 - it0) & 1) * kStage);
-    __syncthreads();
-  }
+};
+}  // namespace kvdma
 
-  if (kvalid && nsplit == 1) {
-    bf16_t* ko = dk + (krow + kj) * DH;
-    bf16_t* vo = dv + (krow + kj) * DH;
-#pragma unroll
-    for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        *reinterpret_cast<u32x2*>(ko + d) =
-            u32x2{pack_bf16x2(dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale),
-                  pack_bf16x2(dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale)};
-        *reinterpret_cast<u32x2*>(vo + d) = u32x2{pack_bf16x2(dva[db][4 * rq], dva[db][4 * rq + 1]),
-                                                  pack_bf16x2(dva[db][4 * rq + 2], dva[db][4 * rq + 3])};
-      }
-  } else if (kvalid) {
-    // fp32 partials of this split: part[split][dk | dv][b][kv head][key][d] (attn_dkv_reduce_kernel).
-    const long plane = (long)B * Hkv * S * DH;
-    float* ko = part + (2L * split) * plane + (krow + kj) * DH;
-    float* vo = ko + plane;
-#pragma unroll
-    for (int db = 0; db < C::kDB; ++db)
-#pragma unroll
-      for (int rq = 0; rq < 4; ++rq) {
-        const int d = 32 * db + 8 * rq + 4 * hf;
-        *reinterpret_cast<f32x4*>(ko + d) = f32x4{dka[db][4 * rq] * scale, dka[db][4 * rq + 1] * scale,
-                                                  dka[db][4 * rq + 2] * scale, dka[db][4 * rq + 3] * scale};
-        *reinterpret_cast<f32x4*>(vo + d) = f32x4{dva[db][4 * rq], dva[db][4 * rq + 1], dva[db][4 * rq + 2],
-                                                  dva[db][4 * rq + 3]};
-      }
-  }
-}
-
-// ------------------------------------------------------------------------------------------
-// Operand tiles of the head_dim-128 backward: 64-query Q and dO tiles are copied global -> LDS by
-// buffer_load ... lds (16 bytes per lane, rows past S read as zeros) into 256 B rows whose 16-byte
-// chunks are XOR-swizzled by sw(r) = 4 (r & 3) + ((r >> 2) & 3): a bijection over any 16
-// consecutive rows (row fragments, 16 lanes per LDS cycle) that also sends the aligned 4-chunk block
-// of each of 4 consecutive rows to a different quarter of the banks (transposed fragments, 32 lanes
-// x 8 bytes per LDS cycle). Row fragments (S = Q K^T, dP = dO V^T) are ds_read_b128; the transposed
-// operands of dV += dO^T P and dK += Q^T dS are ds_read_b64_tr_b16 of the same tiles. The two reads
-// of a transposed fragment start at query rows 4 hf and 4 hf + 8 of each 16-row slab, which is the
-// order of the probability / dS registers (MFMA accumulator rows), so no permuted copy of a tile is
-// kept. Packed: with contiguous, gapless segments, query q shares key k's segment and q >= k iff
-// k <= q < seg_end(k), the first position whose seg_start exceeds k, so the mask is a range test on
-// a per-lane limit.
-// ------------------------------------------------------------------------------------------
-namespace dkv128 {
-constexpr int kRowB = 256;                 // bytes per 128-wide bf16 row
-constexpr int kTile = kKT * kRowB;         // 16 KiB per 64-row tile
-constexpr int kScal = 2 * 256;             // L and D of the 64 queries
-constexpr int kStage = 2 * kTile + kScal;  // Q, dO, scalars
-__device__ __forceinline__ int sw(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 // First index i in [lo, hi) with a[i] > x (hi if none); a is non-decreasing.
 __device__ __forceinline__ int first_above(const int32_t* a, int lo, int hi, int x) {
   while (lo < hi) {
@@ -436,10 +157,9 @@ __device__ __forceinline__ int first_above(const int32_t* a, int lo, int hi, int
   }
   return lo;
 }
-}  // namespace dkv128
 
 // ------------------------------------------------------------------------------------------
-// Backward dK, dV for head_dim 128, operand-split: 8 waves per 128-key workgroup, two per SIMD.
+// Backward dK, dV (head_dim 64, 96, 128), operand-split: 8 waves per 128-key workgroup, two per SIMD.
 // Waves 0-3 ("P waves") own 32 keys each and hold K: S = Q K^T, P = exp2(S scale log2 e - L log2 e)
 // (hidden pairs 0), P handed to the partner wave through LDS, dV^T += dO^T P. Waves 4-7 ("dS waves")
 // own the same keys and hold V: dP = dO V^T, dS = P (dP - D) with the partner's P, dK^T += Q^T dS.
@@ -448,29 +168,34 @@ __device__ __forceinline__ int first_above(const int32_t* a, int lo, int hi, int
 // (dV) and starts tile t+1 (S, P), the dS wave finishes tile t (dS, dK) and starts tile t+1 (dP),
 // so each has 32 products with its probability or dS arithmetic between them, and the SIMD
 // overlaps the arithmetic of one with the products of the other. Q and dO tiles are copied
-// global -> LDS in the layout above (same swizzle and fragment reads) into a ring of three stages, the copy of tile t+3 issued when tile t's stage is released; P goes through a
-// ring of three LDS buffers. The loop is unrolled by three so every stage is named statically.
+// global -> LDS in the K/V tile layout of the forward (kvdma: same swizzle and fragment reads) into
+// a ring of three stages, the copy of tile t+3 issued when tile t's stage is released; P goes
+// through a ring of three LDS buffers. The loop is unrolled by three so every stage is named
+// statically.
 // ------------------------------------------------------------------------------------------
 namespace dkvab {
-constexpr int kStage = dkv128::kStage;          // Q, dO, L log2 e, D
+constexpr int kScal = 2 * 256;                  // L and D of the 64 queries
+template <int DH>
+constexpr int kStage = 2 * kvdma::Lay<DH>::kTile + kScal;  // Q, dO, L log2 e, D
 constexpr int kPBytes = kKT * 32 * 2;           // P of one key group (64 queries x 32 keys, bf16)
 constexpr int kPBuf = 4 * kPBytes;              // P of the workgroup's four key groups
 }  // namespace dkvab
 
-template <bool PACKED>
+template <int DH, bool PACKED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
+void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                                const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
                                const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
                                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
                                float scale_log2, float scale, int causal, int nsplit,
                                float* __restrict__ part) {
-  using namespace dkv128;
-  constexpr int DH = 128;
+  using L = kvdma::Lay<DH>;
+  constexpr int kRowB = L::kRowB, kTile = L::kTile;
+  auto sw = [](int r) { return L::sw(r); };
   constexpr int kDK = DH / 16, kDB = DH / 32;
-  __shared__ __attribute__((aligned(1024))) char st0[dkvab::kStage];
-  __shared__ __attribute__((aligned(1024))) char st1[dkvab::kStage];
-  __shared__ __attribute__((aligned(1024))) char st2[dkvab::kStage];
+  __shared__ __attribute__((aligned(1024))) char st0[dkvab::kStage<DH>];
+  __shared__ __attribute__((aligned(1024))) char st1[dkvab::kStage<DH>];
+  __shared__ __attribute__((aligned(1024))) char st2[dkvab::kStage<DH>];
   __shared__ __attribute__((aligned(1024))) char pb0[dkvab::kPBuf];
   __shared__ __attribute__((aligned(1024))) char pb1[dkvab::kPBuf];
   __shared__ __attribute__((aligned(1024))) char pb2[dkvab::kPBuf];
@@ -533,12 +258,19 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[db][r] = 0.f;
 
-  // Copy lanes: wave w issues 2 x 1 KiB per tile and operand (rows 4 (8 j + w) .. +3).
-  uint32_t coff[2];
+  // Copy lanes: a tile of each operand is kNp 1 KiB pieces, piece p holding rows kRpp p .. + kRpp - 1;
+  // P wave w copies pieces w + 8 m and (for its dS partner) w + 4 + 8 m, m < kNp / 8. A lane's source
+  // is the logical chunk its LDS slot holds (chunks past head_dim point beyond the buffer and read
+  // zeros).
+  constexpr int kNp = kTile / 1024, kM = kNp / 8;
+  constexpr int kLpr = L::kChunks, kRpp = 64 / kLpr;  // lanes per LDS row, rows per piece
+  constexpr int kCopies = 4 * kM;                      // per operand pair and tile, per P wave: Q, dO
+  uint32_t coff[kM];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = 4 * (8 * j + w) + (lane >> 4);
-    coff[j] = (uint32_t)(row * kRowB + (((lane & 15) ^ sw(row)) << 4));
+  for (int m = 0; m < kM; ++m) {
+    const int row = kRpp * (8 * m + w) + lane / kLpr;
+    const int c = (lane % kLpr) ^ sw(row);
+    coff[m] = 16 * c < 2 * DH ? (uint32_t)(row * 2 * DH + 16 * c) : 0x7ffffff0u;
   }
   int ro[kDK];
 #pragma unroll
@@ -575,15 +307,16 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     const long qrow = (long)(bidx * Hq + kvh * G + hh) * S;
     const int q0 = q_begin + tq * kKT;
     const int rows = live ? ((S - q0 < kKT) ? S - q0 : kKT) : 0;
-    return CopySrc{q + (qrow + q0) * DH, d_o + (qrow + q0) * DH, (w < 4 ? lse : dvec) + qrow + q0, rows * kRowB, rows * 4};
+    return CopySrc{q + (qrow + q0) * DH, d_o + (qrow + q0) * DH, (w < 4 ? lse : dvec) + qrow + q0, rows * 2 * DH, rows * 4};
   };
-  // The P waves copy for their dS partners too (the dS waves are the longer role): load j (0-7) of a
-  // P wave covers Q (j < 4) or dO rows, piece (j & 1) of wave w + 4 (j & 2), whose rows lie 16 on
-  // with the same swizzle (sw(r + 16) = sw(r)).
+  // The P waves copy for their dS partners too (the dS waves are the longer role): load j of a P wave
+  // covers Q (j < 2 kM) or dO rows, piece 8 m + w (m = j % kM) or that of wave w + 4 (j / kM odd),
+  // whose rows lie 4 kRpp on with the same swizzle (it repeats every 16 rows).
   auto issue_one = [&](const CopySrc& c, char* st, int j) __attribute__((always_inline)) {
-    const int pw = w + ((j & 2) ? 4 : 0);
-    lds_copy16(j < 4 ? c.qs : c.ds, c.bytes, st + (j < 4 ? 0 : kTile) + 1024 * (8 * (j & 1) + pw),
-               coff[j & 1] + ((j & 2) ? 16u * kRowB : 0u));
+    const int m = j % kM, part = (j / kM) & 1;
+    const bool qop = j < 2 * kM;
+    lds_copy16(qop ? c.qs : c.ds, c.bytes, st + (qop ? 0 : kTile) + 1024 * (8 * m + w + 4 * part),
+               coff[m] + (part ? (uint32_t)(4 * kRpp * 2 * DH) : 0u));
   };
   auto issue_scal = [&](const CopySrc& c, char* st) __attribute__((always_inline)) {
     if (grp == 0) lds_copy4(c.scal, c.sbytes, st + 2 * kTile + (pwave ? 0 : 256), (uint32_t)(4 * lane));
@@ -612,9 +345,13 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
         if (ks + 2 < kDK) rd(ks + 2);
 #pragma unroll
         for (int h = 0; h < 2; ++h) a1[h] = mfma32(rf[ks % 3][h], opf[ks], a1[h]);
-        // The copy loads of the tile after next, one per k16 step of the P waves, between products
-        // that wait: a copy load holds its wave at issue while the CU's load path serves others.
-        if (pwave) issue_one(cx, sx, ks);
+        // The copy loads of the tile after next, spread over the k16 steps of the P waves, between
+        // products that wait: a copy load holds its wave at issue while the CU's load path serves
+        // others.
+        if (pwave) {
+#pragma unroll
+          for (int j = kCopies * ks / kDK; j < kCopies * (ks + 1) / kDK; ++j) issue_one(cx, sx, j);
+        }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
@@ -670,8 +407,8 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
       }
     }
     bf16x8 tf[4][4];
-    tr_slab<0>(ta0, ta1, tf);
-    tr_slab<1>(ta0, ta1, tf);
+    tr_slab<0, kDB, kRowB>(ta0, ta1, tf);
+    tr_slab<1, kDB, kRowB>(ta0, ta1, tf);
     bf16x8 bo[2][2];
 #pragma unroll
     for (int h = 0; h < 2; ++h)
@@ -693,18 +430,18 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
           }
         }
     }
-    slab_wait<8>(tf[0]);
+    slab_wait<2 * kDB, kDB>(tf[0]);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[0][db], bo[0][0], acc[db]);
-    tr_slab<2>(ta0, ta1, tf);
-    slab_wait<8>(tf[1]);
+    tr_slab<2, kDB, kRowB>(ta0, ta1, tf);
+    slab_wait<2 * kDB, kDB>(tf[1]);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[1][db], bo[0][1], acc[db]);
-    tr_slab<3>(ta0, ta1, tf);
-    slab_wait<8>(tf[2]);
+    tr_slab<3, kDB, kRowB>(ta0, ta1, tf);
+    slab_wait<2 * kDB, kDB>(tf[2]);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[2][db], bo[1][0], acc[db]);
-    slab_wait<0>(tf[3]);
+    slab_wait<0, kDB>(tf[3]);
 #pragma unroll
     for (int db = 0; db < kDB; ++db) acc[db] = mfma32(tf[3][db], bo[1][1], acc[db]);
   };
@@ -725,7 +462,7 @@ void attn_bwd_dkv128_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __res
     if (pwave) {
       const CopySrc c0 = copy_src(0, true);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) issue_one(c0, st0, j);
+      for (int j = 0; j < kCopies; ++j) issue_one(c0, st0, j);
     }
     issue_scal(copy_src(0, true), st0);
     sync();
@@ -818,45 +555,6 @@ __global__ __launch_bounds__(256) void attn_dkv_reduce_kernel(const float* __res
 // below); S^T = K Q^T and dP^T = V dO^T read row fragments, O^T += V^T P^T and dQ^T += K^T dS^T
 // read transposed fragments of the same tiles. Two LDS stages, one barrier per key tile.
 // ------------------------------------------------------------------------------------------
-namespace kvdma {
-// LDS layout of a 64-position K/V tile for head_dim DH: rows of kRowB bytes, 16-byte chunk c of row r
-// at slot c ^ sw(r). head_dim 64 packs a row into 128 B; 96 and 128 use 256 B rows (96 leaves chunks
-// 12-15 empty: their copies read nothing and write zeros). Both swizzles keep every row-fragment
-// read (ds_read_b128, 16 rows at one chunk per 16 lanes) and every transposed read
-// (ds_read_b64_tr_b16, 4 rows x 2 chunks per 16 lanes) on distinct banks, and repeat every 16 rows.
-template <int DH>
-struct Lay {
-  static constexpr int kRowB = DH == 64 ? 128 : 256;
-  static constexpr int kChunks = kRowB / 16;
-  static constexpr int kTile = kKT * kRowB;
-  static constexpr int kStage = 2 * kTile;  // K, V
-  static __device__ __forceinline__ int sw(int r) {
-    if constexpr (DH == 64) return ((r & 2) << 1) | ((r >> 2) & 3);
-    else return ((r & 3) << 2) | ((r >> 2) & 3);
-  }
-};
-
-// Per-lane constants: row-fragment swizzle and the transposed-read offsets tro[t] of read t (0, 1)
-// of head_dim block 0 within a 16-row slab (block db adds db << 6 by XOR: 4 db only touches chunk
-// bits 2 and up of the swizzled 16-byte chunk index).
-template <int DH>
-struct Lanes {
-  int sw_r;
-  int tro[2];
-  __device__ __forceinline__ void init() {
-    using L = Lay<DH>;
-    const int lane = threadIdx.x & 63;
-    const int hf = lane >> 5, col = lane & 31;
-    sw_r = L::sw(col & 15);
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int rl = 4 * hf + 8 * t + ((lane & 15) >> 2);
-      const int c0 = 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-      tro[t] = rl * L::kRowB + ((c0 ^ L::sw(rl)) << 4) + 8 * (lane & 1);
-    }
-  }
-};
-}  // namespace kvdma
 
 template <int DH, bool PACKED, bool DQ>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
@@ -1370,13 +1068,8 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   const int ns = attn_dkv_nsplit(sh.b, sh.hq, sh.hkv, sh.s, DH, sh.causal);
   float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(dvec) + attn_dvec_bytes(sh.b, sh.hq, sh.s));
   dim3 sgrid(((sh.s + 127) / 128) * sh.b * sh.hkv * ns);
-  if constexpr (DH == 128) {
-    if (sid) hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
-    else hipLaunchKernelGGL((attn_bwd_dkv128_ab_kernel<false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
-  } else {
-    if (sid) hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, true>), sgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
-    else hipLaunchKernelGGL((attn_bwd_dkv_kernel<DH, false>), sgrid, block, 0, st, q, k, v, d_o, lse, dvec, sid, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
-  }
+  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
+  else hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
   e = hipGetLastError();
   if (e != hipSuccess || ns == 1) return e;
   const long plane = (long)sh.b * sh.hkv * sh.s * DH;
