@@ -281,25 +281,26 @@ def lce_ladder(reps=10):
 # ------------------------------------------------------------------------------------------------
 # Attention (configs 4, 5)
 # ------------------------------------------------------------------------------------------------
-def _attn_inputs(s, seed=0, b=ATT_B):
+def _attn_inputs(s, seed=0, b=ATT_B, dh=ATT_DH):
     import torch
 
     g = torch.Generator(device="cuda").manual_seed(seed)
-    mk = lambda h: torch.randn(b, h, s, ATT_DH, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
+    mk = lambda h: torch.randn(b, h, s, dh, generator=g, device="cuda").to(torch.bfloat16)  # noqa: E731
     return mk(ATT_HQ), mk(ATT_HKV), mk(ATT_HKV), mk(ATT_HQ)
 
 
-def bench_attention(steps, warmup, mode="causal", s=None):
-    """Flash attention fwd and fwd+bwd at B=1, Hq=32, Hkv=8, head_dim 128. mode: "causal" (config 4,
-    S=8192), "packed" (config 5, S=16384, seeded document lengths), "full" (non-causal, S=8192)."""
+def bench_attention(steps, warmup, mode="causal", s=None, dh=ATT_DH):
+    """Flash attention fwd and fwd+bwd at B=1, Hq=32, Hkv=8, head_dim `dh` (128: configs 4, 5). mode:
+    "causal" (config 4, S=8192), "packed" (config 5, S=16384, seeded document lengths), "full"
+    (non-causal, S=8192)."""
     import torch
 
     from mlx_train_perf.attention.api import kernel_backward, kernel_forward
     from mlx_train_perf.plan import launch as plan
 
     s = s or (16384 if mode == "packed" else 8192)
-    q, k, v, do = _attn_inputs(s)
-    scale = 1.0 / math.sqrt(ATT_DH)
+    q, k, v, do = _attn_inputs(s, dh=dh)
+    scale = 1.0 / math.sqrt(dh)
     sid = sst = None
     causal = mode != "full"
     if mode == "packed":
@@ -336,8 +337,8 @@ def bench_attention(steps, warmup, mode="causal", s=None):
     torch.cuda.empty_cache()
     fb_peak, _ = marginal_peak_bytes(fwdbwd)
     state.clear()
-    flops_fwd = 2.0 * 2 * ATT_DH * ATT_HQ * ATT_B * pairs
-    flops_fb = 2.0 * 7 * ATT_DH * ATT_HQ * ATT_B * pairs
+    flops_fwd = 2.0 * 2 * dh * ATT_HQ * ATT_B * pairs
+    flops_fb = 2.0 * 7 * dh * ATT_HQ * ATT_B * pairs
     out = {"seq": s, "fwd_ms": fwd_s * 1e3, "fwdbwd_ms": fb_s * 1e3, "bwd_ms": (fb_s - fwd_s) * 1e3,
            "pairs_per_head": pairs, "algorithmic_tflop": flops_fb / 1e12,
            "fwd_tflops": flops_fwd / fwd_s / 1e12, "tflops": flops_fb / fb_s / 1e12,
@@ -388,6 +389,16 @@ def attention_ladder(steps, warmup):
     for s in (2048, 4096, 8192):
         r = bench_attention(steps, warmup, "causal", s=s)
         out[f"s{s}"] = {k: r[k] for k in ("fwd_ms", "fwdbwd_ms", "fwd_tflops", "tflops", "mfma_frac")}
+    return out
+
+
+def attention_headdim_ladder(steps, warmup):
+    """Causal fwd and fwd+bwd at S=8192, 32/8 heads, head_dim 64 and 96 (the other head dims the
+    reference's kernels take, src/mlx_train_perf/attention/api.py:107-110; 128 is config 4 itself)."""
+    out = {}
+    for dh in (64, 96):
+        r = bench_attention(steps, warmup, "causal", dh=dh)
+        out[f"d{dh}"] = {k: r[k] for k in ("fwd_ms", "fwdbwd_ms", "fwd_tflops", "tflops", "mfma_frac")}
     return out
 
 
@@ -777,6 +788,7 @@ def main():
         torch.cuda.empty_cache()
         result["lce_ladder_fwd"] = lce_ladder()
         result["attention_ladder_causal"] = attention_ladder(max(3, args.steps // 2), 2)
+        result["attention_headdim_s8192"] = attention_headdim_ladder(max(3, args.steps // 2), 2)
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline_lce()
         result["cpu_baseline_c1"] = cpu_baseline_c1()
