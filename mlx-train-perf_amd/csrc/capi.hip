@@ -199,15 +199,37 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) 
   return c;
 }
 
+// Bytes of the fp32 part tiles of a split dH product: the most any (row block, vocab chunk) of the
+// backward takes (the last row block and the last chunk may be shorter and split otherwise).
+size_t lce_dh_parts_max(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+  const int64_t last_rows = n - (n - 1) / row_block * row_block;
+  const int64_t last_tiles = (v - (v - 1) / chunk * chunk + kTile - 1) / kTile;
+  size_t most = 0;
+  for (int64_t rows : {row_block, last_rows})
+    for (int64_t kt : {chunk / kTile, last_tiles}) {
+      const size_t b = mtp::lce_dh_parts_bytes((long)rows, (long)d, (long)kt);
+      if (b > most) most = b;
+    }
+  return most;
+}
+
+// Gradient tiles [row_block][chunk + kGPitchPad] bf16, then the fp32 dH accumulator
+// [row_block][d] when the vocab takes more than one chunk, then the split dH's fp32 part tiles.
+size_t lce_bwd_acc_offset(int64_t chunk, int64_t row_block) {
+  return (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2;
+}
+size_t lce_bwd_parts_offset(int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+  const int64_t nchunks = (v + chunk - 1) / chunk;
+  return lce_bwd_acc_offset(chunk, row_block) + (nchunks > 1 ? (size_t)row_block * (size_t)d * 4 : 0);
+}
+
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block) {
   (void)head_kind;
   if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
+  if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block < 1 || row_block > n) row_block = n;
-  const int64_t nchunks = (v + chunk - 1) / chunk;
-  size_t bytes = (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2;
-  if (nchunks > 1) bytes += (size_t)row_block * (size_t)d * 4;
-  return bytes;
+  return lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block);
 }
 
 int64_t mtp_lce_head_t_ld(int64_t v) { return v < 1 ? 0 : (int64_t)mtp::lce_head_t_ld((long)v); }
@@ -254,14 +276,15 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
     return fail(MTP_ERR_WORKSPACE, "lce backward needs a workspace of %zu bytes at chunk=%lld, row_block=%lld (got %zu)", need, (long long)chunk, (long long)row_block, workspace ? workspace_bytes : (size_t)0);
   if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
   mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
-  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2);
+  float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_acc_offset(chunk, row_block));
+  float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_parts_offset(d, v, chunk, row_block));
   mtp::LceHead head = make_head(w, w_q, scales, biases, head_kind);
   head.wt = static_cast<const mtp::bf16_t*>(w_t);
   hipError_t e = mtp::launch_lce_bwd(head, static_cast<const mtp::bf16_t*>(hidden),
                                      targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
                                      (int)row_block,
                                      static_cast<mtp::bf16_t*>(d_hidden), static_cast<mtp::bf16_t*>(d_w), gbuf, acc32,
-                                     static_cast<hipStream_t>(stream));
+                                     parts, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }

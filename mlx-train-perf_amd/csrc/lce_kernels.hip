@@ -1306,21 +1306,55 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
   }
 }
 
+// Split-K order of the dH product: `ksplit` parts of the vocab contraction for each of the
+// mtiles x ntiles output tiles. With sa > 0 (sa | mtiles, (32 / sa) | ntiles) the work is dealt in
+// blocks of sa x (32 / sa) tiles of one part, block s going to XCD s % 8 in resident round s / 8, so
+// the 32 workgroups of one XCD read sa row panels and 32 / sa column panels of the same vocab range
+// per stage. With sa == 0 workgroup g takes part g / (M N) and tile g % (M N), row-major. Returns
+// false for padding workgroups.
+__device__ __forceinline__ bool xcd_split_tile(int mtiles, int ntiles, int ksplit, int sa, int& m, int& n,
+                                               int& part) {
+  const int g = blockIdx.x;
+  if (sa == 0) {
+    const int tiles = mtiles * ntiles;
+    part = g / tiles;
+    m = (g % tiles) / ntiles;
+    n = g % ntiles;
+    return part < ksplit;
+  }
+  const int sb = 32 / sa, slot = g >> 3;
+  const int blk = (slot >> 5) * 8 + (g & 7), i = slot & 31;
+  const int mb = mtiles / sa, nb = ntiles / sb;
+  part = blk / (mb * nb);
+  if (part >= ksplit) return false;
+  const int rem = blk % (mb * nb);
+  m = (rem % mb) * sa + i % sa;
+  n = (rem / mb) * sb + i / sa;
+  return true;
+}
+
 // ------------------------------------------------------------------------------------------
 // Backward step 2: dH[t][d] (+)= sum_{v in chunk} G[t][v] W[v][d].
 // mode 0: acc32 = part; 1: acc32 += part; 2: dH = bf16(acc32 + part); 3: dH = bf16(part).
+// ksplit > 1: each workgroup contracts one of ksplit vocab ranges of its tile (k tiles
+// [p kt / ksplit, (p + 1) kt / ksplit) of the chunk's kt) and stores the fp32 tile to
+// parts[p][tile][256][256] (tile = row tile * dtiles + column tile); lce_bwd_dh_reduce_kernel sums
+// the parts in order and applies the mode.
 // ------------------------------------------------------------------------------------------
 template <int Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16_t* __restrict__ W,
                        const bf16_t* __restrict__ Wt, int ldt, const uint32_t* __restrict__ Wq,
                        const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, int N, int D, int V,
-                       int v_begin, int v_end, float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode) {
+                       int v_begin, int v_end, float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode,
+                       int ksplit, int split_a, float* __restrict__ parts) {
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
-  int rt, dt;
-  if (xcd_rect_tile(rtiles, dtiles, rt, dt)) {
+  int rt, dt, part = 0;
+  if (ksplit > 1) {
+    if (!xcd_split_tile(rtiles, dtiles, ksplit, split_a, rt, dt, part)) return;
+  } else if (xcd_rect_tile(rtiles, dtiles, rt, dt)) {
   } else if (rtiles % 8 == 0) {
     if (!xcd_rows_tile(rtiles, dtiles, rt, dt)) return;
   } else if (!xcd_tile(rtiles, dtiles, rt, dt)) {
@@ -1333,50 +1367,69 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
   const int t0 = rt * kTile;
   const int d0 = dt * kTile;
   const int vlim = v_end < V ? v_end : V;
+  // This workgroup's vocab range [vb, vb + kc) (the whole chunk unless split).
+  const int ktiles = kc / kTile;
+  const int kb = (int)(((long)part * ktiles) / ksplit);
+  const int koff = kb * kTile;
+  kc = ((int)(((long)(part + 1) * ktiles) / ksplit) - kb) * kTile;
+  const int vb = v_begin + koff;
   const int nk = kc / kBK;
-  const bool full = (t0 + kTile <= N) && (v_begin + kc <= vlim) && (d0 + kTile <= D);
+  const bool full = (t0 + kTile <= N) && (vb + kc <= vlim) && (d0 + kTile <= D);
 
   f32x16 acc[4][kNJ];
   if (D % kBK == 0 && Wt != nullptr) {
     // Transposed (for the 4-bit head: dequantized) head [D][ldt], zeros past V: both operands
     // are K-contiguous rows.
     DmaRowOp oa;
-    oa.init(G + (long)t0 * ldg, ldg, N - t0);
+    oa.init(G + (long)t0 * ldg + koff, ldg, N - t0);
     DmaRowOp ob;
-    ob.init(Wt + (long)d0 * ldt + v_begin, ldt, D - d0);
+    ob.init(Wt + (long)d0 * ldt + vb, ldt, D - d0);
     gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
   } else if (!Q4 && D % kBK == 0) {
     // G columns past the chunk's last vocab row are zeros, so the W rows they meet only need to
     // be readable (kvalid clamps them to the last row of W).
     DmaRowOp oa;
-    oa.init(G + (long)t0 * ldg, ldg, N - t0);
+    oa.init(G + (long)t0 * ldg + koff, ldg, N - t0);
     DmaTransOp ob;
-    ob.init(W + (long)v_begin * D + d0, D, V - v_begin, D - d0);
+    ob.init(W + (long)vb * D + d0, D, V - vb, D - d0);
     gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
   } else {
     RowKLoader la;
-    la.base = G + (long)t0 * ldg;
+    la.base = G + (long)t0 * ldg + koff;
     la.ld = ldg;
     la.nrows = N - t0;
     la.K = kc;
     if constexpr (Q4) {
       Q4TransLoader lb;
-      lb.wq = Wq + (long)v_begin * (D >> 3);
-      lb.sc = Sc + (long)v_begin * (D >> 6);
-      lb.bi = Bi + (long)v_begin * (D >> 6);
+      lb.wq = Wq + (long)vb * (D >> 3);
+      lb.sc = Sc + (long)vb * (D >> 6);
+      lb.bi = Bi + (long)vb * (D >> 6);
       lb.D = D;
       lb.d0 = d0;
-      lb.kvalid = vlim - v_begin;
+      lb.kvalid = vlim - vb;
       lb.dvalid = D - d0;
       if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     } else {
       TransLoader lb;
-      lb.w = W + (long)v_begin * D + d0;
+      lb.w = W + (long)vb * D + d0;
       lb.ld = D;
-      lb.kvalid = vlim - v_begin;
+      lb.kvalid = vlim - vb;
       lb.dvalid = D - d0;
       if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
     }
+  }
+  if (ksplit > 1) {
+    // The whole 256 x 256 fp32 tile (rows or columns past N or D are never read back).
+    float* dst = parts + ((long)(part * rtiles + rt) * dtiles + dt) * (kTile * kTile);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j)
+          dst[(128 * wa + 32 * i + 8 * (r >> 2) + 4 * lhalf + (r & 3)) * kTile + 64 * wb + 32 * j + lcol] =
+              acc[i][j][r];
+    return;
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -1403,6 +1456,32 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
     }
 }
 
+
+// Sum of a split dH product's fp32 parts (in part order, so the result does not depend on which
+// workgroup finished first), then the mode of lce_bwd_dh_kernel. One block per 4 rows of a tile,
+// one thread per 4 columns (D % 4 == 0, so a group of 4 is inside or past D as a whole).
+__global__ __launch_bounds__(256) void lce_bwd_dh_reduce_kernel(const float* __restrict__ parts, int ksplit, int N,
+                                                                 int D, float* __restrict__ acc32,
+                                                                 bf16_t* __restrict__ dH, int mode) {
+  const int dtiles = (D + kTile - 1) / kTile;
+  const long tiles = (long)((N + kTile - 1) / kTile) * dtiles;
+  const long tile = blockIdx.x >> 6;
+  const int row = 4 * (blockIdx.x & 63) + (threadIdx.x >> 6), col = 4 * (threadIdx.x & 63);
+  const int t = (int)(tile / dtiles) * kTile + row, d = (int)(tile % dtiles) * kTile + col;
+  if (t >= N || d >= D) return;
+  const float* src = parts + (tile * kTile + row) * kTile + col;
+  f32x4 s = *reinterpret_cast<const f32x4*>(src);
+  for (int p = 1; p < ksplit; ++p) s += *reinterpret_cast<const f32x4*>(src + p * tiles * (kTile * kTile));
+  const long o = (long)t * D + d;
+  if (mode == 0) {
+    *reinterpret_cast<f32x4*>(acc32 + o) = s;
+  } else if (mode == 1) {
+    *reinterpret_cast<f32x4*>(acc32 + o) += s;
+  } else {
+    if (mode == 2) s += *reinterpret_cast<const f32x4*>(acc32 + o);
+    *reinterpret_cast<u32x2*>(dH + o) = u32x2{pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3])};
+  }
+}
 
 // ------------------------------------------------------------------------------------------
 // Backward step 3 (trainable dense head only): dW[v][d] = sum_t G[t][v] H[t][d] for the vocab rows
@@ -1534,16 +1613,65 @@ hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt,
 // measured ~1% faster at the flagship shape than two rounds of half the tiles each).
 constexpr long kFwdWaves = 1;
 
-// Vocab splits for a persistent launch over N rows and V vocab columns: enough workgroups for
-// `per_cu` per compute unit, in a multiple of 8 when that many so every XCD residue holds a split.
+// Vocab splits for a persistent launch over N rows and V vocab columns with `per_cu` workgroups
+// resident per compute unit: the count that minimizes resident rounds x (vocab tiles per split + 1),
+// the 1 standing for a workgroup's pipeline fill and partial store; ties go to fewer splits. (A
+// count that only just overflows one round, e.g. 48 row tiles x 6 splits = 288 workgroups, would
+// run two rounds of one split's tiles each.)
 static int lce_nsplit(long N, long V, int per_cu) {
   const long rtiles = (N + kTile - 1) / kTile;
   const long vtiles = (V + kTile - 1) / kTile;
-  long ns = ((long)per_cu * kNumCU + rtiles - 1) / rtiles;
-  if (ns >= 8) ns = (ns + 7) / 8 * 8;
-  if (ns > vtiles) ns = vtiles;
-  if (ns < 1) ns = 1;
-  return (int)ns;
+  const long slots = (long)per_cu * kNumCU;
+  long best = 1, best_cost = -1;
+  for (long ns = 1; ns <= vtiles && ns <= 1024; ++ns) {
+    const long cost = (rtiles * ns + slots - 1) / slots * ((vtiles + ns - 1) / ns + 1);
+    if (best_cost < 0 || cost < best_cost) {
+      best = ns;
+      best_cost = cost;
+    }
+  }
+  return (int)best;
+}
+
+// Parts of the dH product's vocab contraction (1 = none) for `rows` rows, D columns and `ktiles`
+// 256-wide vocab tiles: the count that minimizes resident rounds (one workgroup per CU) x (k tiles
+// per part + a workgroup's fill and store: 1, or 4 for an fp32 part) plus the reduction's reads
+// (about parts x tiles / 128 k-tile times); at most 8 parts of at least 8 k tiles each. The
+// flagship's 16 x 16 tiles per row block fill one round and stay whole; 16 x 20 (D = 5120) take
+// 4 parts, 8 x 16 (N = 2048) take 2.
+int lce_dh_ksplit(long rows, long D, long ktiles) {
+  const long tiles = ((rows + kTile - 1) / kTile) * ((D + kTile - 1) / kTile);
+  int best = 1;
+  long best_cost = (tiles + kNumCU - 1) / kNumCU * (ktiles + 1);
+  for (int ks = 2; ks <= 8 && ks * 8 <= ktiles; ++ks) {
+    const long cost = (tiles * ks + kNumCU - 1) / kNumCU * ((ktiles + ks - 1) / ks + 4) + ks * tiles / 128;
+    if (cost < best_cost) {
+      best = ks;
+      best_cost = cost;
+    }
+  }
+  return best;
+}
+
+size_t lce_dh_parts_bytes(long rows, long D, long ktiles) {
+  const int ks = lce_dh_ksplit(rows, D, ktiles);
+  if (ks == 1) return 0;
+  const long tiles = ((rows + kTile - 1) / kTile) * ((D + kTile - 1) / kTile);
+  return (size_t)ks * (size_t)tiles * kTile * kTile * sizeof(float);
+}
+
+// Block edge for xcd_split_tile: the sa x (32 / sa) block with the fewest panels per stage that
+// divides the tile grid, or 0 (row-major order) when none does.
+static int lce_dh_split_a(int rtiles, int dtiles) {
+  int best = 0, best_sum = 1 << 30;
+  for (int a = 1; a <= 32; a *= 2) {
+    const int b = 32 / a;
+    if (rtiles % a == 0 && dtiles % b == 0 && a + b < best_sum) {
+      best = a;
+      best_sum = a + b;
+    }
+  }
+  return best;
 }
 
 int lce_fwd_nsplit(long N, long V) { return lce_nsplit(N, V, kFwdWaves); }
@@ -1577,7 +1705,8 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 // One block of rows [0, N) of the backward (all its vocab chunks).
 static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                                const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
-                               bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
+                               bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts,
+                               hipStream_t stream) {
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   const int nchunks = (V + chunk - 1) / chunk;
@@ -1611,16 +1740,28 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
     else if (c == 0) mode = 0;
     else if (c == nchunks - 1) mode = 2;
     else mode = 1;
+    const int ks = lce_dh_ksplit(N, D, ctiles);
+    const int sa = ks > 1 ? lce_dh_split_a(rtiles, dtiles) : 0;
     dim3 hgrid(8 * rtiles * ((dtiles + 7) / 8));
+    if (ks > 1) {
+      const int blocks = sa ? (rtiles / sa) * (dtiles / (32 / sa)) * ks : 0;
+      hgrid = dim3(sa ? (blocks + 7) / 8 * 256 : rtiles * dtiles * ks);
+    }
     if (h.q4) {
       hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
-                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode);
+                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
     } else {
       hipLaunchKernelGGL(lce_bwd_dh_kernel<0>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
-                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode);
+                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (ks > 1) {
+      hipLaunchKernelGGL(lce_bwd_dh_reduce_kernel, dim3(rtiles * dtiles * 64), dim3(256), 0, stream, parts, ks, N, D,
+                         acc32, dH, mode);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+    }
     if (dW != nullptr && !h.q4) {
       dim3 wgrid(8 * ctiles * ((dtiles + 7) / 8));
       if (N % kBK == 0 && D % kBK == 0)
@@ -1639,13 +1780,14 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
 // sums over every row, so it takes a single block.
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
-                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream) {
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, hipStream_t stream) {
   if (dW != nullptr || row_block >= N)
-    return lce_bwd_rows(h, H, targets, lse, dnll, N, D, V, ignore_index, chunk, dH, dW, Gbuf, acc32, stream);
+    return lce_bwd_rows(h, H, targets, lse, dnll, N, D, V, ignore_index, chunk, dH, dW, Gbuf, acc32, parts,
+                        stream);
   for (int r0 = 0; r0 < N; r0 += row_block) {
     const int rows = (N - r0 < row_block) ? N - r0 : row_block;
     hipError_t e = lce_bwd_rows(h, H + (long)r0 * D, targets + r0, lse + r0, dnll + r0, rows, D, V, ignore_index,
-                                chunk, dH + (long)r0 * D, nullptr, Gbuf, acc32, stream);
+                                chunk, dH + (long)r0 * D, nullptr, Gbuf, acc32, parts, stream);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

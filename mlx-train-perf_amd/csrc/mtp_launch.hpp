@@ -27,6 +27,10 @@ struct LceHead {
 
 int lce_fwd_nsplit(long N, long V);
 long lce_head_t_ld(long V);
+// Parts of the backward's dH contraction over `ktiles` 256-wide vocab tiles for a block of `rows`
+// rows (1 = one workgroup per output tile), and the fp32 part tiles that takes (0 when 1).
+int lce_dh_ksplit(long rows, long D, long ktiles);
+size_t lce_dh_parts_bytes(long rows, long D, long ktiles);
 
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream);
 
@@ -36,7 +40,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
-                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, hipStream_t stream);
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, hipStream_t stream);
 
 struct AttnShape {
   int b, hq, hkv, s, dh;

@@ -5,8 +5,8 @@ The reference plans Metal dispatches against a GPU-watchdog time budget
 watchdog on compute queues, so every op is one launch sequence and the planner's job is geometry and
 workspace: how many vocab splits the LCE forward uses, how wide a backward vocab chunk may be for a
 workspace budget, and the attention grid. The integer formulas here mirror the C-ABI's
-(mlx-train-perf_amd/csrc/lce_kernels.hip lce_fwd_nsplit; capi.hip mtp_lce_bwd_row_block, mtp_lce_bwd_chunk;
-attn_kernels.hip attn_dkv_nsplit) so that plans
+(mlx-train-perf_amd/csrc/lce_kernels.hip lce_nsplit, lce_dh_ksplit; capi.hip mtp_lce_bwd_row_block,
+mtp_lce_bwd_chunk, mtp_lce_bwd_workspace_bytes; attn_kernels.hip attn_dkv_nsplit) so that plans
 can be checked and sized on the CPU; a GPU test asserts they agree with the library.
 """
 from __future__ import annotations
@@ -46,15 +46,45 @@ def packed_pairs(lengths: list[int]) -> int:
 FWD_WGS_PER_CU = 1  # forward workgroups per CU (csrc/lce_kernels.hip)
 
 
-def lce_fwd_splits(n: int, v: int) -> int:
-    """Vocab splits of the forward: about FWD_WGS_PER_CU workgroups per CU, a multiple of 8 (one
-    split per XCD residue) when >= 8, never more than the vocab tiles."""
+def lce_nsplit(n: int, v: int, per_cu: int = FWD_WGS_PER_CU) -> int:
+    """Vocab splits of a persistent LCE launch (forward, and the backward's gradient tiles per
+    chunk): the count minimizing resident rounds x (vocab tiles per split + 1), ties to fewer
+    splits, never more than the vocab tiles (or 1024)."""
     rtiles = -(-n // TILE)
     vtiles = -(-v // TILE)
-    ns = -(-(FWD_WGS_PER_CU * NUM_CU) // rtiles)
-    if ns >= 8:
-        ns = -(-ns // 8) * 8
-    return max(1, min(ns, vtiles))
+    slots = per_cu * NUM_CU
+    best, best_cost = 1, None
+    for ns in range(1, min(vtiles, 1024) + 1):
+        cost = -(-(rtiles * ns) // slots) * (-(-vtiles // ns) + 1)
+        if best_cost is None or cost < best_cost:
+            best, best_cost = ns, cost
+    return best
+
+
+def lce_fwd_splits(n: int, v: int) -> int:
+    """Vocab splits of the forward (lce_nsplit at FWD_WGS_PER_CU workgroups per CU)."""
+    return lce_nsplit(n, v, FWD_WGS_PER_CU)
+
+
+def lce_dh_ksplit(rows: int, d: int, ktiles: int) -> int:
+    """Parts of the backward's dH contraction over `ktiles` 256-wide vocab tiles for a block of
+    `rows` rows: the count (1..8, each part >= 8 k tiles) minimizing resident rounds x (k tiles per
+    part + 1, or + 4 for an fp32 part) + parts x tiles / 128 for the ordered reduction."""
+    tiles = -(-rows // TILE) * -(-d // TILE)
+    best, best_cost = 1, -(-tiles // NUM_CU) * (ktiles + 1)
+    ks = 2
+    while ks <= 8 and ks * 8 <= ktiles:
+        cost = -(-(tiles * ks) // NUM_CU) * (-(-ktiles // ks) + 4) + ks * tiles // 128
+        if cost < best_cost:
+            best, best_cost = ks, cost
+        ks += 1
+    return best
+
+
+def lce_dh_parts_bytes(rows: int, d: int, ktiles: int) -> int:
+    """fp32 part tiles of a split dH product (0 when it is not split)."""
+    ks = lce_dh_ksplit(rows, d, ktiles)
+    return 0 if ks == 1 else ks * -(-rows // TILE) * -(-d // TILE) * TILE * TILE * 4
 
 
 def lce_fwd_workspace_bytes(n: int, v: int) -> int:
@@ -90,10 +120,15 @@ def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
 
 
 def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int | None = None) -> int:
-    """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD] plus the fp32 dH accumulator when >1 chunk."""
+    """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD], the fp32 dH accumulator when >1 chunk,
+    and the fp32 part tiles of a split dH product (the most any row block and chunk takes)."""
+    chunk = min(chunk, -(-v // TILE) * TILE)
     rows = n if not row_block or row_block > n else row_block
     nchunks = -(-v // chunk)
-    return rows * (chunk + G_PITCH_PAD) * 2 + (rows * d * 4 if nchunks > 1 else 0)
+    last_rows = n - (n - 1) // rows * rows
+    last_tiles = -(-(v - (v - 1) // chunk * chunk) // TILE)
+    parts = max(lce_dh_parts_bytes(r, d, kt) for r in (rows, last_rows) for kt in (chunk // TILE, last_tiles))
+    return rows * (chunk + G_PITCH_PAD) * 2 + (rows * d * 4 if nchunks > 1 else 0) + parts
 
 
 @dataclass(frozen=True)

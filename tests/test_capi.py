@@ -32,7 +32,9 @@ def test_library_exports_every_declared_symbol():
     assert lib.mtp_abi_version() == _native.ABI_VERSION == 2
 
 
-@pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1)])
+@pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1),
+                                           (8192, 5120, 152064), (2048, 4096, 151936), (8192, 1536, 151936),
+                                           (12288, 4096, 32000), (4352, 3584, 152064), (1000, 2048, 8000)])
 def test_plans_agree_with_python_planner(n, d, v):
     lib = _native.load()
     assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, 0) == plan.lce_fwd_workspace_bytes(n, v)

@@ -254,10 +254,11 @@ def test_transposed_head_cache_keeps_two_heads():
 
 
 @pytest.mark.parametrize(("n", "d", "v", "row_block", "head"), [(1000, 256, 3000, 256, "dense"), (700, 128, 2100, 512, "dense"),
-                                                                (600, 128, 1500, 256, "q4")])
+                                                                (600, 128, 1500, 256, "q4"), (1000, 512, 6000, 256, "q4")])
 def test_backward_row_blocks_match_all_rows(n, d, v, row_block, head):
     """mtp_lce_bwd in row blocks (one gradient buffer reused per block) gives dH bitwise equal to one
-    all-rows block: every G element and every dH tile is computed the same way either way."""
+    all-rows block: every G element and every dH tile is computed the same way either way (at these
+    shapes every block splits its dH contraction alike: not at all, or in 3 parts at 6000 columns)."""
     from mlx_train_perf import _native
 
     print(f"[lce bwd row blocks] n={n} d={d} v={v} row_block={row_block} head={head}", flush=True)
@@ -296,3 +297,75 @@ def test_backward_row_blocks_match_all_rows(n, d, v, row_block, head):
     _, olse, _ = olce.forward(h, wf, t, ignore_index=IGN)
     odh = olce.backward(h, wf, t, olse, ct.cpu(), ignore_index=IGN, dtype=torch.float64)
     assert rel_l2(outs[1], odh) <= 1e-2
+
+
+def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1):
+    """Forward then backward through the C-ABI (whole vocab in one chunk, all rows in one block);
+    with_wt passes the transposed (4-bit: dequantized) head made by mtp_lce_head_transpose."""
+    from mlx_train_perf import _native
+
+    lib = _native.load()
+    n, d = h.shape
+    v = w.shape[0]
+    if head == "dense":
+        kind, wd = _native.HEAD_DENSE, w.cuda()
+        ptrs, keep = (wd.data_ptr(), None, None, None), (wd,)
+    else:
+        kind = _native.HEAD_Q4
+        keep = tuple(x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))
+        ptrs = (None, keep[0].data_ptr(), keep[1].data_ptr(), keep[2].data_ptr())
+    hd, td = h.cuda(), t.cuda()
+    stream = torch.cuda.current_stream().cuda_stream
+    wt_ptr = None
+    if with_wt:
+        wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device="cuda")
+        _native.check(lib.mtp_lce_head_transpose(*ptrs, v, d, kind, wt.data_ptr(), stream), domain="loss")
+        keep, wt_ptr = keep + (wt,), wt.data_ptr()
+    fws = lib.mtp_lce_fwd_workspace_bytes(n, d, v, kind)
+    ws = torch.empty(fws, dtype=torch.uint8, device="cuda")
+    nll, lse, tgt = (torch.empty(n, device="cuda") for _ in range(3))
+    _native.check(lib.mtp_lce_fwd(hd.data_ptr(), *ptrs, td.data_ptr(), n, d, v, kind, IGN, nll.data_ptr(),
+                                  lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), fws, stream), domain="loss")
+    chunk = (v + 255) // 256 * 256
+    bws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, kind, chunk, 0)
+    bw = torch.empty(bws, dtype=torch.uint8, device="cuda")
+    ctd = ct.cuda()
+    w_ptr, wq_ptr, sc_ptr, bi_ptr = ptrs
+    outs = []
+    for _ in range(reps):
+        dh = torch.full((n, d), 7.0, dtype=torch.bfloat16, device="cuda")
+        _native.check(lib.mtp_lce_bwd(hd.data_ptr(), w_ptr, wt_ptr, wq_ptr, sc_ptr, bi_ptr, td.data_ptr(), n, d, v,
+                                      kind, IGN, lse.data_ptr(), ctd.data_ptr(), dh.data_ptr(), None, chunk, 0,
+                                      bw.data_ptr(), bws, stream), domain="loss")
+        torch.cuda.synchronize()
+        outs.append(dh.cpu())
+    wf = w if head == "dense" else oquant.dequantize_affine(*(x.cpu() for x in keep[:3]), dtype=torch.float32)
+    return outs, wf
+
+
+# (n, d, v, head, with_wt): 4 x 8 row/column tiles take the XCD block order (4 x 8 blocks of one
+# part, half the last round padding); 2 x 2 and 2 x 1 tiles the row-major order; n = 1000 and
+# v = 8000 leave partial last row and vocab tiles; d = 200 (not a multiple of 64) runs the
+# register-staged operand path, the 4-bit head without its transposed copy the in-kernel dequant.
+@pytest.mark.parametrize(("n", "d", "v", "head", "with_wt"), [(1000, 2048, 8000, "dense", True),
+                                                               (1000, 2048, 8000, "dense", False),
+                                                               (1024, 2048, 5000, "q4", True),
+                                                               (1000, 512, 6000, "q4", False),
+                                                               (300, 200, 5000, "dense", False)])
+def test_backward_split_contraction(n, d, v, head, with_wt):
+    """The dH contraction split over vocab ranges (fp32 part tiles summed in part order by a second
+    kernel) matches the oracle and repeats bitwise."""
+    from mlx_train_perf.plan import launch as plan
+
+    ks = plan.lce_dh_ksplit(n, d, (v + 255) // 256)
+    print(f"[lce bwd split] n={n} d={d} v={v} head={head} with_wt={with_wt} parts={ks}", flush=True)
+    assert ks > 1
+    h, w, t = lce_inputs(n, d, v, seed=n + d + v, w_std=0.05 if head == "q4" else 0.02)
+    ct = _cotangent(t)
+    outs, wf = _capi_backward(h, w, t, ct, head=head, with_wt=with_wt, reps=2)
+    assert torch.equal(outs[0], outs[1])
+    _, olse, _ = olce.forward(h, wf, t, ignore_index=IGN)
+    odh = olce.backward(h, wf, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(outs[0], odh) <= 1e-2
+    assert (outs[0].double() - odh).abs().max() <= 5e-3
+    assert (outs[0][t == IGN] == 0).all()

@@ -34,6 +34,49 @@ def test_lce_forward_splits(n, v):
     assert plan.lce_fwd_workspace_bytes(n, v) == 8 * ns * n
 
 
+def test_lce_splits_fill_whole_rounds():
+    """Persistent-launch splits: a split count that just overflows one resident round (48 row tiles x
+    6 splits = 288 workgroups on 256 CUs) is never chosen; the makespan (rounds x tiles per split)
+    is never worse than the rule "about one workgroup per CU, rounded up to a multiple of 8"."""
+    def makespan(rt, vt, ns):
+        return -(-(rt * ns) // 256) * -(-vt // ns)
+
+    assert plan.lce_fwd_splits(12288, 32000) == 5          # 240 workgroups, one round of 25 tiles
+    assert plan.lce_fwd_splits(12288, 151936) == 16        # 3 rounds of 38 tiles, not 2 x 99
+    assert plan.lce_fwd_splits(16384, 128256) == 4
+    for n in (256, 1000, 2048, 4096, 8192, 12288, 16384, 65536):
+        for v in (1024, 32000, 128256, 151936, 262144):
+            rt, vt = -(-n // 256), -(-v // 256)
+            ns = plan.lce_fwd_splits(n, v)
+            old = -(-256 // rt)
+            old = min(-(-old // 8) * 8 if old >= 8 else old, vt)
+            assert makespan(rt, vt, ns) <= makespan(rt, vt, max(old, 1)), (n, v)
+
+
+def test_lce_dh_split_fills_rounds():
+    """The dH contraction is split only when its output tiles leave the last resident round part
+    empty: 16 x 16 tiles (the flagship's 4096-row blocks) and any multiple of 256 tiles stay whole;
+    16 x 20 tiles (D = 5120) take 4 parts (5 rounds of a quarter of the vocab instead of 2 whole
+    rounds), 8 x 16 (N = 2048) take 2; parts never exceed 8 or leave fewer than 8 k tiles each."""
+    assert plan.lce_dh_ksplit(4096, 4096, 594) == 1
+    assert plan.lce_dh_ksplit(8192, 8192, 594) == 1
+    assert plan.lce_dh_ksplit(4096, 5120, 594) == 4
+    assert plan.lce_dh_ksplit(2048, 4096, 594) == 2
+    assert plan.lce_dh_ksplit(8192, 896, 594) == 2
+    assert plan.lce_dh_ksplit(64, 64, 15) == 1
+    for rows in (256, 1000, 4096, 8192):
+        for d in (64, 896, 2048, 4096, 5120):
+            for kt in (1, 7, 16, 100, 594):
+                ks = plan.lce_dh_ksplit(rows, d, kt)
+                assert 1 <= ks <= 8 and (ks == 1 or kt >= 8 * ks)
+                tiles = -(-rows // 256) * -(-d // 256)
+                # a split never adds resident rounds of whole-vocab work
+                assert -(-(tiles * ks) // 256) * -(-kt // ks) <= -(-tiles // 256) * kt
+    # the workspace adds the fp32 part tiles only when the product is split
+    assert plan.lce_dh_parts_bytes(4096, 4096, 594) == 0
+    assert plan.lce_dh_parts_bytes(4096, 5120, 594) == 4 * 320 * 256 * 256 * 4
+
+
 def test_flagship_forward_workspace_under_10mb():
     p = plan.lce_plan(n=8192, v=151936, d=4096)
     assert p.fwd_workspace_bytes + 3 * 8192 * 4 < 0.01e9
