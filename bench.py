@@ -632,7 +632,7 @@ def pmc_summary(command: str, *dirs: str) -> str:
     algorithmic_bytes = {   # bytes that must cross HBM at least once per launch
         "lce_fwd_kernel<0>": 2.0 * (V * D + N * D),
         "lce_fwd_kernel<1>": 0.5 * V * D + 4.0 * V * D / 64 + 2.0 * N * D,
-        "attn_kv128_kernel<false, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
+        "attn_kv_kernel<128, false, false>": 2.0 * (32 + 2 * 8) * 8192 * 128 + 4.0 * 32 * 8192 + 2.0 * 32 * 8192 * 128,
     }
     kernels = {}
     for k in sorted(merged):
