@@ -1003,6 +1003,46 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   }
 }
 
+// H_t . W_y as an fp32 dot product over the wave (every lane returns the total). A 4-bit row is
+// dequantized in fp32; with RB each weight is first rounded to bf16, as in the product tiles.
+template <int Q4, bool RB>
+__device__ __forceinline__ float row_dot(const bf16_t* __restrict__ h, const bf16_t* __restrict__ W,
+                                         const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
+                                         const bf16_t* __restrict__ Bi, long long y, int D, int lane) {
+  float dot = 0.f;
+  if constexpr (Q4) {
+    const uint32_t* q = Wq + y * (D >> 3);
+    const bf16_t* sc = Sc + y * (D >> 6);
+    const bf16_t* bi = Bi + y * (D >> 6);
+    auto rb = [](float x) { return RB ? (float)(__bf16)x : x; };
+    for (int wd = lane; wd < (D >> 3); wd += 64) {
+      const u32x4 hv = *reinterpret_cast<const u32x4*>(h + 8 * wd);
+      const uint32_t qq = q[wd];
+      const float s = bf16_to_f32(sc[wd >> 3]);
+      const float b = bf16_to_f32(bi[wd >> 3]);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const float w0 = rb(__builtin_fmaf(s, (float)((qq >> (8 * p)) & 0xFu), b));
+        const float w1 = rb(__builtin_fmaf(s, (float)((qq >> (8 * p + 4)) & 0xFu), b));
+        dot = __builtin_fmaf(bf16lo(hv[p]), w0, dot);
+        dot = __builtin_fmaf(bf16hi(hv[p]), w1, dot);
+      }
+    }
+  } else {
+    const bf16_t* wr = W + y * D;
+    for (int c = lane; c < (D >> 3); c += 64) {
+      const u32x4 hv = *reinterpret_cast<const u32x4*>(h + 8 * c);
+      const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + 8 * c);
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        dot = __builtin_fmaf(bf16lo(hv[p]), bf16lo(wv[p]), dot);
+        dot = __builtin_fmaf(bf16hi(hv[p]), bf16hi(wv[p]), dot);
+      }
+    }
+  }
+  return wave_sum(dot);
+}
+
 // Per token: merge the vocab-split partials into lse, compute the target logit as an fp32 dot
 // product H_t . W_{y_t}, and apply the ignore_index contract (ignored rows: nll = 0, tgt = 0).
 // One wave per token.
@@ -1027,39 +1067,7 @@ __global__ __launch_bounds__(256) void lce_fwd_finalize_kernel(
   const bool ignored = (y == ignore_index);
   const bool inrange = (y >= 0) && (y < (long long)V);
   float dot = 0.f;
-  if (!ignored && inrange) {
-    const bf16_t* h = H + (long)t * D;
-    if constexpr (Q4) {
-      const uint32_t* q = Wq + (long)y * (D >> 3);
-      const bf16_t* sc = Sc + (long)y * (D >> 6);
-      const bf16_t* bi = Bi + (long)y * (D >> 6);
-      for (int wd = lane; wd < (D >> 3); wd += 64) {
-        const u32x4 hv = *reinterpret_cast<const u32x4*>(h + 8 * wd);
-        const uint32_t qq = q[wd];
-        const float s = bf16_to_f32(sc[wd >> 3]);
-        const float b = bf16_to_f32(bi[wd >> 3]);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const float w0 = __builtin_fmaf(s, (float)((qq >> (8 * p)) & 0xFu), b);
-          const float w1 = __builtin_fmaf(s, (float)((qq >> (8 * p + 4)) & 0xFu), b);
-          dot = __builtin_fmaf(bf16lo(hv[p]), w0, dot);
-          dot = __builtin_fmaf(bf16hi(hv[p]), w1, dot);
-        }
-      }
-    } else {
-      const bf16_t* wr = W + (long)y * D;
-      for (int c = lane; c < (D >> 3); c += 64) {
-        const u32x4 hv = *reinterpret_cast<const u32x4*>(h + 8 * c);
-        const u32x4 wv = *reinterpret_cast<const u32x4*>(wr + 8 * c);
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          dot = __builtin_fmaf(bf16lo(hv[p]), bf16lo(wv[p]), dot);
-          dot = __builtin_fmaf(bf16hi(hv[p]), bf16hi(wv[p]), dot);
-        }
-      }
-    }
-    dot = wave_sum(dot);
-  }
+  if (!ignored && inrange) dot = row_dot<Q4, false>(H + (long)t * D, W, Wq, Sc, Bi, y, D, lane);
   if (lane == 0) {
     lse[t] = l;
     tgt[t] = (ignored || !inrange) ? 0.f : dot;
@@ -1154,7 +1162,8 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
 }
 
 // ------------------------------------------------------------------------------------------
-// Backward step 1, persistent form (hidden dim a multiple of 64). Workgroup (row tile, vocab
+// Backward step 1, persistent form (hidden dim a multiple of 64), without the one-hot term and
+// the zero padding columns (see lce_bwd_g_fix_kernel). Workgroup (row tile, vocab
 // split) walks its split's vocab tiles of the chunk back to back on the DMA core, in the
 // forward's XCD-grouped order; the next tile's first two stages are issued during the current
 // tile's last k-step. Each lane stores its G values straight from the accumulator layout (8-byte
@@ -1200,10 +1209,9 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
   const int vlim = v_end < V ? v_end : V;
   const int colb = 128 * wa + 4 * lhalf;  // this lane's first G column within a tile
 
-  // Per-thread token rows (fixed for the workgroup): coefficient, log2-domain lse, the target's
-  // column within the chunk (-1 when outside it or ignored) and the row's G byte offset.
+  // Per-thread token rows (fixed for the workgroup): coefficient, log2-domain lse and the row's G
+  // byte offset.
   float coef[kNJ], l2[kNJ];
-  int yrel[kNJ];
   uint32_t gvo[kNJ];
 #pragma unroll
   for (int j = 0; j < kNJ; ++j) {
@@ -1211,14 +1219,10 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
     const int t = t0 + r;
     coef[j] = 0.f;
     l2[j] = 0.f;
-    yrel[j] = -1;
     gvo[j] = 2u * (uint32_t)(r * ldg + colb);
     if (t < N) {
-      const long long y = targets[t];
-      const bool ign = y == ignore_index;
-      coef[j] = ign ? 0.f : dnll[t];
+      coef[j] = targets[t] == ignore_index ? 0.f : dnll[t];
       l2[j] = lse[t] * kLog2e;
-      yrel[j] = (!ign && y >= v_begin && y < vlim) ? (int)(y - v_begin) : -1;
     }
   }
   // G rows of this row tile; stores to rows past N fall outside the range and are dropped.
@@ -1279,30 +1283,50 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
     }
     pre = has_next;
 
-    // G = bf16((exp(z - lse) - onehot) * coef), zero in columns past the chunk's last vocab row.
-    // Tile column of acc[i][j][4q + u] is colb + 32 i + 8 q + u.
+    // G = bf16(exp(z - lse) coef): an fma, an exp and a multiply per element. The one-hot term of
+    // each row's target column and the zeros of the columns past the chunk's last vocab row (the
+    // chunk's last tile only; their head rows are clamped copies of a valid row, so these values
+    // are finite) are written afterwards by lce_bwd_g_fix_kernel. Tile column of acc[i][j][4q + u]
+    // is colb + 32 i + 8 q + u.
     const int tl = v0 - v_begin;
-    const int lim = vlim - v0 - colb;
 #pragma unroll
-    for (int j = 0; j < kNJ; ++j) {
-      const int yd = yrel[j] - tl - colb;
+    for (int j = 0; j < kNJ; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           float gv[4];
 #pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const int idx = 32 * i + 8 * q + u;
-            // Branch-free: the columns past the chunk multiply a finite p (their head rows are
-            // clamped copies of a valid row) by zero.
-            const float p = fast_exp2(acc[i][j][4 * q + u] * kLog2e - l2[j]) - (idx == yd ? 1.f : 0.f);
-            gv[u] = p * (idx < lim ? coef[j] : 0.f);
-          }
+          for (int u = 0; u < 4; ++u) gv[u] = fast_exp2(acc[i][j][4 * q + u] * kLog2e - l2[j]) * coef[j];
           const u32x2 val = u32x2{pack_bf16x2(gv[0], gv[1]), pack_bf16x2(gv[2], gv[3])};
           __builtin_amdgcn_raw_buffer_store_b64(val, gr, gvo[j] + 64 * i + 16 * q, 2 * tl, 0);
         }
-    }
+  }
+}
+
+// Backward step 1b (after lce_bwd_g_persist_kernel), one wave per row of the chunk's G:
+//  * columns [vlim - v_begin, kc) past the chunk's last vocab row (kc = the padded chunk width)
+//    are set to zero;
+//  * a row whose target lies in the chunk gets G[t][y_t - v_begin] = bf16((exp(z - lse) - 1) coef),
+//    z = H_t . W_{y_t} as an fp32 dot product (4-bit weights rounded to bf16, as in the product
+//    tiles), overwriting the bf16(exp(z - lse) coef) the persistent kernel stored there.
+template <int Q4>
+__global__ __launch_bounds__(256) void lce_bwd_g_fix_kernel(
+    const bf16_t* __restrict__ H, const bf16_t* __restrict__ W, const uint32_t* __restrict__ Wq,
+    const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
+    const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index, int N, int D, int V,
+    int v_begin, int v_end, int kc, int ldg, bf16_t* __restrict__ G) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;
+  const int vlim = v_end < V ? v_end : V;
+  for (int c = vlim - v_begin + lane; c < kc; c += 64) G[(long)t * ldg + c] = 0;
+  const long long y = targets[t];
+  if (y == ignore_index || y < v_begin || y >= vlim) return;
+  const float z = row_dot<Q4, true>(H + (long)t * D, W, Wq, Sc, Bi, y, D, lane);
+  if (lane == 0) {
+    const float p = fast_exp2(z * kLog2e - lse[t] * kLog2e) - 1.f;
+    G[(long)t * ldg + (y - v_begin)] = __builtin_bit_cast(bf16_t, (__bf16)(p * dnll[t]));
   }
 }
 
@@ -1727,6 +1751,16 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
       } else {
         hipLaunchKernelGGL(lce_bwd_g_persist_kernel<0>, pgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
                            lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, Gbuf);
+      }
+      hipError_t pe = hipGetLastError();
+      if (pe != hipSuccess) return pe;
+      dim3 tgrid((N + 3) / 4), tblock(256);
+      if (h.q4) {
+        hipLaunchKernelGGL(lce_bwd_g_fix_kernel<1>, tgrid, tblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, Gbuf);
+      } else {
+        hipLaunchKernelGGL(lce_bwd_g_fix_kernel<0>, tgrid, tblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, Gbuf);
       }
     } else {
       dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
