@@ -14,9 +14,9 @@
 //
 // All GEMM-shaped work uses one 256x256 workgroup tile: 8 waves (2 per SIMD), each a 128x64
 // sub-tile of 4x2 MFMA 32x32x16 blocks, BK = 64, two LDS stages of 64 KiB. The hot path feeds the
-// stages by direct global->LDS copies (gemm_dma); the register-staged core (gemm_256x256) serves
-// the 4-bit head, whose rows are dequantized in registers, and shapes whose contraction length is
-// not a multiple of 64.
+// stages by direct global->LDS copies (gemm_dma), the 4-bit head's tiles by dequantization in
+// registers between the MFMAs (RegQ4Op, RegQ4TransOp); the register-staged core (gemm_256x256)
+// serves dense shapes whose contraction length is not a multiple of 64.
 #include <type_traits>
 
 #include "mtp_common.hpp"
@@ -119,55 +119,6 @@ struct TransLoader {
     if (tid >= 256) return;
     const int vb = tid >> 5, db = tid & 31;
     u32x4 y[8];
-    transpose8x8(x, y);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) lds_write16(lds, lds_off(8 * db + j, vb), y[j]);
-  }
-};
-
-// Transposed 4-bit operand for G . W_q: rows of the tile are columns d, the contraction runs over
-// the quantized rows v. Each thread dequantizes an 8 (v) x 8 (d) block (one word per row) and
-// transposes it in registers.
-struct Q4TransLoader {
-  const uint32_t* wq;   // row k=0 of the chunk
-  const bf16_t* sc;
-  const bf16_t* bi;
-  int D;
-  int d0;
-  int kvalid;
-  int dvalid;
-  uint32_t q[8];
-  float s[8], b[8];
-
-  template <bool FULL>
-  __device__ __forceinline__ void load(int kt) {
-    const int tid = threadIdx.x;
-    const int vb = tid >> 5, db = tid & 31;
-    const int d = 8 * db;
-    const int word = (d0 + d) >> 3;
-    const int grp = (d0 + d) >> 6;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int k = kt * kBK + 8 * vb + i;
-      if (tid < 256 && (FULL || (k < kvalid && d < dvalid))) {
-        q[i] = wq[(long)k * (D >> 3) + word];
-        const long g = (long)k * (D >> 6) + grp;
-        s[i] = bf16_to_f32(sc[g]);
-        b[i] = bf16_to_f32(bi[g]);
-      } else {
-        q[i] = 0u;
-        s[i] = 0.f;
-        b[i] = 0.f;
-      }
-    }
-  }
-  __device__ __forceinline__ void store(char* lds) const {
-    const int tid = threadIdx.x;
-    if (tid >= 256) return;
-    const int vb = tid >> 5, db = tid & 31;
-    u32x4 x[8], y[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) x[i] = dequant8(q[i], s[i], b[i]);
     transpose8x8(x, y);
 #pragma unroll
     for (int j = 0; j < 8; ++j) lds_write16(lds, lds_off(8 * db + j, vb), y[j]);
@@ -352,8 +303,34 @@ struct DmaRowOp : RowFrags {
 // lane s reads 4 columns of k-row (s >> 2) and receives 4 consecutive k of one column, so the
 // pair yields the 8 consecutive k an MFMA operand lane needs. k-rows at or past kvalid re-read
 // row kvalid - 1; columns at or past ncols re-read the last 8 columns.
-struct DmaTransOp {
+// Fragment reads of a transposed operand tile: 64 k-rows of 512 B (256 columns), the 16-byte chunk
+// of columns 8 s .. 8 s + 7 of k-row k at chunk position s ^ 4 (k & 3); each fragment is two
+// ds_read_b64_tr_b16 (8 consecutive k of one column).
+struct TransFrags {
   static constexpr int kReads = 2;
+  int lo[4];           // per-lane fragment offsets (per 32-column block)
+
+  template <int NB>
+  __device__ __forceinline__ void setup(int first_col) {
+    const int l = threadIdx.x & 63;
+    const int kl = 8 * (l >> 5) + ((l >> 2) & 3);
+    const int kr = (l >> 2) & 3;
+    const int low = 2 * ((l >> 4) & 1) + ((l & 3) >> 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int jb = (first_col >> 5) + b;
+      lo[b] = kl * 512 + (((4 * jb) ^ (4 * kr)) + low) * 16 + 8 * (l & 1);
+    }
+  }
+  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
+    const lds_bf16x4* p = (const lds_bf16x4*)(st + lo[b] + ks * 16 * 512);
+    const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
+    const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
+    return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+  }
+};
+
+struct DmaTransOp : TransFrags {
   static constexpr bool kInline = false;
   static constexpr bool kPartner = false;  // issue2 is never selected (kept so that calls compile)
   const char* base;    // k = 0, column 0 of the tile
@@ -361,7 +338,6 @@ struct DmaTransOp {
   int kvalid;
   int rk[4];           // per-lane k-row (within a stage) of the four copies
   uint32_t cofs[4];    // per-lane column byte offsets
-  int lo[4];           // per-lane fragment offsets (per 32-column block)
 
   __device__ __forceinline__ void init(const bf16_t* b, int ld, int kvalid_, int ncols) {
     base = reinterpret_cast<const char*>(b);
@@ -390,48 +366,59 @@ struct DmaTransOp {
     }
   }
   __device__ __forceinline__ void issue2(int kt, char* dst, int, bool live = true) const { issue(kt, dst, live); }
-  template <int NB>
-  __device__ __forceinline__ void setup(int first_col) {
-    const int l = threadIdx.x & 63;
-    const int kl = 8 * (l >> 5) + ((l >> 2) & 3);
-    const int kr = (l >> 2) & 3;
-    const int low = 2 * ((l >> 4) & 1) + ((l & 3) >> 1);
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      const int jb = (first_col >> 5) + b;
-      lo[b] = kl * 512 + (((4 * jb) ^ (4 * kr)) + low) * 16 + 8 * (l & 1);
-    }
-  }
-  __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
-    const lds_bf16x4* p = (const lds_bf16x4*)(st + lo[b] + ks * 16 * 512);
-    const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-    const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
-    return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
-  }
 };
 
-// 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16), dequantized
-// in registers. Thread t owns half a tile row: row t >> 1, k 32 (t & 1) .. +31 of each 64-deep slab,
-// i.e. 4 packed words, which it loads straight into registers one stage ahead (`qn`). While the
-// MFMAs of stage kt run it dequantizes slab kt + 1 (`qc`), bf16(scale * q + bias) in fp32, into
-// the next stage's A tile, one 16-byte LDS write per word in the row layout that RowFrags reads.
-// The scales and biases go through LDS: the copier threads (waves 0-3, thread t for row t) load
-// those of slab kt + 2 during stage kt and store them packed (scale | bias << 16) into a two-slot
-// ring before the barrier; after it every thread reads its row's pair. So the non-copier waves
+// Register state shared by the two 4-bit operands below. Each thread owns 4 packed words (32
+// values) of every 64-deep stage, loaded straight into registers one stage ahead (`qn`); while the
+// MFMAs of stage kt run it dequantizes stage kt + 1 (`qc`), bf16(scale * q + bias) in fp32, into the
+// next stage's tile, one 16-byte LDS write per word (word c at LDS offset wo ^ (c << 4)). The 4 words
+// share one (scale, bias) pair, which goes through LDS: the copier threads (waves 0-3, thread c)
+// load pair c of stage kt + 2 during stage kt and store it packed (scale | bias << 16) into a
+// two-slot ring before the barrier; after it thread t reads pair t >> 1. So the non-copier waves
 // issue one vector-memory load per stage.
 constexpr int kQ4SbBytes = 2 * 256 * 4;  // the scale/bias ring, after the four operand tiles
-struct RegQ4Op : RowFrags {
+struct Q4Regs {
   static constexpr bool kInline = true;
   static constexpr bool kPartner = true;  // no copies of its own
-  __amdgpu_buffer_rsrc_t rq, rs, rb;      // packed words, scales, biases of the tile's rows
-  uint32_t qo;                            // this thread's byte offset in the packed words
-  uint32_t so;                            // copier thread t: byte offset of row t's scale and bias
-  uint32_t wo;                            // LDS byte offset of its first 16-byte chunk (word 0)
-  int last;                               // index of the last slab
-  char* ring;                             // the scale/bias ring (2 slots x 256 rows x 4 B)
+  __amdgpu_buffer_rsrc_t rq, rs, rb;      // packed words, scales, biases
+  uint32_t wo;                            // LDS byte offset of this thread's word 0
+  char* ring;                             // the scale/bias ring (2 slots x 256 pairs x 4 B)
   u32x4 qc, qn;
-  uint32_t sb;                            // packed raw scale and bias of the slab being dequantized
-  uint32_t s0, b0, s1, b1;                // copier threads: raw scale / bias of slabs in flight
+  uint32_t sb;                            // packed raw scale and bias of the stage being dequantized
+  uint32_t s0, b0, s1, b1;                // copier threads: raw scale / bias of stages in flight
+
+  // Copier threads, once the loads have landed: store the pair of stage kt into its ring slot.
+  template <bool SECOND>
+  __device__ __forceinline__ void put_sb(int kt) const {
+    const uint32_t v = SECOND ? (s1 | (b1 << 16)) : (s0 | (b0 << 16));
+    *reinterpret_cast<uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x & 255)) = v;
+  }
+  // Every thread, after the barrier that follows put_sb(kt): its pair of stage kt.
+  __device__ __forceinline__ void get_sb(int kt) {
+    sb = *reinterpret_cast<const uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x >> 1));
+  }
+  // qc = qn where it stands: left to itself the compiler sinks the copy to the loop's top and puts
+  // a wait for the load before it there, after the next stage's copies, which it then waits for too.
+  __device__ __forceinline__ void shift() {
+    qc = qn;
+    asm volatile("" : "+v"(qc));
+  }
+  template <int C>
+  __device__ __forceinline__ void produce_word(char* stage) const {
+    lds_write16(stage, (int)(wo ^ (C << 4)), dequant8(qc[C], __uint_as_float(sb << 16), __uint_as_float(sb & 0xffff0000u)));
+  }
+  __device__ __forceinline__ void issue(int, char*, bool = true) const {}
+  __device__ __forceinline__ void issue2(int, char*, int, bool = true) const {}
+};
+
+// 4-bit rows (w_q [rows][K/8] u32, low nibble first; scales/biases [rows][K/64] bf16) as the
+// K-contiguous A operand (the head in the forward and the gradient tiles). Thread t owns half a tile
+// row: row t >> 1, k 32 (t & 1) .. +31 of each 64-deep slab, in the row layout RowFrags reads;
+// copier thread c loads the pair of row c.
+struct RegQ4Op : RowFrags, Q4Regs {
+  uint32_t qo;                            // this thread's byte offset in the packed words
+  uint32_t so;                            // copier thread c: byte offset of row c's scale and bias
+  int last;                               // index of the last slab
 
   __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D, int nrows,
                                        char* ring_) {
@@ -471,28 +458,66 @@ struct RegQ4Op : RowFrags {
       b0 = bv;
     }
   }
-  // Copier threads, once the loads have landed: store the pair of slab kt into its ring slot.
+};
+
+// 4-bit head as the transposed B operand of the dH product (G . W: the contraction runs over the
+// quantized rows v, the tile's 256 columns are hidden dims d). A packed word holds 8 consecutive d
+// of one row, i.e. 8 columns of one k-row, so it is dequantized straight into the transposed tile
+// layout that TransFrags reads (no register transpose). Thread t owns 4 consecutive words: k-row
+// t >> 3 of each 64-row stage, columns d0 + 32 (t & 7) .. +31 (one scale group); copier thread c
+// loads the pair of k-row c >> 2, column group c & 3, which is pair t >> 1 for thread t. Rows past
+// kvalid re-read the last valid row and columns past D the last 32 (their products only meet zero
+// G columns or land in dropped dH columns).
+struct RegQ4TransOp : TransFrags, Q4Regs {
+  uint32_t qcol;                          // byte offset of this thread's 4 words within a row
+  uint32_t scol;                          // copier thread c: byte offset of its pair within a row
+  uint32_t rowq, rows;                    // row pitch of the words and of the scales / biases
+  int krow, crow, last;                   // k-row of this thread, of its copier pair; last row
+
+  __device__ __forceinline__ void init(const uint32_t* wq, const bf16_t* sc_, const bf16_t* bi_, int D, int d0,
+                                       int kvalid, char* ring_) {
+    const int t = threadIdx.x, c = t & 255;
+    rq = dma_rsrc(reinterpret_cast<const char*>(wq), 4L * kvalid * (D >> 3));
+    rs = dma_rsrc(reinterpret_cast<const char*>(sc_), 2L * kvalid * (D >> 6));
+    rb = dma_rsrc(reinterpret_cast<const char*>(bi_), 2L * kvalid * (D >> 6));
+    rowq = 4u * (uint32_t)(D >> 3);
+    rows = 2u * (uint32_t)(D >> 6);
+    int dc = d0 + 32 * (t & 7);
+    if (dc > D - 32) dc = D - 32;
+    qcol = 4u * (uint32_t)(dc >> 3);
+    int dg = d0 + 64 * (c & 3);
+    if (dg > D - 64) dg = D - 64;
+    scol = 2u * (uint32_t)(dg >> 6);
+    krow = t >> 3;
+    crow = c >> 2;
+    last = kvalid - 1;
+    // column chunk 4 (t & 7) + c of k-row krow sits at position (4 (t & 7) + c) ^ 4 (krow & 3) =
+    // 4 ((t & 7) ^ (krow & 3)) + c.
+    wo = (uint32_t)(krow * 512 + ((4 * ((t & 7) ^ (krow & 3))) << 4));
+    ring = ring_;
+  }
+  template <bool CUR>
+  __device__ __forceinline__ void load_q(int kt) {
+    int r = 64 * kt + krow;
+    if (r > last) r = last;
+    const u32x4 q = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rq, (uint32_t)r * rowq + qcol, 0, 0));
+    if constexpr (CUR) qc = q; else qn = q;
+  }
   template <bool SECOND>
-  __device__ __forceinline__ void put_sb(int kt) const {
-    const uint32_t v = SECOND ? (s1 | (b1 << 16)) : (s0 | (b0 << 16));
-    *reinterpret_cast<uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x & 255)) = v;
+  __device__ __forceinline__ void load_sb(int kt) {
+    int r = 64 * kt + crow;
+    if (r > last) r = last;
+    const uint32_t o = (uint32_t)r * rows + scol;
+    const uint32_t sv = __builtin_amdgcn_raw_buffer_load_b16(rs, o, 0, 0);
+    const uint32_t bv = __builtin_amdgcn_raw_buffer_load_b16(rb, o, 0, 0);
+    if constexpr (SECOND) {
+      s1 = sv;
+      b1 = bv;
+    } else {
+      s0 = sv;
+      b0 = bv;
+    }
   }
-  // Every thread, after the barrier that follows put_sb(kt): its row's pair of slab kt.
-  __device__ __forceinline__ void get_sb(int kt) {
-    sb = *reinterpret_cast<const uint32_t*>(ring + ((kt & 1) << 10) + 4 * (threadIdx.x >> 1));
-  }
-  // qc = qn where it stands: left to itself the compiler sinks the copy to the loop's top and puts
-  // a wait for the load before it there, after the next stage's copies, which it then waits for too.
-  __device__ __forceinline__ void shift() {
-    qc = qn;
-    asm volatile("" : "+v"(qc));
-  }
-  template <int C>
-  __device__ __forceinline__ void produce_word(char* stage) const {
-    lds_write16(stage, (int)(wo ^ (C << 4)), dequant8(qc[C], __uint_as_float(sb << 16), __uint_as_float(sb & 0xffff0000u)));
-  }
-  __device__ __forceinline__ void issue(int, char*, bool = true) const {}
-  __device__ __forceinline__ void issue2(int, char*, int, bool = true) const {}
 };
 
 template <class OA, class OB>
@@ -580,12 +605,24 @@ __device__ __forceinline__ void dma_sched_copy() {
 // outstanding; the caller must barrier before writing LDS itself.
 // PRE_VM: VMEM operations the caller issued after the prefetched stages (only with `pre`); the
 // first wait leaves them in flight.
+// The operand of a gemm_dma call that is dequantized in registers (kInline), A or B.
+template <class OA, class OB>
+__device__ __forceinline__ auto& inline_op(OA& oa, OB& ob) {
+  if constexpr (OB::kInline) return ob;
+  else return oa;
+}
+
 template <int PRE_VM = 0, class OA, class OB, class NEXT>
 __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x16 (&acc)[4][kNJ], bool pre,
                                          bool has_next, const NEXT& next) {
   constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
   const int w = threadIdx.x >> 6;
   constexpr bool kCopiers = OA::kPartner && OB::kPartner;
+  // The 4-bit operand dequantized in registers (at most one; its tile is A or B of each stage).
+  constexpr bool kQ = OA::kInline || OB::kInline;
+  static_assert(!(OA::kInline && OB::kInline), "at most one inline operand");
+  constexpr int kQOff = OB::kInline ? 32768 : 0;
+  auto& q = inline_op(oa, ob);
   const int wsc = __builtin_amdgcn_readfirstlane(w);
   oa.template setup<4>(128 * (w & 1));
   ob.template setup<kNJ>(64 * (w >> 1));
@@ -597,12 +634,12 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
   if (!pre) {
-    if constexpr (OA::kInline) {
-      oa.template load_q<true>(0);
-      oa.template load_q<false>(1);
+    if constexpr (kQ) {
+      q.template load_q<true>(0);
+      q.template load_q<false>(1);
       if (wsc < 4) {
-        oa.template load_sb<false>(0);
-        oa.template load_sb<true>(1);
+        q.template load_sb<false>(0);
+        q.template load_sb<true>(1);
       }
     }
     oa.issue(0, lds);
@@ -612,26 +649,26 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       ob.issue(1, lds + kDmaStage + 32768);
     }
   }
-  if constexpr (OA::kInline) {
-    // Stage 0's A tile is dequantized here, with nothing to overlap; each later one during the
-    // k-steps of the stage before it.
+  if constexpr (kQ) {
+    // Stage 0's 4-bit tile is dequantized here, with nothing to overlap; each later one during
+    // the k-steps of the stage before it.
     if (pre) wait_vmcnt<PRE_VM>(); else wait_vmcnt<0>();
     if (wsc < 4) {
-      oa.template put_sb<false>(0);
-      oa.template put_sb<true>(1);
+      q.template put_sb<false>(0);
+      q.template put_sb<true>(1);
     }
     wait_lgkmcnt0();
     raw_barrier();
-    oa.get_sb(0);
-    oa.template produce_word<0>(lds);
-    oa.template produce_word<1>(lds);
-    oa.template produce_word<2>(lds);
-    oa.template produce_word<3>(lds);
-    oa.get_sb(1);
-    oa.shift();
+    q.get_sb(0);
+    q.template produce_word<0>(lds + kQOff);
+    q.template produce_word<1>(lds + kQOff);
+    q.template produce_word<2>(lds + kQOff);
+    q.template produce_word<3>(lds + kQOff);
+    q.get_sb(1);
+    q.shift();
     // Slab 2: the stage loop loads slab kt + 3 after its barrier, ahead of the copies.
-    oa.template load_q<false>(2);
-    if (wsc < 4) oa.template load_sb<false>(2);
+    q.template load_q<false>(2);
+    if (wsc < 4) q.template load_sb<false>(2);
     wait_lgkmcnt0();
   } else {
     if (pre) wait_vmcnt<PRE_VM>();
@@ -653,21 +690,21 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     for (int kt = 0; kt + 1 < nk; ++kt) {
       char* cur = lds + ((kt & 1) ? kDmaStage : 0);
       char* nxt = lds + ((kt & 1) ? 0 : kDmaStage);
-      if constexpr (OA::kInline) {
-        // 4-bit A: dequantize slab kt + 1 (qc) into the next stage's A tile (free since the last
-        // barrier) between this stage's MFMAs.
+      if constexpr (kQ) {
+        // 4-bit operand: dequantize slab kt + 1 (qc) into the next stage's tile (free since the
+        // last barrier) between this stage's MFMAs.
         dma_read_frags(oa, ob, cur, 1, ga, gb);
         dma_mfma(fa, fb, acc);
-        oa.template produce_word<0>(nxt);
-        oa.template produce_word<1>(nxt);
+        q.template produce_word<0>(nxt + kQOff);
+        q.template produce_word<1>(nxt + kQOff);
         dma_sched_q4<NR, 2>();
         dma_read_frags(oa, ob, cur, 2, fa, fb);
         dma_mfma(ga, gb, acc);
-        oa.template produce_word<2>(nxt);
+        q.template produce_word<2>(nxt + kQOff);
         dma_sched_q4<NR, 1>();
         dma_read_frags(oa, ob, cur, 3, ga, gb);
         dma_mfma(fa, fb, acc);
-        oa.template produce_word<3>(nxt);
+        q.template produce_word<3>(nxt + kQOff);
         dma_sched_q4<NR, 1>();
       } else {
         dma_read_frags(oa, ob, cur, 1, ga, gb);
@@ -682,20 +719,20 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       }
       wait_lgkmcnt0();
       wait_vmcnt<0>();
-      if constexpr (OA::kInline) {
-        oa.shift();
+      if constexpr (kQ) {
+        q.shift();
         if constexpr (R != 2) {
-          oa.template put_sb<false>(kt + 2);
+          q.template put_sb<false>(kt + 2);
           wait_lgkmcnt0();
         }
       }
       raw_barrier();
-      if constexpr (OA::kInline) {
+      if constexpr (kQ) {
         // Slab kt + 3 (the copiers: also its scales and biases), issued before the stage's copies
         // so that it does not queue behind them; it has until the next barrier to land.
-        oa.get_sb(kt + 2);
-        oa.template load_q<false>(kt + 3);
-        if constexpr (R != 2) oa.template load_sb<false>(kt + 3);
+        q.get_sb(kt + 2);
+        q.template load_q<false>(kt + 3);
+        if constexpr (R != 2) q.template load_sb<false>(kt + 3);
       }
       const bool live = kt + 2 < nk;
       if constexpr (R == 0) {
@@ -1372,7 +1409,7 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
                        const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, int N, int D, int V,
                        int v_begin, int v_end, float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode,
                        int ksplit, int split_a, float* __restrict__ parts) {
-  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + kQ4SbBytes : kLdsBytes];
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
   int rt, dt, part = 0;
@@ -1409,31 +1446,30 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
     DmaRowOp ob;
     ob.init(Wt + (long)d0 * ldt + vb, ldt, D - d0);
     gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
-  } else if (!Q4 && D % kBK == 0) {
-    // G columns past the chunk's last vocab row are zeros, so the W rows they meet only need to
-    // be readable (kvalid clamps them to the last row of W).
+  } else if (D % kBK == 0) {
+    // G columns past the chunk's last vocab row are zeros, so the head rows they meet only need
+    // to be readable (rows past the valid range re-read the last valid one).
     DmaRowOp oa;
     oa.init(G + (long)t0 * ldg + koff, ldg, N - t0);
-    DmaTransOp ob;
-    ob.init(W + (long)vb * D + d0, D, V - vb, D - d0);
-    gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
-  } else {
+    if constexpr (Q4) {
+      // The 4-bit head, dequantized in registers into the transposed tile (no bf16 copy).
+      RegQ4TransOp ob;
+      ob.init(Wq + (long)vb * (D >> 3), Sc + (long)vb * (D >> 6), Bi + (long)vb * (D >> 6), D, d0, vlim - vb,
+              lds + kLdsBytes);
+      gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+    } else {
+      DmaTransOp ob;
+      ob.init(W + (long)vb * D + d0, D, V - vb, D - d0);
+      gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
+    }
+  } else if constexpr (!Q4) {
+    // Dense heads whose hidden dim is not a multiple of 64 (a 4-bit head's always is).
     RowKLoader la;
     la.base = G + (long)t0 * ldg + koff;
     la.ld = ldg;
     la.nrows = N - t0;
     la.K = kc;
-    if constexpr (Q4) {
-      Q4TransLoader lb;
-      lb.wq = Wq + (long)vb * (D >> 3);
-      lb.sc = Sc + (long)vb * (D >> 6);
-      lb.bi = Bi + (long)vb * (D >> 6);
-      lb.D = D;
-      lb.d0 = d0;
-      lb.kvalid = vlim - vb;
-      lb.dvalid = D - d0;
-      if (full) gemm_256x256<true>(la, lb, nk, lds, acc); else gemm_256x256<false>(la, lb, nk, lds, acc);
-    } else {
+    {
       TransLoader lb;
       lb.w = W + (long)vb * D + d0;
       lb.ld = D;
