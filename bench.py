@@ -779,6 +779,20 @@ def main():
         q4 = bench_lce(max(3, args.steps // 4), 1, "q4")
         result["qlora_lce"] = {**q4, "tokens_per_s": N / q4["sec_per_step"],
                                "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
+        # The same step without the cached bf16 transposed head (the dH product dequantizes the 4-bit
+        # head in registers as well): the memory / time trade of MTP_LCE_TRANSPOSED_HEAD=0.
+        from mlx_train_perf.core import loss as L
+        os.environ["MTP_LCE_TRANSPOSED_HEAD"] = "0"
+        try:
+            L.clear_transposed_head_cache()
+            torch.cuda.empty_cache()
+            q4n = bench_lce(3, 1, "q4")
+        finally:
+            del os.environ["MTP_LCE_TRANSPOSED_HEAD"]
+        result["qlora_lce"]["no_head_copy"] = {
+            "ms_per_step": q4n["sec_per_step"] * 1e3, "tokens_per_s": N / q4n["sec_per_step"],
+            "bwd_ms": q4n["bwd_ms"], "bwd_marginal_peak_gb": q4n["bwd_marginal_peak_gb"],
+            "bwd_footprint_gb": q4n["bwd_footprint_gb"]}
     if not args.no_extras and "attention" in parts:
         torch.cuda.empty_cache()
         result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, "causal")
