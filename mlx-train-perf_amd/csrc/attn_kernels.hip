@@ -188,7 +188,7 @@ void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
                                const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
                                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
                                float scale_log2, float scale, int causal, int nsplit,
-                               float* __restrict__ part) {
+                               float* __restrict__ part, const int32_t* __restrict__ order) {
   using L = kvdma::Lay<DH>;
   constexpr int kRowB = L::kRowB, kTile = L::kTile;
   auto sw = [](int r) { return L::sw(r); };
@@ -203,13 +203,25 @@ void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   const int G = Hq / Hkv;
   const int nkv = B * Hkv;
   // Block g: split g % nsplit of key block (g / nsplit) / nkv of kv head (g / nsplit) % nkv; the
-  // earliest keys (most work under the causal mask) first.
+  // earliest keys (most work under the causal mask) first. Packed, with a work order: item
+  // order[g / (nsplit Hkv)] (batch row item / nkb, key block item % nkb), heaviest first, with its
+  // Hkv heads and splits consecutive.
   const int g = blockIdx.x;
   const int split = g % nsplit;
-  const int kvi = (g / nsplit) % nkv;
-  const int ktile = (g / nsplit) / nkv;
-  const int bidx = kvi / Hkv;
-  const int kvh = kvi % Hkv;
+  int bidx, kvh, ktile;
+  if (PACKED && order != nullptr) {
+    const int nkb = (S + 127) / 128;
+    int item = order[g / (nsplit * Hkv)];
+    item = item < 0 ? 0 : (item < B * nkb ? item : B * nkb - 1);  // in range whatever the order holds
+    bidx = item / nkb;
+    ktile = item % nkb;
+    kvh = (g / nsplit) % Hkv;
+  } else {
+    const int kvi = (g / nsplit) % nkv;
+    ktile = (g / nsplit) / nkv;
+    bidx = kvi / Hkv;
+    kvh = kvi % Hkv;
+  }
   const int k0 = ktile * 128;
 
   const int tid = threadIdx.x;
@@ -562,7 +574,8 @@ void attn_kv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, 
                     const bf16_t* __restrict__ d_o, const bf16_t* __restrict__ o_in, const float* __restrict__ lse_in,
                     float* __restrict__ dvec, const int32_t* __restrict__ seg_id,
                     const int32_t* __restrict__ seg_start, bf16_t* __restrict__ out, float* __restrict__ lse_out,
-                    int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal) {
+                    int B, int Hq, int Hkv, int S, float scale_log2, float scale, int causal,
+                    const int32_t* __restrict__ order) {
   using L = kvdma::Lay<DH>;
   constexpr int kRowB = L::kRowB, kTile = L::kTile, kStage = L::kStage;
   auto sw = [](int r) { return L::sw(r); };
@@ -578,10 +591,21 @@ void attn_kv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, 
   const int hgb = Hq / hpw;
   const int nhg = B * hgb;
   const int g = blockIdx.x;
-  const int hg = g % nhg;
-  const int pb = npb - 1 - g / nhg;  // heaviest (latest) query blocks first
-  const int bidx = hg / hgb;
-  const int h0 = (hg % hgb) * hpw;
+  // Heaviest query blocks first: the latest under the causal mask; packed, with a work order, item
+  // order[g / hgb] (batch row item / npb, query block item % npb), its head groups consecutive.
+  int pb, bidx, h0;
+  if (PACKED && order != nullptr) {
+    int item = order[g / hgb];
+    item = item < 0 ? 0 : (item < B * npb ? item : B * npb - 1);  // in range whatever the order holds
+    bidx = item / npb;
+    pb = item % npb;
+    h0 = (g % hgb) * hpw;
+  } else {
+    const int hg = g % nhg;
+    pb = npb - 1 - g / nhg;
+    bidx = hg / hgb;
+    h0 = (hg % hgb) * hpw;
+  }
   const int kvh = h0 / G;
 
   const int tid = threadIdx.x;
@@ -1007,6 +1031,69 @@ void attn_kv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, 
 // block's items are then split over nsplit workgroups (1, 2, 4 or 8: the smallest that brings the
 // heaviest workgroup under the share), whose fp32 partials attn_dkv_reduce_kernel sums. At B = 1,
 // Hkv = 8 causal this gives 8 splits at S <= 1024, 4 at 2048, 2 at 4096 and 1 from 8192 on.
+// Longest-first work orders of a packed backward, one workgroup per order. Workgroup 0 orders the
+// B npb query blocks of the dQ pass (P queries each), workgroup 1 the B nkb 128-key blocks of the
+// dK/dV pass, by the tile counts their kernels' loops run (from seg_start, exactly as the kernels
+// bound them); order[r] is the item of rank r, most tiles first. A counting sort over kSchedBuckets
+// buckets of cost >> shift; items of one bucket land in any order, which changes only the schedule:
+// every item writes its own outputs.
+constexpr int kSchedBuckets = 2048;
+__global__ __launch_bounds__(1024) void attn_sched_kernel(const int32_t* __restrict__ seg_start, int B, int S, int P,
+                                                         int32_t* __restrict__ q_order, int32_t* __restrict__ kv_order) {
+  __shared__ int cnt[kSchedBuckets];
+  __shared__ int wsum[16];
+  const bool kv = blockIdx.x == 1;
+  const int nblk = kv ? (S + 127) / 128 : (S + P - 1) / P;
+  const int n = B * nblk;
+  int32_t* order = kv ? kv_order : q_order;
+  int shift = 0;
+  while (((S + 63) / 64 + 2) >> shift >= kSchedBuckets) ++shift;
+  auto cost = [&](int i) {
+    const int b = i / nblk, blk = i % nblk;
+    const int32_t* sst = seg_start + (long)b * S;
+    int c;
+    if (kv) {
+      const int k0 = blk * 128;
+      const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
+      const int q_end = first_above(sst, 0, S, klast);
+      const int q_begin = (k0 / kKT) * kKT;
+      c = q_end > q_begin ? (q_end - q_begin + kKT - 1) / kKT : 0;
+    } else {
+      const int q0 = blk * P;
+      const int q1 = (q0 + P < S) ? q0 + P : S;
+      const int kv0 = (sst[q0] / kKT) * kKT;
+      c = (q1 - kv0 + kKT - 1) / kKT;
+    }
+    return c >> shift;
+  };
+  const int t = threadIdx.x;
+  for (int j = t; j < kSchedBuckets; j += 1024) cnt[j] = 0;
+  __syncthreads();
+  for (int i = t; i < n; i += 1024) atomicAdd(&cnt[cost(i)], 1);
+  __syncthreads();
+  // First rank of each bucket, buckets in descending cost: thread t sums buckets (descending
+  // position) 2t and 2t + 1, then an exclusive scan over the 1024 threads.
+  const int ja = kSchedBuckets - 1 - 2 * t, jb = ja - 1;
+  const int ca = cnt[ja], cb = cnt[jb];
+  int x = ca + cb;
+  const int lane = t & 63, wv = t >> 6;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
+  }
+  if (lane == 63) wsum[wv] = x;
+  __syncthreads();
+  int before = 0;
+  for (int u = 0; u < wv; ++u) before += wsum[u];
+  const int excl = before + x - (ca + cb);
+  __syncthreads();
+  cnt[ja] = excl;
+  cnt[jb] = excl + ca;
+  __syncthreads();
+  for (int i = t; i < n; i += 1024) order[atomicAdd(&cnt[cost(i)], 1)] = i;
+}
+
 int attn_dkv_nsplit(int b, int hq, int hkv, int s, int dh, int causal) {
   if (b < 1 || hkv < 1 || s < 1 || hq % hkv) return 1;
   const long G = hq / hkv;
@@ -1025,12 +1112,26 @@ size_t attn_dvec_bytes(int b, int hq, int s) {
   return ((size_t)b * hq * s * sizeof(float) + 255) / 256 * 256;
 }
 
+namespace {
+size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+int fwd_rows(int hq, int hkv) {  // query positions per forward / dQ workgroup
+  const int G = hq / hkv;
+  return 32 * (4 / ((G % 4 == 0) ? 4 : ((G % 2 == 0) ? 2 : 1)));
+}
+// Byte offset of the packed work orders: after D and the fp32 dK/dV partials of the larger split.
+size_t attn_order_offset(int b, int hq, int hkv, int s, int dh) {
+  const int ns1 = attn_dkv_nsplit(b, hq, hkv, s, dh, 1), ns0 = attn_dkv_nsplit(b, hq, hkv, s, dh, 0);
+  const int ns = ns1 > ns0 ? ns1 : ns0;
+  return attn_dvec_bytes(b, hq, s) + (ns > 1 ? (size_t)ns * 2 * (size_t)b * hkv * s * dh * sizeof(float) : 0);
+}
+}  // namespace
+
 size_t attn_bwd_workspace(int b, int hq, int hkv, int s, int dh) {
-  // D plus, when either mode splits, the fp32 dK/dV partials of the larger split.
-  const int ns = attn_dkv_nsplit(b, hq, hkv, s, dh, 1) > attn_dkv_nsplit(b, hq, hkv, s, dh, 0)
-                     ? attn_dkv_nsplit(b, hq, hkv, s, dh, 1) : attn_dkv_nsplit(b, hq, hkv, s, dh, 0);
-  if (ns == 1) return (size_t)b * hq * s * sizeof(float);
-  return attn_dvec_bytes(b, hq, s) + (size_t)ns * 2 * (size_t)b * hkv * s * dh * sizeof(float);
+  // D, the fp32 dK/dV partials when either mode splits (the larger split), and the two work orders
+  // of a packed backward (int32 per dQ query block and per dK/dV key block).
+  const int P = fwd_rows(hq, hkv);
+  return attn_order_offset(b, hq, hkv, s, dh) + round256((size_t)b * ((s + P - 1) / P) * 4) +
+         round256((size_t)b * ((s + 127) / 128) * 4);
 }
 
 namespace {
@@ -1046,8 +1147,8 @@ hipError_t fwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
                   const int32_t* sst, bf16_t* o, float* lse, hipStream_t st) {
   const float sl2 = sh.scale * kLog2e;
   dim3 grid(fwd_grid(sh)), block(256);
-  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, nullptr);
+  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, false>), grid, block, 0, st, q, k, v, nullptr, nullptr, nullptr, nullptr, sid, sst, o, lse, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, nullptr);
   return hipGetLastError();
 }
 
@@ -1057,19 +1158,31 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
                   bf16_t* dk, bf16_t* dv, float* dvec, hipStream_t st) {
   dim3 block(256);
   hipError_t e = hipSuccess;
-  // The dQ pass forms D = rowsum(dO o O) itself and writes it for the dK/dV pass.
+  // Workspace: D (formed by the dQ pass for the dK/dV pass), the split dK/dV partials, and the
+  // packed work orders.
   const float sl2 = sh.scale * kLog2e;
+  char* ws = reinterpret_cast<char*>(dvec);
+  int32_t* q_order = nullptr;
+  int32_t* kv_order = nullptr;
+  if (sid) {
+    const int P = fwd_rows(sh.hq, sh.hkv);
+    q_order = reinterpret_cast<int32_t*>(ws + attn_order_offset(sh.b, sh.hq, sh.hkv, sh.s, DH));
+    kv_order = q_order + round256((size_t)sh.b * ((sh.s + P - 1) / P) * 4) / 4;
+    hipLaunchKernelGGL(attn_sched_kernel, dim3(2), dim3(1024), 0, st, sst, sh.b, sh.s, P, q_order, kv_order);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   dim3 qgrid(fwd_grid(sh));
-  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
-  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal);
+  if (sid) hipLaunchKernelGGL((attn_kv_kernel<DH, true, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, q_order);
+  else hipLaunchKernelGGL((attn_kv_kernel<DH, false, true>), qgrid, block, 0, st, q, k, v, d_o, o, lse, dvec, sid, sst, dq, nullptr, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, nullptr);
   e = hipGetLastError();
   if (e != hipSuccess) return e;
   // Split key blocks write fp32 partials after the D vector in the workspace; the reduce sums them.
   const int ns = attn_dkv_nsplit(sh.b, sh.hq, sh.hkv, sh.s, DH, sh.causal);
-  float* part = reinterpret_cast<float*>(reinterpret_cast<char*>(dvec) + attn_dvec_bytes(sh.b, sh.hq, sh.s));
+  float* part = reinterpret_cast<float*>(ws + attn_dvec_bytes(sh.b, sh.hq, sh.s));
   dim3 sgrid(((sh.s + 127) / 128) * sh.b * sh.hkv * ns);
-  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
-  else hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part);
+  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part, kv_order);
+  else hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part, nullptr);
   e = hipGetLastError();
   if (e != hipSuccess || ns == 1) return e;
   const long plane = (long)sh.b * sh.hkv * sh.s * DH;
