@@ -15,7 +15,7 @@ the ladders and the CPU baselines; marginal peak memory measured the worker's wa
 Profiling modes (their output is what profiles/ holds):
     python bench.py --pmc-workload                      # the program rocprofv3 --pmc passes profile
     python bench.py --pmc-summary CMD DIR [DIR ...]     # counters of those passes -> markdown
-    python bench.py --trace-summary CSV TITLE CMD       # rocprofv3 --kernel-trace csv -> markdown
+    python bench.py --trace-summary CSV TITLE CMD [STATS] # rocprofv3 --kernel-trace (--stats) csv -> markdown
 """
 from __future__ import annotations
 
@@ -680,11 +680,11 @@ def pmc_summary(command: str, *dirs: str) -> str:
     return "\n".join(lines)
 
 
-def trace_summary(trace_csv: str, title: str, command: str) -> str:
+def trace_summary(trace_csv: str, title: str, command: str, stats_csv: str | None = None) -> str:
     """Markdown table of this library's kernels from a rocprofv3 --kernel-trace csv (one row per
     dispatch), one line per (kernel, grid size) -- i.e. per launch shape, since the ladders reuse the
     kernels at other sizes: calls, median, mean, the mean without the shape's first dispatch (its
-    warm-up), min and max."""
+    warm-up), min and max. With the same run's --stats csv, its per-kernel calls and average too."""
     import collections
     import csv
     import re
@@ -697,14 +697,22 @@ def trace_summary(trace_csv: str, title: str, command: str) -> str:
             durs[(name, grid)].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
     out = [f"# {title}", "", "Command (repository root on the GPU box):", "", "```", command, "```", "",
            "Per-launch-shape durations from `rocprofv3 --kernel-trace` (one row per dispatch), microseconds; "
-           "grid = work-items. The bench line's roofline uses the median of its per-launch event times; compare "
-           "it with the median here.", "",
+           "grid = work-items. The bench line's roofline uses the mean of its per-launch event times (which "
+           "also hold the forward's 22 us finalize launch); compare it with the mean here.", "",
            "| kernel | grid | calls | median us | mean us | mean w/o first us | min us | max us |",
            "|---|---:|---:|---:|---:|---:|---:|---:|"]
     for (name, grid), d in sorted(durs.items(), key=lambda kv: -sum(kv[1])):
         rest = d[1:] or d
         out.append(f"| `{name}` | {grid} | {len(d)} | {statistics.median(d):.1f} | {sum(d) / len(d):.1f} | "
                    f"{sum(rest) / len(rest):.1f} | {min(d):.1f} | {max(d):.1f} |")
+    if stats_csv:
+        out += ["", "`rocprofv3 --stats` of the same run (all launch shapes of a kernel together), microseconds:", "",
+                "| kernel | calls | average us | min us | max us |", "|---|---:|---:|---:|---:|"]
+        for r in csv.DictReader(open(stats_csv)):
+            if "mtp::" in r["Name"]:
+                name = re.sub(r"\(.*", "", r["Name"]).replace("void ", "").replace("mtp::", "").strip()
+                out.append(f"| `{name}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                           f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} |")
     return "\n".join(out) + "\n"
 
 
@@ -718,8 +726,9 @@ def main():
     ap.add_argument("--pmc-workload", action="store_true", help="run the profiled workloads once (no timing)")
     ap.add_argument("--pmc-summary", nargs="+", metavar="ARG",
                     help="COMMAND DIR [DIR ...]: summarize rocprofv3 --pmc csv outputs into markdown")
-    ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "TITLE", "COMMAND"),
-                    help="summarize a rocprofv3 --kernel-trace csv into markdown")
+    ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
+                    help="TRACE_CSV TITLE COMMAND [STATS_CSV]: summarize a rocprofv3 --kernel-trace csv (and the "
+                         "same run's --stats csv) into markdown")
     ap.add_argument("--parts", default="lce,qlora,attention,ladder",
                     help="comma list of lce, qlora, attention, ladder (lce is the headline line)")
     args = ap.parse_args()
@@ -746,7 +755,7 @@ def main():
     sec = lce["sec_per_step"]
     flops_step = 6.0 * N * V * D
     fwd_flops = 2.0 * N * V * D
-    ach = fwd_flops / (lce["fwd_kernel_ms_median"] * 1e-3) / 1e12
+    ach = fwd_flops / (lce["fwd_kernel_ms_mean"] * 1e-3) / 1e12
     result = {
         "metric": "fused-LCE fwd+bwd tokens/s @N8192 V151936 D4096 (bf16, frozen head)",
         "value": N / sec,
@@ -765,7 +774,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "lce_fwd_kernel<0> (+ lce_fwd_finalize_kernel in the event window)",
                      "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
                      "traffic": committed_traffic("lce_fwd_kernel<0>"),
-                     "timing": f"median of {lce['fwd_kernel_launches']} launches, HIP events on the launch stream"},
+                     "timing": f"mean of {lce['fwd_kernel_launches']} launches (after one warm-up), HIP events on "
+                               "the launch stream; the window also holds the 22 us finalize launch"},
         "step_mfma_frac": flops_step / sec / 1e12 / PEAK_BF16_TFLOPS,
         "lce": {**lce, "step_tflops": flops_step / sec / 1e12},
     }
