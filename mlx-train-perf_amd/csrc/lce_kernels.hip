@@ -1674,23 +1674,26 @@ hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt,
 constexpr long kFwdWaves = 1;
 
 // Vocab splits for a persistent launch over N rows and V vocab columns with `per_cu` workgroups
-// resident per compute unit: the count that minimizes resident rounds x (vocab tiles per split + 1),
-// the 1 standing for a workgroup's pipeline fill and partial store; ties go to fewer splits. (A
-// count that only just overflows one round, e.g. 48 row tiles x 6 splits = 288 workgroups, would
-// run two rounds of one split's tiles each.)
+// resident per compute unit. cost(ns) = resident rounds x (vocab tiles per split + 1), the 1 standing
+// for a workgroup's pipeline fill and partial store; the plan is the fewest splits within 5% of the
+// cheapest count, since every split adds partials for the finalize to merge (and to the workspace).
+// At most 2048 workgroups (8 resident rounds at one per CU), so splits x N <= 2048 x 256 and the
+// forward's partials [2][splits][N] fp32 never exceed 4 MiB for N <= 524288. (A count that only just
+// overflows one round, e.g. 48 row tiles x 6 splits = 288 workgroups, would run two rounds of one
+// split's tiles each.)
 static int lce_nsplit(long N, long V, int per_cu) {
   const long rtiles = (N + kTile - 1) / kTile;
   const long vtiles = (V + kTile - 1) / kTile;
   const long slots = (long)per_cu * kNumCU;
-  long best = 1, best_cost = -1;
-  for (long ns = 1; ns <= vtiles && ns <= 1024; ++ns) {
-    const long cost = (rtiles * ns + slots - 1) / slots * ((vtiles + ns - 1) / ns + 1);
-    if (best_cost < 0 || cost < best_cost) {
-      best = ns;
-      best_cost = cost;
-    }
-  }
-  return (int)best;
+  long top = vtiles < 1024 ? vtiles : 1024;
+  if (top > 2048 / rtiles) top = 2048 / rtiles > 1 ? 2048 / rtiles : 1;
+  auto cost = [&](long ns) { return (rtiles * ns + slots - 1) / slots * ((vtiles + ns - 1) / ns + 1); };
+  long least = cost(1);
+  for (long ns = 2; ns <= top; ++ns)
+    if (cost(ns) < least) least = cost(ns);
+  for (long ns = 1; ns <= top; ++ns)
+    if (cost(ns) * 100 <= least * 105) return (int)ns;
+  return 1;
 }
 
 // Parts of the dH product's vocab contraction (1 = none) for `rows` rows, D columns and `ktiles`

@@ -48,17 +48,19 @@ FWD_WGS_PER_CU = 1  # forward workgroups per CU (csrc/lce_kernels.hip)
 
 def lce_nsplit(n: int, v: int, per_cu: int = FWD_WGS_PER_CU) -> int:
     """Vocab splits of a persistent LCE launch (forward, and the backward's gradient tiles per
-    chunk): the count minimizing resident rounds x (vocab tiles per split + 1), ties to fewer
-    splits, never more than the vocab tiles (or 1024)."""
+    chunk): cost(ns) = resident rounds x (vocab tiles per split + 1); the fewest splits within 5% of
+    the cheapest count (every split adds partials to merge), never more than the vocab tiles, 1024,
+    or 2048 workgroups in all (so splits x n <= 524288: 4 MiB of forward partials)."""
     rtiles = -(-n // TILE)
     vtiles = -(-v // TILE)
     slots = per_cu * NUM_CU
-    best, best_cost = 1, None
-    for ns in range(1, min(vtiles, 1024) + 1):
-        cost = -(-(rtiles * ns) // slots) * (-(-vtiles // ns) + 1)
-        if best_cost is None or cost < best_cost:
-            best, best_cost = ns, cost
-    return best
+    top = max(1, min(vtiles, 1024, 2048 // rtiles))
+
+    def cost(ns: int) -> int:
+        return -(-(rtiles * ns) // slots) * (-(-vtiles // ns) + 1)
+
+    least = min(cost(ns) for ns in range(1, top + 1))
+    return next(ns for ns in range(1, top + 1) if cost(ns) * 100 <= least * 105)
 
 
 def lce_fwd_splits(n: int, v: int) -> int:

@@ -37,12 +37,14 @@ def test_lce_forward_splits(n, v):
 def test_lce_splits_fill_whole_rounds():
     """Persistent-launch splits: a split count that just overflows one resident round (48 row tiles x
     6 splits = 288 workgroups on 256 CUs) is never chosen; the makespan (rounds x tiles per split)
-    is never worse than the rule "about one workgroup per CU, rounded up to a multiple of 8"."""
+    stays within 5% of the rule "about one workgroup per CU, rounded up to a multiple of 8" (the plan
+    takes the fewest splits within 5% of its cheapest count) and is often far below it."""
     def makespan(rt, vt, ns):
         return -(-(rt * ns) // 256) * -(-vt // ns)
 
+    assert plan.lce_fwd_splits(8192, 151936) == 8           # one round of 32 x 8, the flagship
     assert plan.lce_fwd_splits(12288, 32000) == 5          # 240 workgroups, one round of 25 tiles
-    assert plan.lce_fwd_splits(12288, 151936) == 16        # 3 rounds of 38 tiles, not 2 x 99
+    assert plan.lce_fwd_splits(12288, 151936) == 5         # one round of 119 tiles, not 2 x 99
     assert plan.lce_fwd_splits(16384, 128256) == 4
     for n in (256, 1000, 2048, 4096, 8192, 12288, 16384, 65536):
         for v in (1024, 32000, 128256, 151936, 262144):
@@ -50,7 +52,16 @@ def test_lce_splits_fill_whole_rounds():
             ns = plan.lce_fwd_splits(n, v)
             old = -(-256 // rt)
             old = min(-(-old // 8) * 8 if old >= 8 else old, vt)
-            assert makespan(rt, vt, ns) <= makespan(rt, vt, max(old, 1)), (n, v)
+            assert makespan(rt, vt, ns) <= 1.05 * makespan(rt, vt, max(old, 1)) + 1, (n, v)
+
+
+def test_lce_forward_partials_fit_the_noalloc_scratch():
+    """At most 2048 forward workgroups, so splits x n <= 524288 and the partials [2][splits][n] fp32
+    fit the 4 MiB no-alloc scratch for every n <= 524288, whatever v."""
+    for v in (1, 1000, 32000, 151936, 262144, 1 << 20):
+        for n in list(range(256, 70000, 256)) + [131072, 300000, 524288]:
+            assert plan.lce_fwd_workspace_bytes(n, v) <= 4 << 20, (n, v)
+    assert plan.lce_fwd_workspace_bytes(524289, 151936) > 4 << 20
 
 
 def test_lce_dh_split_fills_rounds():
