@@ -85,9 +85,10 @@ size_t mtp_lce_fwd_noalloc_max_workspace_bytes(void);
 
 /* Rows per backward block for a workspace budget (bytes): n when the whole padded vocab's gradient
  * tiles for all rows fit the budget; else a multiple of 256 (n split in 2 or 4 blocks) whose
- * whole-vocab gradient tiles fit it while the dH product keeps >= 256 output tiles per block;
- * else n (the vocab is chunked instead). Replaces the reference's chunk budgeting
- * (core/kernel/launch.py:63-72), which bounds the per-dispatch size. */
+ * whole-vocab gradient tiles fit it while the dH product keeps >= 256 output tiles per block; else,
+ * when chunking the vocab would take more than 2 chunks, 8 or 16 blocks that fit (their dH products
+ * split the contraction over the vocab); else n (the vocab is chunked instead). Replaces the
+ * reference's chunk budgeting (core/kernel/launch.py:63-72), which bounds the per-dispatch size. */
 int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
 /* Vocab columns per backward chunk, a multiple of 256, when all n rows form one block (a trainable
@@ -96,8 +97,10 @@ int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_byt
 int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
 /* Workspace bytes needed by mtp_lce_bwd at a given chunk and row block (0 or >= n: all rows): the
- * bf16 gradient tile buffer [row_block][chunk + 64] (the row pitch is padded off a power of two)
- * plus, when more than one chunk is needed, an fp32 [row_block][d] dH accumulator. */
+ * bf16 gradient tile buffer [row_block][chunk + 64] (the row pitch is padded off a power of two),
+ * an fp32 [row_block][d] dH accumulator when more than one chunk is needed, and, when a block's dH
+ * product splits its vocab contraction to fill the GPU, its fp32 part tiles
+ * [parts][tiles][256][256] (the most any row block and chunk of the plan takes). */
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block);
 

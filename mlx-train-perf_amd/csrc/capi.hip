@@ -175,11 +175,21 @@ int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_byt
   const size_t row_bytes = (size_t)(vpad + mtp::kGPitchPad) * 2;  // one row of gradient tiles
   if ((size_t)n * row_bytes <= budget_bytes) return n;
   // Split the rows in 2 or 4 blocks while each block's whole-vocab G fits the budget and its dH
-  // product keeps at least one 256 x 256 output tile per CU; otherwise chunk the vocab instead.
+  // product keeps at least one 256 x 256 output tile per CU.
   for (int64_t parts = 2; parts <= 4; parts *= 2) {
     const int64_t rows = round_up((n + parts - 1) / parts, kTile);
     if ((rows / kTile) * ((d + kTile - 1) / kTile) < mtp::kNumCU) break;
     if ((size_t)rows * row_bytes <= budget_bytes) return rows;
+  }
+  // Otherwise the vocab is chunked, with an fp32 dH read-modify-write per chunk. Past 2 chunks,
+  // up to 16 smaller row blocks whose dH products split their contraction (lce_dh_ksplit) instead
+  // measured faster (N = 30720, D = 2048: 50.0 against 52.3 ms).
+  const int64_t chunk = mtp_lce_bwd_chunk(n, d, v, budget_bytes);
+  if ((v + chunk - 1) / chunk > 2) {
+    for (int64_t parts = 8; parts <= 16; parts *= 2) {
+      const int64_t rows = round_up((n + parts - 1) / parts, kTile);
+      if ((size_t)rows * row_bytes <= budget_bytes) return rows;
+    }
   }
   return n;
 }
