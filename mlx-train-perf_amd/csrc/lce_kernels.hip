@@ -819,16 +819,20 @@ __device__ __forceinline__ bool xcd_rows_tile(int mtiles, int ntiles, int& m, in
   return n < ntiles;
 }
 
-// One resident round of exactly 8 x 32 workgroups (one per CU) over an M x N tile grid with
-// M % 4 == 0, N % 8 == 0 and (M / 4) (N / 8) == 8: XCD x (workgroup g runs on XCD g % 8) takes the
-// 4 x 8 rectangle (M group x % (M / 4), N group x / (M / 4)), so its 32 workgroups share 4 M-operand
-// and 8 N-operand slabs per stage in its L2. With M / 8 = 2 (a 16-tile row block) the row-grouped
-// orders give each XCD 2 x 16 tiles instead: 18 slabs per stage, and each XCD streams the whole
-// N operand. Returns false when the grid is not of this form (use the other orders then).
+// Resident rounds of 8 x 32 workgroups (one per CU) over an M x N tile grid with M % 4 == 0,
+// N in {8, 16, 32, 64} and M % (256 / N) == 0: round r = g / 256 covers M tiles
+// [r M_r, (r + 1) M_r), M_r = 256 / N, and within it XCD x (workgroup g runs on XCD g % 8) takes the
+// 4 x 8 rectangle (M group x % (M_r / 4), N group x / (M_r / 4)), so its 32 workgroups share 4
+// M-operand and 8 N-operand slabs per stage in its L2. With M / 8 = 2 (a 16-tile row block) the
+// row-grouped orders give each XCD 2 x 16 tiles instead: 18 slabs per stage, and each XCD streams
+// the whole N operand; one split per row tile (N = 1) gives it 32 row slabs and one head slab: 33.
+// Returns false when the grid is not of this form (use the other orders then).
 __device__ __forceinline__ bool xcd_rect_tile(int mtiles, int ntiles, int& m, int& n) {
-  if (mtiles % 4 != 0 || ntiles % 8 != 0 || (mtiles / 4) * (ntiles / 8) != 8) return false;
-  const int nmg = mtiles / 4, x = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  m = 4 * (x % nmg) + (slot & 3);
+  if (mtiles % 4 != 0 || ntiles % 8 != 0 || 8 % (ntiles / 8) != 0) return false;
+  const int nmg = 8 / (ntiles / 8);  // M groups of 4 per round
+  if ((mtiles / 4) % nmg != 0) return false;
+  const int g = blockIdx.x, rnd = g >> 8, x = g & 7, slot = (g & 255) >> 3;
+  m = 4 * (rnd * nmg + x % nmg) + (slot & 3);
   n = 8 * (x / nmg) + (slot >> 2);
   return true;
 }
@@ -1691,6 +1695,11 @@ static int lce_nsplit(long N, long V, int per_cu) {
   long least = cost(1);
   for (long ns = 2; ns <= top; ++ns)
     if (cost(ns) < least) least = cost(ns);
+  // A count the XCD rectangles tile (rounds of 256 / ns row tiles x ns splits) first: 12 operand
+  // slabs per stage per XCD instead of up to 33.
+  if (per_cu == 1)
+    for (long ns = 8; ns <= 32 && ns <= top; ns *= 2)
+      if (rtiles % (256 / ns) == 0 && cost(ns) * 100 <= least * 105) return (int)ns;
   for (long ns = 1; ns <= top; ++ns)
     if (cost(ns) * 100 <= least * 105) return (int)ns;
   return 1;

@@ -48,9 +48,10 @@ FWD_WGS_PER_CU = 1  # forward workgroups per CU (csrc/lce_kernels.hip)
 
 def lce_nsplit(n: int, v: int, per_cu: int = FWD_WGS_PER_CU) -> int:
     """Vocab splits of a persistent LCE launch (forward, and the backward's gradient tiles per
-    chunk): cost(ns) = resident rounds x (vocab tiles per split + 1); the fewest splits within 5% of
-    the cheapest count (every split adds partials to merge), never more than the vocab tiles, 1024,
-    or 2048 workgroups in all (so splits x n <= 524288: 4 MiB of forward partials)."""
+    chunk): cost(ns) = resident rounds x (vocab tiles per split + 1). Within 5% of the cheapest count:
+    8, 16 or 32 when the XCD rectangles tile it (n's row tiles a multiple of 256 / ns), else the
+    fewest splits (every split adds partials to merge); never more than the vocab tiles, 1024, or
+    2048 workgroups in all (so splits x n <= 524288: 4 MiB of forward partials)."""
     rtiles = -(-n // TILE)
     vtiles = -(-v // TILE)
     slots = per_cu * NUM_CU
@@ -60,6 +61,10 @@ def lce_nsplit(n: int, v: int, per_cu: int = FWD_WGS_PER_CU) -> int:
         return -(-(rtiles * ns) // slots) * (-(-vtiles // ns) + 1)
 
     least = min(cost(ns) for ns in range(1, top + 1))
+    if per_cu == 1:   # a count the XCD rectangles tile (256 / ns row tiles x ns splits per round) first
+        for ns in (8, 16, 32):
+            if ns <= top and rtiles % (256 // ns) == 0 and cost(ns) * 100 <= least * 105:
+                return ns
     return next(ns for ns in range(1, top + 1) if cost(ns) * 100 <= least * 105)
 
 

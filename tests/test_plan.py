@@ -43,9 +43,12 @@ def test_lce_splits_fill_whole_rounds():
         return -(-(rt * ns) // 256) * -(-vt // ns)
 
     assert plan.lce_fwd_splits(8192, 151936) == 8           # one round of 32 x 8, the flagship
-    assert plan.lce_fwd_splits(12288, 32000) == 5          # 240 workgroups, one round of 25 tiles
-    assert plan.lce_fwd_splits(12288, 151936) == 5         # one round of 119 tiles, not 2 x 99
-    assert plan.lce_fwd_splits(16384, 128256) == 4
+    # XCD rectangles (256 / ns row tiles x ns splits per round) when within 5% of the cheapest count
+    assert plan.lce_fwd_splits(12288, 32000) == 16         # 3 rounds of 16 x 16, not 2 rounds of 48 x 6
+    assert plan.lce_fwd_splits(12288, 151936) == 16
+    assert plan.lce_fwd_splits(16384, 128256) == 8         # 2 rounds of 32 x 8
+    assert plan.lce_fwd_splits(65536, 151936) == 8         # 8 rounds of 32 x 8, not 1 split per row tile
+    assert plan.lce_fwd_splits(30720, 151936) == 2         # 120 row tiles: no rectangle; fewest splits
     for n in (256, 1000, 2048, 4096, 8192, 12288, 16384, 65536):
         for v in (1024, 32000, 128256, 151936, 262144):
             rt, vt = -(-n // 256), -(-v // 256)
