@@ -86,7 +86,7 @@ size_t mtp_lce_fwd_noalloc_max_workspace_bytes(void);
 /* Rows per backward block for a workspace budget (bytes): n when the whole padded vocab's gradient
  * tiles for all rows fit the budget; else a multiple of 256 (n split in 2 or 4 blocks) whose
  * whole-vocab gradient tiles fit it while the dH product keeps >= 256 output tiles per block; else,
- * when chunking the vocab would take more than 2 chunks, 8 or 16 blocks that fit (their dH products
+ * when chunking the vocab would take more than 4 chunks, 8 or 16 blocks that fit (their dH products
  * split the contraction over the vocab); else n (the vocab is chunked instead). Replaces the
  * reference's chunk budgeting (core/kernel/launch.py:63-72), which bounds the per-dispatch size. */
 int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_bytes);

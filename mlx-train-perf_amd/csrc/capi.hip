@@ -181,11 +181,12 @@ int64_t mtp_lce_bwd_row_block(int64_t n, int64_t d, int64_t v, size_t budget_byt
     if ((rows / kTile) * ((d + kTile - 1) / kTile) < mtp::kNumCU) break;
     if ((size_t)rows * row_bytes <= budget_bytes) return rows;
   }
-  // Otherwise the vocab is chunked, with an fp32 dH read-modify-write per chunk. Past 2 chunks,
-  // up to 16 smaller row blocks whose dH products split their contraction (lce_dh_ksplit) instead
-  // measured faster (N = 30720, D = 2048: 50.0 against 52.3 ms).
+  // Otherwise the vocab is chunked, with an fp32 dH read-modify-write per chunk. Past 4 chunks,
+  // 8 or 16 smaller row blocks whose dH products split their contraction (lce_dh_ksplit) instead
+  // measured faster (N = 30720, D = 2048, 7 chunks: 50.0 against 52.1 ms); at 3 chunks the chunked
+  // plan was (N = 12288, D = 4096: 34.7 ms against 35.4 for 4 blocks and 36.4 for 8).
   const int64_t chunk = mtp_lce_bwd_chunk(n, d, v, budget_bytes);
-  if ((v + chunk - 1) / chunk > 2) {
+  if ((v + chunk - 1) / chunk > 4) {
     for (int64_t parts = 8; parts <= 16; parts *= 2) {
       const int64_t rows = round_up((n + parts - 1) / parts, kTile);
       if ((size_t)rows * row_bytes <= budget_bytes) return rows;

@@ -102,7 +102,7 @@ def lce_bwd_row_block(n: int, d: int, v: int, budget: int) -> int:
     """Rows per backward block (mirror of mtp_lce_bwd_row_block): all n when the whole padded
     vocab's gradient tiles fit the budget; else n split in 2 or 4 blocks (a multiple of 256 rows)
     whose whole-vocab tiles fit it while the dH product keeps >= NUM_CU output tiles; else, when
-    chunking the vocab would take more than 2 chunks, 8 or 16 blocks that fit (their dH products
+    chunking the vocab would take more than 4 chunks, 8 or 16 blocks that fit (their dH products
     split the contraction); else n."""
     vpad = -(-v // TILE) * TILE
     row_bytes = (vpad + G_PITCH_PAD) * 2
@@ -114,7 +114,7 @@ def lce_bwd_row_block(n: int, d: int, v: int, budget: int) -> int:
             break
         if rows * row_bytes <= budget:
             return rows
-    if -(-v // lce_bwd_chunk(n, d, v, budget)) > 2:
+    if -(-v // lce_bwd_chunk(n, d, v, budget)) > 4:
         for parts in (8, 16):
             rows = -(-(-(-n // parts)) // TILE) * TILE
             if rows * row_bytes <= budget:
