@@ -10,6 +10,8 @@ GPU so the full shapes finish in seconds:
       fp32-head convention, tests/test_kernel_quant_parity.py:74-97): nll within 2e-3 relative and
       8e-3 absolute (the reference's bf16-dequant pin), dL/dH within 1e-2 relative-L2, through both
       backward paths (cached dequantized transposed head, and in-register dequant).
+- Shapes past the flagship whose launches run several resident rounds of XCD rectangles (forward
+  and gradient tiles at n=16384, v=65536; the dH product at n=16384, d=2048): same bars.
 - C4  GQA causal attention B=1, Hq=32, Hkv=8, S=8192, head_dim 128: O, dQ, dK, dV within 1e-2
       relative-L2, O within 1.2e-2 x max(1, |O|max) max-abs (the reference's bf16 forward pin), L
       within 2e-3; the
@@ -132,7 +134,8 @@ def test_c3_flagship_lce_q4(monkeypatch):
     onll, olse, _ = olce.forward(h, wdq, t, ignore_index=IGN, dtype=torch.float64)
     odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
     _check_lce(nll, lse, dh, onll, olse, odh, t, nll_abs=8e-3)
-    # the backward without the cached transposed head: 8x8 blocks dequantized in registers
+    # the backward without the cached transposed head: the 4-bit head dequantized in registers into
+    # the dH product's transposed operand tiles
     print("[C3] in-register dequant backward (MTP_LCE_TRANSPOSED_HEAD=0)", flush=True)
     monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", "0")
     L.clear_transposed_head_cache()
@@ -140,6 +143,43 @@ def test_c3_flagship_lce_q4(monkeypatch):
     assert (dh2[t == IGN] == 0).all()
     r = _rel_l2(dh2, odh)
     print(f"  dH rel-L2 {r:.3e}", flush=True)
+    assert r <= 1e-2
+
+
+@pytest.mark.parametrize(("n", "d", "v"), [(16384, 64, 65536), (16384, 2048, 4096)])
+def test_lce_multi_round_xcd_rectangles(n, d, v):
+    """Grids of several resident rounds of 256 workgroups in XCD rectangles: at n=16384, v=65536 the
+    forward takes 8 splits of 64 row tiles (2 rounds) and so do the gradient tiles of the two-chunk
+    backward (whose dH products split their vocab contraction); at d=2048, v=4096 the one-chunk dH
+    product has 64 x 8 output tiles (2 rounds)."""
+    from mlx_train_perf.core.loss import DenseHead
+    from mlx_train_perf.plan import launch as plan
+
+    print(f"[lce rounds] N={n} D={d} V={v}", flush=True)
+    rt = n // 256
+    if v == 65536:
+        assert plan.lce_fwd_splits(n, v) == 8 and rt * 8 == 2 * 256
+        chunk = plan.lce_bwd_chunk(n, d, v, plan.DEFAULT_LCE_BWD_BUDGET)
+        assert -(-v // chunk) == 2 and plan.lce_nsplit(n, chunk, 1) == 8
+        assert plan.lce_dh_ksplit(n, d, chunk // 256) > 1
+    else:
+        assert plan.lce_bwd_row_block(n, d, v, plan.DEFAULT_LCE_BWD_BUDGET) == n and rt * (d // 256) == 2 * 256
+    g = torch.Generator(device="cuda").manual_seed(n + d + v)
+    h = torch.randn(n, d, generator=g, device="cuda")
+    h = (h / torch.sqrt((h * h).mean(dim=-1, keepdim=True) + 1e-6)).to(torch.bfloat16)
+    w = (torch.randn(v, d, generator=g, device="cuda") * 0.02).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g, device="cuda")
+    t[torch.randperm(n, generator=g, device="cuda")[: n // 20]] = IGN
+    nll, lse, dh, ct = _kernel_lce(h, DenseHead(weight=w, trainable=False), t)
+    onll, olse, _ = olce.forward(h, w, t, ignore_index=IGN, dtype=torch.float64)
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    err = (nll.double() - onll).abs()
+    assert (err <= 2e-3 * onll.abs() + 1e-4).all(), f"nll: worst {float(err.max()):.3e}"
+    assert float((lse.double() - olse).abs().max()) <= 2e-3 * float(olse.abs().max())
+    ign = t == IGN
+    assert (nll[ign] == 0).all() and (dh[ign] == 0).all()
+    r = _rel_l2(dh, odh)
+    print(f"  nll max-abs {float(err.max()):.3e}, dH rel-L2 {r:.3e}", flush=True)
     assert r <= 1e-2
 
 
