@@ -155,9 +155,11 @@ int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t
                  int64_t s, int64_t dh, float scale, int32_t causal, const int32_t* seg_id,
                  const int32_t* seg_start, void* o, float* lse, void* stream);
 
-/* Workspace bytes for mtp_attn_bwd: the fp32 row term D = rowsum(dO * O), [b][hq][s], plus, at
- * shapes where the dK/dV pass splits its key blocks (mtp_attn_bwd_dkv_splits > 1 for either value
- * of causal), fp32 dK/dV partials [splits][2][b][hkv][s][dh] after D padded to 256 bytes. */
+/* Workspace bytes for mtp_attn_bwd: the fp32 row term D = rowsum(dO * O), [b][hq][s], padded to
+ * 256 bytes; at shapes where the dK/dV pass splits its key blocks (mtp_attn_bwd_dkv_splits > 1 for
+ * either value of causal), fp32 dK/dV partials [splits][2][b][hkv][s][dh]; then the int32 work
+ * orders a packed call sorts its dQ query blocks and dK/dV key blocks into (one entry per block,
+ * each order padded to 256 bytes). */
 size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh);
 
 /* Workgroups per 128-key block of the dK/dV pass (1, 2, 4 or 8): the launch plan's
