@@ -69,6 +69,26 @@ def test_causal_parity(shape):
     _check(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
 
 
+# Edge lengths: one and two positions (query 0 attends to key 0 alone: P = 1, so dS and with it dQ
+# and dK are 0), and one past a 32-query wave block.
+@pytest.mark.parametrize("shape", [(1, 4, 2, 1, 128), (1, 4, 4, 2, 64), (2, 8, 2, 33, 96), (1, 4, 1, 1, 64)])
+def test_causal_parity_edge_lengths(shape):
+    b, hq, hkv, s, d = shape
+    print(f"[attn causal edge] {shape}", flush=True)
+    q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=3 * s + d)
+    scale = 1.0 / math.sqrt(d)
+    o, lse, dq, dk, dv = _run_kernel(q, k, v, do, scale)
+    oo, ol = oatt.attention_forward(q, k, v, scale=scale, causal=True, dtype=torch.float64)
+    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, causal=True, dtype=torch.float64)
+    assert rel_l2(o, oo) <= 1e-2 and (lse.double() - ol).abs().max() <= 2e-3
+    for got, want in ((dq, odq), (dk, odk), (dv, odv)):
+        assert torch.isfinite(got.float()).all()
+        if want.abs().max() < 1e-9:  # exactly-zero gradients (s = 1): a relative norm is undefined
+            assert got.abs().max() <= 1e-3
+        else:
+            assert rel_l2(got, want) <= 1e-2
+
+
 @pytest.mark.parametrize("shape", [(1, 8, 2, 1100, 128), (1, 4, 1, 130, 96), (1, 4, 2, 257, 64)])
 def test_causal_parity_rising_maxima(shape):
     """Scores with a large spread whose row maxima keep rising along the keys, so the online

@@ -73,6 +73,41 @@ def test_backward_parity_dense(n, d, v, chunk):
     assert (dh[t == IGN] == 0).all()
 
 
+# Edge shapes: one token, a single class (p = 1, so nll and dL/dH are 0), vocabularies below, at and
+# one past a 256-row tile.
+@pytest.mark.parametrize(("n", "d", "v"), [(1, 64, 100), (2, 64, 1), (1, 192, 2), (3, 128, 256), (5, 64, 257)])
+def test_edge_shapes_dense(n, d, v):
+    print(f"[lce edge dense] n={n} d={d} v={v}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n + 5 * v)
+    hd, nll, lse, tgt = _kernel(h, w, t)
+    onll, olse, otgt = olce.forward(h, w, t, ignore_index=IGN)
+    assert ((nll.cpu().double() - onll).abs() <= 2e-3 * onll.abs() + 1e-4).all()
+    assert (lse.cpu().double() - olse).abs().max() <= 2e-3 * max(1.0, olse.abs().max().item())
+    ct = _cotangent(t)
+    nll.backward(ct.to("cuda"))
+    dh = hd.grad.cpu()
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    if v == 1:
+        assert odh.abs().max() == 0 and dh.abs().max() <= 1e-3
+    else:
+        assert rel_l2(dh, odh) <= 1e-2
+
+
+@pytest.mark.parametrize(("n", "d", "v"), [(1, 64, 100), (3, 128, 257)])
+def test_edge_shapes_quantized(n, d, v):
+    print(f"[lce edge q4] n={n} d={d} v={v}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=31 + n + v, w_std=0.05)
+    wq, sc, bi = oquant.quantize_affine(w.float(), group_size=64, scale_dtype=torch.bfloat16)
+    wdq = oquant.dequantize_affine(wq, sc, bi, group_size=64, dtype=torch.float32)
+    hd, nll, lse, tgt = _kernel(h, None, t, head="q4", wq=wq, sc=sc, bi=bi)
+    onll, olse, otgt = olce.forward(h, wdq, t, ignore_index=IGN)
+    assert (nll.cpu().double() - onll).abs().max() <= 8e-3
+    ct = _cotangent(t)
+    nll.backward(ct.to("cuda"))
+    odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+
+
 @pytest.mark.parametrize(("n", "d", "v", "chunk"), [(64, 64, 1024, None), (65, 192, 1027, 256),
                                                     (300, 512, 5000, 1024), (2048, 128, 9000, 4096)])
 def test_quantized_parity(n, d, v, chunk):
