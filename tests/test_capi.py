@@ -8,6 +8,8 @@ import re
 from pathlib import Path
 
 import pytest
+from hypothesis import given, settings
+from hypothesis import strategies as st
 
 from mlx_train_perf import _native
 from mlx_train_perf.plan import launch as plan
@@ -50,6 +52,35 @@ def test_plans_agree_with_python_planner(n, d, v):
         assert p.bwd_row_block == rb
         assert p.bwd_workspace_bytes == lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, p.bwd_chunk, rb)
     assert lib.mtp_attn_bwd_workspace_bytes(1, 32, 8, 8192, 128) == plan.attn_plan(b=1, hq=32, hkv=8, s=8192).bwd_workspace_bytes
+
+
+@settings(max_examples=400, deadline=None, derandomize=True)
+@given(n=st.integers(1, 1 << 17), d=st.integers(1, 160).map(lambda k: 64 * k), v=st.integers(1, 1 << 18),
+       budget_log2=st.integers(16, 36))
+def test_plans_agree_over_random_shapes(n, d, v, budget_log2):
+    """The Python mirrors of the launch planner (vocab splits, chunks, row blocks, dH contraction
+    parts, workspace sizes) against the library over seeded random shapes and budgets."""
+    lib = _native.load()
+    budget = 1 << budget_log2
+    assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, 0) == plan.lce_fwd_workspace_bytes(n, v)
+    c = lib.mtp_lce_bwd_chunk(n, d, v, budget)
+    assert c == plan.lce_bwd_chunk(n, d, v, budget)
+    rb = lib.mtp_lce_bwd_row_block(n, d, v, budget)
+    assert rb == plan.lce_bwd_row_block(n, d, v, budget)
+    for rows in (0, n, rb):
+        assert lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, c, rows) == plan.lce_bwd_workspace_bytes(n, d, v, c, rows)
+
+
+@settings(max_examples=300, deadline=None, derandomize=True)
+@given(b=st.integers(1, 8), hkv=st.sampled_from([1, 2, 4, 8]), g=st.sampled_from([1, 2, 3, 4, 8]),
+       s=st.integers(1, 40000), dh=st.sampled_from([64, 96, 128]), causal=st.booleans())
+def test_attention_plans_agree_over_random_shapes(b, hkv, g, s, dh, causal):
+    lib = _native.load()
+    hq = hkv * g
+    assert lib.mtp_attn_bwd_dkv_splits(b, hq, hkv, s, dh, int(causal)) == plan.attn_dkv_splits(
+        b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=causal)
+    assert lib.mtp_attn_bwd_workspace_bytes(b, hq, hkv, s, dh) == plan.attn_bwd_workspace_bytes(
+        b=b, hq=hq, hkv=hkv, s=s, dh=dh)
 
 
 def test_dkv_split_table_agrees_with_python_planner():
