@@ -740,7 +740,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one MI355X; --gpus {args.gpus} is not supported (this build runs on one GPU; "
-              "see DESIGN.md for how the path would shard)", file=sys.stderr)
+              "sharding across GPUs is a design here, not a measured configuration)", file=sys.stderr)
         sys.exit(2)
     import torch
 
