@@ -1,8 +1,8 @@
 """GPU parity over seeded random shapes (the shapes are fixed by the seed, so every run checks the
-same cases): LCE forward and dL/dH for dense and 4-bit heads, and attention forward and gradients
-with causal and packed masks, against the CPU oracle, at the same tolerances as the fixed-shape
-tests (per-token NLL 2e-3 relative, 8e-3 absolute for the 4-bit head; gradients and O 1e-2
-relative-L2; L 2e-3)."""
+same cases): LCE forward and dL/dH for dense and 4-bit heads (and dL/dW for a trainable head), and
+attention forward and gradients with causal, non-causal and packed masks, against the CPU oracle,
+at the same tolerances as the fixed-shape tests (per-token NLL 2e-3 relative, 8e-3 absolute for
+the 4-bit head; gradients and O 1e-2 relative-L2; L 2e-3)."""
 from __future__ import annotations
 
 import math
@@ -31,6 +31,11 @@ ATTN_CASES = []
 for _ in range(10):
     _hkv, _g = _R.choice([1, 2, 4]), _R.choice([1, 2, 3, 4])
     ATTN_CASES.append((_R.randint(1, 2), _hkv * _g, _hkv, _R.randint(1, 700), _R.choice([64, 96, 128])))
+NONCAUSAL_CASES = []
+for _ in range(5):
+    _hkv, _g = _R.choice([1, 2]), _R.choice([1, 2, 4])
+    NONCAUSAL_CASES.append((_R.randint(1, 2), _hkv * _g, _hkv, _R.randint(1, 500), _R.choice([64, 96, 128])))
+DW_CASES = [(_R.randint(1, 600), _R.choice([64, 128, 200, 256, 384]), _R.randint(2, 4000)) for _ in range(5)]
 PACKED_CASES = []
 for _ in range(6):
     _lens = [_R.randint(1, 200) for _ in range(_R.randint(1, 6))]
@@ -83,10 +88,28 @@ def test_lce_random_quantized(n, d, v):
         assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
 
 
-def _check_attention(res, q, k, v, do, scale, seg_id=None):
+@pytest.mark.parametrize(("n", "d", "v"), DW_CASES)
+def test_lce_random_trainable_head(n, d, v):
+    from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
+
+    print(f"[lce random dw] n={n} d={d} v={v}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n * 13 + d + v)
+    hd = h.cuda().requires_grad_(True)
+    wd = w.cuda().requires_grad_(True)
+    nll, lse, _ = kernel_forward_parts(hd, DenseHead(weight=wd, trainable=True), t.cuda(), ignore_index=IGN)
+    ct = torch.rand(n, generator=torch.Generator().manual_seed(n + 2)) + 0.5
+    nll.backward(ct.cuda())
+    _, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
+    odh = olce.backward(h, w, t, olse, ct, ignore_index=IGN, dtype=torch.float64)
+    odw = olce.backward_dw(h, w, t, olse, ct, ignore_index=IGN)
+    assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
+    assert rel_l2(wd.grad.cpu(), odw) <= 1e-2
+
+
+def _check_attention(res, q, k, v, do, scale, seg_id=None, causal=True):
     o, lse, dq, dk, dv = res
-    oo, ol = oatt.attention_forward(q, k, v, scale=scale, causal=True, seg_id=seg_id, dtype=torch.float64)
-    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, causal=True, seg_id=seg_id,
+    oo, ol = oatt.attention_forward(q, k, v, scale=scale, causal=causal, seg_id=seg_id, dtype=torch.float64)
+    odq, odk, odv = oatt.attention_backward(q, k, v, oo, ol, do, scale=scale, causal=causal, seg_id=seg_id,
                                             dtype=torch.float64)
     assert rel_l2(o, oo) <= 1e-2 and (lse.double() - ol).abs().max() <= 2e-3
     for got, want in ((dq, odq), (dk, odk), (dv, odv)):
@@ -104,6 +127,15 @@ def test_attention_random_causal(shape):
     q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=5 * s + d + hq)
     scale = 1.0 / math.sqrt(d)
     _check_attention(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
+
+
+@pytest.mark.parametrize("shape", NONCAUSAL_CASES)
+def test_attention_random_noncausal(shape):
+    b, hq, hkv, s, d = shape
+    print(f"[attn random non-causal] {shape}", flush=True)
+    q, k, v, do = attn_inputs(b, hq, hkv, s, d, seed=11 * s + d + hq)
+    scale = 1.0 / math.sqrt(d)
+    _check_attention(_run_kernel(q, k, v, do, scale, causal=False), q, k, v, do, scale, causal=False)
 
 
 @pytest.mark.parametrize(("lengths", "hq", "hkv", "d"), PACKED_CASES)
