@@ -1,5 +1,6 @@
 """Bench harness: fused linear cross-entropy fwd+bwd on one MI355X, with the
-flash-attention (configs 4, 5), QLoRA (config 3), size ladders and CPU baselines reported beside it.
+flash-attention (configs 4, 5), QLoRA (config 3), a trainable-head step (dL/dW), size ladders and
+CPU baselines reported beside it.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--parts ...]
 
@@ -238,6 +239,40 @@ def bench_lce(steps, warmup, head_kind="dense"):
             "bwd_row_blocks": p.bwd_row_blocks, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks,
             "transposed_head_cache_gb": head_t / 1e9,
             "bwd_footprint_gb": (bwd_peak + head_t) / 1e9}
+
+
+def bench_trainable_lce(steps, warmup):
+    """LCE fwd+bwd with a trainable dense head at the flagship shape: dL/dH and dL/dW (the dW kernel,
+    one owner per (vocab, hidden) output tile). Four vocab-tile products per step (forward logits;
+    backward logits, dH and dW), 2 N V D flops each."""
+    import torch
+
+    from mlx_train_perf.core import loss as L
+    from mlx_train_perf.core.loss import DenseHead
+
+    h, w, t = lce_inputs_gpu(N, D, V)
+    wd = w.detach().requires_grad_(True)
+    head = DenseHead(weight=wd, trainable=True)
+    hd = h.detach().requires_grad_(True)
+    valid = (t != IGNORE)
+    ct = (valid.float() / valid.sum()).contiguous()
+
+    def step():
+        hd.grad = None
+        wd.grad = None
+        nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        nll.backward(ct)
+
+    sec = time_region(step, steps, warmup)
+    hd.grad = None
+    wd.grad = None
+    torch.cuda.empty_cache()
+    nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+    bwd_peak, _ = marginal_peak_bytes(lambda: nll.backward(ct))
+    flops = 4 * 2.0 * N * V * D
+    return {"ms_per_step": sec * 1e3, "tokens_per_s": N / sec, "step_tflops": flops / sec / 1e12,
+            "step_mfma_frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "bwd_marginal_peak_gb": bwd_peak / 1e9,
+            "products_per_step": 4}
 
 
 def lce_ladder(reps=10):
@@ -729,8 +764,8 @@ def main():
     ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
                     help="TRACE_CSV TITLE COMMAND [STATS_CSV]: summarize a rocprofv3 --kernel-trace csv (and the "
                          "same run's --stats csv) into markdown")
-    ap.add_argument("--parts", default="lce,qlora,attention,ladder",
-                    help="comma list of lce, qlora, attention, ladder (lce is the headline line)")
+    ap.add_argument("--parts", default="lce,qlora,trainable,attention,ladder",
+                    help="comma list of lce, qlora, trainable, attention, ladder (lce is the headline line)")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary))
@@ -803,6 +838,9 @@ def main():
             "ms_per_step": q4n["sec_per_step"] * 1e3, "tokens_per_s": N / q4n["sec_per_step"],
             "bwd_ms": q4n["bwd_ms"], "bwd_marginal_peak_gb": q4n["bwd_marginal_peak_gb"],
             "bwd_footprint_gb": q4n["bwd_footprint_gb"]}
+    if not args.no_extras and "trainable" in parts:
+        torch.cuda.empty_cache()
+        result["trainable_head_lce"] = bench_trainable_lce(max(3, args.steps // 4), 1)
     if not args.no_extras and "attention" in parts:
         torch.cuda.empty_cache()
         result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, "causal")
