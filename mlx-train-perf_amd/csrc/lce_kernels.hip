@@ -614,7 +614,7 @@ __device__ __forceinline__ auto& inline_op(OA& oa, OB& ob) {
 
 template <int PRE_VM = 0, class OA, class OB, class NEXT>
 __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x16 (&acc)[4][kNJ], bool pre,
-                                         bool has_next, const NEXT& next) {
+                                         bool has_next, const NEXT& next, long next_shift = 0) {
   constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
   const int w = threadIdx.x >> 6;
   constexpr bool kCopiers = OA::kPartner && OB::kPartner;
@@ -742,8 +742,19 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
         dma_mfma(ga, gb, acc);
         dma_sched_copy<NR>();
       } else if constexpr (R == 1) {
-        oa.issue2(kt + 2, cur, wsc, live);
-        ob.issue2(kt + 2, cur + 32768, wsc, live);
+        if constexpr (std::is_same<OA, DmaRowOp>::value && std::is_same<OB, DmaRowOp>::value) {
+          // With next_shift (the caller's next tile lies next_shift bytes on in A, both tiles whole,
+          // nk even), the copies of stage nk (past the end) carry the next tile's stage 0 instead:
+          // into this buffer, stage 0's, so they leave the window after the last barrier. Scalar
+          // selects keep the body branch-free.
+          const bool sel = next_shift != 0 && kt + 2 == nk;
+          const int ktv = sel ? 0 : kt + 2;
+          oa.issue2_at(sel ? next_shift : 0L, ktv, cur, wsc, live || sel);
+          ob.issue2(ktv, cur + 32768, wsc, live || sel);
+        } else {
+          oa.issue2(kt + 2, cur, wsc, live);
+          ob.issue2(kt + 2, cur + 32768, wsc, live);
+        }
         dma_read_frags(oa, ob, nxt, 0, fa, fb);
         dma_mfma(ga, gb, acc);
         dma_sched_mix<NR, 16>();
@@ -931,11 +942,14 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       // Both this tile and the next are whole: the next one reuses this tile's lane offsets.
       const bool next_whole = v0 + 2 * kTile <= V;
       // Only waves 0-3 copy the next tile's first two stages (theirs and their SIMD partner's, as
-      // in the stage loop): the other waves go straight on to the epilogue's exps meanwhile.
+      // in the stage loop): the other waves go straight on to the epilogue's exps meanwhile. When
+      // the next tile is whole and nk is even, its stage 0 already went out in the stage loop (in
+      // the slot of the copies past the end), and only stage 1 is left for here.
+      const bool early0 = has_next && next_whole && nk % 2 == 0;
       auto next = [&]() {
         if (wsc >= 4) return;
         if (next_whole) {
-          oa.issue2_at(tile_bytes, 0, lds, wsc);
+          if (!early0) oa.issue2_at(tile_bytes, 0, lds, wsc);
           if (nk > 1) oa.issue2_at(tile_bytes, 1, lds + kDmaStage, wsc);
         } else {
           DmaRowOp na;
@@ -943,11 +957,11 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
           na.issue2(0, lds, wsc);
           if (nk > 1) na.issue2(1, lds + kDmaStage, wsc);
         }
-        ob.issue2(0, lds + 32768, wsc);
+        if (!early0) ob.issue2(0, lds + 32768, wsc);
         if (nk > 1) ob.issue2(1, lds + kDmaStage + 32768, wsc);
       };
       f32x16 acc[4][kNJ];
-      gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next);
+      gemm_dma(oa, ob, nk, lds, acc, pre, has_next, next, early0 ? tile_bytes : 0L);
       pre = has_next;
       if (has_next) {
         if (next_whole) oa.base += tile_bytes;
@@ -1289,6 +1303,9 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
     const int v0 = v_begin + vt * kTile;
     const bool has_next = vt + 1 < vt_end;
     const bool next_whole = v0 + 2 * kTile <= vlim;
+    // Dense head, next tile whole, nk even: the next tile's stage 0 goes out in the stage loop (in
+    // the slot of the copies past the end), so only its stage 1 is left for here.
+    const bool early0 = !Q4 && has_next && next_whole && nk % 2 == 0;
     auto next = [&]() {
       if constexpr (Q4) {
         init_a(v0 + kTile);
@@ -1302,7 +1319,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
         // Every wave copies here (with only waves 0-3 copying, as in the forward, this kernel
         // measured 0.2% slower).
         if (next_whole) {
-          oa.issue_at(tile_bytes, 0, lds);
+          if (!early0) oa.issue_at(tile_bytes, 0, lds);
           oa.issue_at(tile_bytes, 1, lds + kDmaStage);
         } else {
           DmaRowOp na;
@@ -1311,11 +1328,11 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
           na.issue(1, lds + kDmaStage);
         }
       }
-      ob.issue(0, lds + 32768);
+      if (!early0) ob.issue(0, lds + 32768);
       ob.issue(1, lds + kDmaStage + 32768);
     };
     f32x16 acc[4][kNJ];
-    gemm_dma<kGStores>(oa, ob, nk, lds, acc, pre, has_next, next);
+    gemm_dma<kGStores>(oa, ob, nk, lds, acc, pre, has_next, next, early0 ? tile_bytes : 0L);
     if constexpr (!Q4) {
       if (has_next) {
         if (next_whole) oa.base += tile_bytes;
