@@ -1,6 +1,14 @@
-"""Bench harness: fused linear cross-entropy fwd+bwd on one MI355X, with the
+"""Bench harness: fused linear cross-entropy fwd+bwd on one MI355X (config 2), with the
 flash-attention (configs 4, 5), QLoRA (config 3), a trainable-head step (dL/dW), size ladders and
 CPU baselines reported beside it.
+
+The five workloads are the reference's published configurations, numbered as it numbers them:
+  1  LCE, N=1024, D=512, V=32000, fp32, 10% ignore_index (the CPU-runnable case);
+  2  LCE, N=8192 (batch 1 x seq 8192), D=4096, V=151936, bf16 dense frozen head (the headline);
+  3  config 2 with the head quantized to 4 bits (affine, groups of 64, bf16 scales and biases);
+  4  causal GQA flash attention, B=1, Hq=32, Hkv=8, S=8192, head_dim 128, bf16;
+  5  config 4's heads over a packed row of S=16384 tokens, document lengths uniform in
+     [64, 2048] from seed 0 (the last one truncated).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extras] [--parts ...]
 
@@ -66,7 +74,7 @@ def lce_inputs_gpu(n, d, v, seed=0, ignore_frac=0.05):
 
 
 def packed_lengths(total: int, lo: int = 64, hi: int = 2048, seed: int = 0) -> list[int]:
-    """document lengths uniform in [lo, hi] from `seed` until `total` is filled."""
+    """Config 5: document lengths uniform in [lo, hi] from `seed` until `total` is filled."""
     import random
 
     rng = random.Random(seed)
@@ -490,7 +498,7 @@ def cpu_baseline_lce(budget_s: float = 4.0):
 
 
 def cpu_baseline_c1():
-    """BASELINE config 1 in full: N=1024, D=512, V=32000 fp32, 10% ignore_index, fwd+bwd."""
+    """Config 1 in full: N=1024, D=512, V=32000 fp32, 10% ignore_index, fwd+bwd."""
     import torch
 
     from oracle import lce as olce

@@ -1,4 +1,5 @@
-"""Seeded synthetic inputs shared by the tests (BASELINE config shapes, scaled down where noted)."""
+"""Seeded synthetic inputs shared by the tests (the reference's published workload shapes, scaled
+down where noted)."""
 from __future__ import annotations
 
 import torch

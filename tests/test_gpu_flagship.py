@@ -1,4 +1,5 @@
-"""GPU parity at the BASELINE flagship configs, through the C-ABI, against the oracle in fp64.
+"""GPU parity at the reference's published flagship workloads (C2-C5 below), through the C-ABI,
+against the oracle in fp64.
 
 The oracle (oracle/lce.py, oracle/attention.py) is device-agnostic torch; here it runs in fp64 on the
 GPU so the full shapes finish in seconds:
@@ -60,7 +61,7 @@ def _rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
 
 
 def _c2_inputs(seed: int = 0):
-    """H ~ N(0,1) RMS-normalized, W ~ N(0, 0.02^2), targets uniform in [0, V) with
+    """Config 2 (N=8192, D=4096, V=151936): H ~ N(0,1) RMS-normalized, W ~ N(0, 0.02^2), targets uniform in [0, V) with
     round(0.05 N) = 410 rows (a seeded permutation) set to ignore_index; generated on the GPU."""
     g = torch.Generator(device="cuda").manual_seed(seed)
     h = torch.randn(N, D, generator=g, device="cuda")
