@@ -835,13 +835,18 @@ def main():
         # The same step without the cached bf16 transposed head (the dH product dequantizes the 4-bit
         # head in registers as well): the memory / time trade of MTP_LCE_TRANSPOSED_HEAD=0.
         from mlx_train_perf.core import loss as L
+        prev = os.environ.get("MTP_LCE_TRANSPOSED_HEAD")
         os.environ["MTP_LCE_TRANSPOSED_HEAD"] = "0"
         try:
             L.clear_transposed_head_cache()
             torch.cuda.empty_cache()
             q4n = bench_lce(3, 1, "q4")
         finally:
-            del os.environ["MTP_LCE_TRANSPOSED_HEAD"]
+            # the user's setting (or its absence) holds for the parts that follow
+            if prev is None:
+                del os.environ["MTP_LCE_TRANSPOSED_HEAD"]
+            else:
+                os.environ["MTP_LCE_TRANSPOSED_HEAD"] = prev
         result["qlora_lce"]["no_head_copy"] = {
             "ms_per_step": q4n["sec_per_step"] * 1e3, "tokens_per_s": N / q4n["sec_per_step"],
             "bwd_ms": q4n["bwd_ms"], "bwd_marginal_peak_gb": q4n["bwd_marginal_peak_gb"],

@@ -72,7 +72,9 @@ int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
  * in a fixed device array inside the library (one per GPU, held until the process ends), whose size
  * mtp_lce_fwd_noalloc_max_workspace_bytes() returns (4 MiB: n up to 524288 tokens at any v). A call
  * whose mtp_lce_fwd_workspace_bytes(n, d, v, head_kind) exceeds it returns MTP_ERR_WORKSPACE before
- * any launch. The first call on a device looks up that device's array address (no allocation).
+ * any launch. The array used is that of the device `stream` runs on (the current device for the
+ * null stream), whatever device the calling thread has current; the first call on a device looks
+ * up that device's array address (no allocation).
  * Outputs are bitwise those of mtp_lce_fwd. Calls on one GPU share its array: two calls whose work
  * overlaps in time on that GPU (different streams, or different host threads) race on it.
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code under

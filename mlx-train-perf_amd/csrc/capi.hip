@@ -96,18 +96,31 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// The current device's address of `scratch`, looked up on the first call on that device.
-int scratch_for_current_device(void** out) {
-  int dev = -1;
-  hipError_t e = hipGetDevice(&dev);
+// The address of `scratch` on the device that runs `stream` (the current device for the null
+// stream), looked up on the first call on that device with that device current. The launch goes to
+// `stream`, so the scratch must be that device's copy whatever device the calling thread has current.
+int scratch_for_stream(hipStream_t stream, void** out) {
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "hipGetDevice failed: %s", hipGetErrorString(e));
+  int dev = cur;
+  if (stream) {
+    hipDevice_t sd = -1;
+    e = hipStreamGetDevice(stream, &sd);
+    if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+    dev = sd;
+  }
   if (dev < 0 || dev >= kMaxDevices) return fail(MTP_ERR_RUNTIME, "device index %d out of range", dev);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(MTP_ERR_RUNTIME, "hipSetDevice(%d) failed: %s", dev, hipGetErrorString(e));
     void* p = nullptr;
     e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    const hipError_t er = dev != cur ? hipSetDevice(cur) : hipSuccess;
     if (e != hipSuccess || !p)
       return fail(MTP_ERR_RUNTIME, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    if (er != hipSuccess) return fail(MTP_ERR_RUNTIME, "hipSetDevice(%d) failed: %s", cur, hipGetErrorString(er));
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
@@ -158,7 +171,7 @@ int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, 
     return fail(MTP_ERR_WORKSPACE, "mtp_lce_fwd_noalloc: n=%lld, v=%lld needs %zu bytes of scratch, above its fixed "
                 "%zu; use mtp_lce_fwd with a caller workspace", (long long)n, (long long)v, need, kNoAllocScratchBytes);
   void* ws = nullptr;
-  rc = scratch_for_current_device(&ws);
+  rc = scratch_for_stream(static_cast<hipStream_t>(stream), &ws);
   if (rc) return rc;
   // Every partial the forward reads is written by the same launch before it is read (one entry
   // per vocab split and token), so the scratch needs no clearing between calls.
@@ -274,6 +287,8 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   if (rc) return rc;
   if (w_t && !aligned16(w_t)) return fail(MTP_ERR_UNSUPPORTED, "w_t must be 16-byte aligned");
   if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
+  if (!aligned16(d_hidden) || (d_w && !aligned16(d_w)))
+    return fail(MTP_ERR_UNSUPPORTED, "d_hidden and d_w must be 16-byte aligned");
   if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
@@ -337,6 +352,7 @@ int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   const size_t need = mtp_attn_bwd_workspace_bytes(b, hq, hkv, s, dh);
   if (!workspace || workspace_bytes < need)
     return fail(MTP_ERR_WORKSPACE, "attention backward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
   mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale, (int)causal};
   hipError_t e = mtp::launch_attn_bwd(sh, static_cast<const mtp::bf16_t*>(q), static_cast<const mtp::bf16_t*>(k),
                                       static_cast<const mtp::bf16_t*>(v), static_cast<const mtp::bf16_t*>(o), lse,

@@ -137,3 +137,10 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 def stream_of(t: torch.Tensor) -> int:
     return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def on_device(t: torch.Tensor):
+    """Context that makes t's GPU the current device for a C-ABI call. The launches go to t's stream;
+    HIP calls inside the library that act on the current device (the no-allocation forward's scratch
+    lookup, error queries) then see the same device whatever the caller had current."""
+    return torch.cuda.device(t.device)

@@ -180,9 +180,10 @@ def kernel_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: 
     hkv = k.shape[1]
     o = torch.empty_like(q)
     lse = torch.empty((b, hq, n), dtype=torch.float32, device=q.device)
-    rc = lib.mtp_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale), int(causal),
-                          _native.ptr(seg_id), _native.ptr(seg_start), o.data_ptr(), lse.data_ptr(),
-                          _native.stream_of(q))
+    with _native.on_device(q):
+        rc = lib.mtp_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale),
+                              int(causal), _native.ptr(seg_id), _native.ptr(seg_start), o.data_ptr(),
+                              lse.data_ptr(), _native.stream_of(q))
     _native.check(rc, domain="attention")
     return o, lse
 
@@ -197,9 +198,11 @@ def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_star
     dv = torch.empty_like(v)
     ws_bytes = lib.mtp_attn_bwd_workspace_bytes(b, hq, hkv, n, dh)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
-    rc = lib.mtp_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), d_o.data_ptr(),
-                          b, hq, hkv, n, dh, float(scale), int(causal), _native.ptr(seg_id), _native.ptr(seg_start),
-                          dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(q))
+    with _native.on_device(q):
+        rc = lib.mtp_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
+                              d_o.data_ptr(), b, hq, hkv, n, dh, float(scale), int(causal), _native.ptr(seg_id),
+                              _native.ptr(seg_start), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
+                              ws_bytes, _native.stream_of(q))
     _native.check(rc, domain="attention")
     return dq, dk, dv
 

@@ -16,8 +16,9 @@ Two model shapes are served:
 
 Refusals (`UnsupportedAttentionError`, at enable time): sliding-window or mixed `layer_types`,
 configured attention dropout, head_dim outside {64, 96, 128}, an unrecognised model shape.
-There is no rate calibration on MI355X, so `seq_len`/`batch_size`/`packed` only validate the
-launch plan up front (`plan/launch.py`); nothing is pre-warmed.
+There is no rate calibration on MI355X. With `seq_len` (and `batch_size`, `packed`) the launch
+plan is validated up front (`plan/launch.py`), and a model already on the GPU runs one zeros
+forward + backward at that shape, which loads the kernels a training step will launch.
 """
 from __future__ import annotations
 
@@ -187,13 +188,46 @@ def _refusals(cfg: Any, layers: Any) -> int:
     return head_dim
 
 
+def _model_device_dtype(model: Any) -> tuple[torch.device, torch.dtype] | None:
+    for p in model.parameters():
+        if p.is_floating_point():
+            return p.device, p.dtype
+    return None
+
+
+def _prewarm(model: Any, *, impl: str, seq_len: int, batch_size: int, hq: int, hkv: int, head_dim: int,
+             packed: bool) -> None:
+    """One zeros forward + backward at the training shape (the counterpart of the reference's
+    `_prewarm_rate_caches`, wrapper.py:170-202), so the first training step does not pay for loading
+    the kernels' code objects; with `packed`, a second one with a single-segment `PackedMask`, which
+    runs the packed instantiations and the backward's work-order sort. A model on the CPU skips it
+    (there is nothing to load), as does a dtype the kernels do not take."""
+    where = _model_device_dtype(model)
+    if where is None or where[0].type != "cuda" or where[1] != torch.bfloat16:
+        return
+    dev, dt = where
+    q = torch.zeros((batch_size, hq, seq_len, head_dim), dtype=dt, device=dev, requires_grad=True)
+    k = torch.zeros((batch_size, hkv, seq_len, head_dim), dtype=dt, device=dev, requires_grad=True)
+    v = torch.zeros((batch_size, hkv, seq_len, head_dim), dtype=dt, device=dev, requires_grad=True)
+    masks: list[PackedMask | None] = [None]
+    if packed:
+        z = torch.zeros((batch_size, seq_len), dtype=torch.int32, device=dev)
+        masks.append(PackedMask(seg_id=z, seg_start=z))
+    for seg in masks:
+        out = flash_attention(q, k, v, scale=1.0 / head_dim ** 0.5, causal=True, impl=impl, segments=seg)  # type: ignore[arg-type]
+        out.backward(torch.zeros_like(out))
+
+
 def enable_flash_attention(model: Any, *, impl: str = "auto", seq_len: int | None = None, batch_size: int = 1,
                            packed: bool = False) -> None:
     """Enable the flash-attention training path on `model` in place (wrapper.py:205-292).
 
     `impl`: forwarded to `flash_attention` per call ("auto"/"kernel" -> HIP kernels,
-    "reference" -> the materialized oracle, small shapes only). `seq_len`/`batch_size`: when given,
-    the launch plan for that shape is computed now so an unsupported shape fails at enable time."""
+    "reference" -> the materialized oracle, small shapes only). `seq_len`/`batch_size`: when given
+    with a kernel impl, the launch plan for that shape is computed now, so an unsupported shape fails
+    at enable time, and a model already on the GPU in bf16 runs one zeros forward + backward at that
+    shape (`packed=True`: also one with a single-segment `PackedMask`, the packed kernels a
+    `mtp_segments=` / `PackedMask` step will launch), as the reference pre-warms its rate caches."""
     cfg = _config_of(model)
     inner = getattr(model, "model", None)
     layers = getattr(inner, "layers", None)
@@ -228,7 +262,10 @@ def enable_flash_attention(model: Any, *, impl: str = "auto", seq_len: int | Non
         hkv = int(getattr(cfg, "num_key_value_heads", hq) or hq)
         if hq % hkv:
             raise UnsupportedAttentionError(f"Hq={hq} must be a multiple of Hkv={hkv}")
-        _plan.attn_plan(b=batch_size, hq=hq, hkv=hkv, s=seq_len)
+        head_dim = _head_dim(cfg)
+        _plan.attn_plan(b=batch_size, hq=hq, hkv=hkv, s=seq_len, dh=head_dim)
+        _prewarm(model, impl=impl, seq_len=seq_len, batch_size=batch_size, hq=hq, hkv=hkv, head_dim=head_dim,
+                 packed=packed)
 
 
 def is_enabled(model: Any) -> bool:

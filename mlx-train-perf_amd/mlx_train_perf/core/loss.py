@@ -274,8 +274,10 @@ def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_ki
                 return e[1]
         lib = _native.load()
         wt = torch.empty((d, lib.mtp_lce_head_t_ld(v)), dtype=torch.bfloat16, device=owner.device)
-        rc = lib.mtp_lce_head_transpose(_native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases),
-                                        v, d, head_kind, wt.data_ptr(), _native.stream_of(owner))
+        with _native.on_device(owner):
+            rc = lib.mtp_lce_head_transpose(_native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
+                                            _native.ptr(biases), v, d, head_kind, wt.data_ptr(),
+                                            _native.stream_of(owner))
         _native.check(rc, domain="loss")
         ents.append(((weakref.ref(owner),) + key, wt))
         del ents[:-_head_t_capacity()]
@@ -297,10 +299,11 @@ class _KernelLCE(torch.autograd.Function):
         tgt = torch.empty(n, dtype=torch.float32, device=dev)
         ws_bytes = lib.mtp_lce_fwd_workspace_bytes(n, d, v, head_kind)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-        rc = lib.mtp_lce_fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
-                             _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ignore_index,
-                             nll.data_ptr(), lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), ws_bytes,
-                             _native.stream_of(hidden2))
+        with _native.on_device(hidden2):
+            rc = lib.mtp_lce_fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
+                                 _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ignore_index,
+                                 nll.data_ptr(), lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), ws_bytes,
+                                 _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         ctx.save_for_backward(hidden2, targets2, lse)
         ctx.head = (w, w_q, scales, biases, head_kind, v)
@@ -331,10 +334,11 @@ class _KernelLCE(torch.autograd.Function):
         d_hidden = torch.empty_like(hidden2)
         w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
         ct = d_nll.to(torch.float32).contiguous()
-        rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),
-                             _native.ptr(scales), _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind,
-                             ctx.ignore_index, lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(),
-                             _native.ptr(d_w), chunk, rows, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
+        with _native.on_device(hidden2):
+            rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),
+                                 _native.ptr(scales), _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind,
+                                 ctx.ignore_index, lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(),
+                                 _native.ptr(d_w), chunk, rows, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         return d_hidden, None, d_w, None, None, None, None, None, None, None
 

@@ -6,7 +6,8 @@ build's kernels and workspaces:
 - loss layer (`_loss_bytes`, plan/estimate.py:252-271): kernel forward = the three fp32 outputs
   plus the vocab-split partials; the backward adds the bf16 gradient chunk and (multi-chunk) the
   fp32 dH accumulator; chunked = fp32 logits chunk x 3; naive = the full (N, V) fp32 logits plus
-  softmax intermediates;
+  softmax intermediates; a trainable head adds its dL/dW (the reference's `d_w` term) and takes
+  every row in one backward block; the kernel backward also keeps a transposed copy of the head;
 - flash-attention saved state (`_flash_saved_state_bytes`, plan/estimate.py:210-220): O in the
   compute dtype plus the fp32 L per layer, and the backward's fp32 D vector.
 Whole-model terms (weights, optimizer, activations) are caller-supplied because they depend on the
@@ -14,6 +15,7 @@ model, not on this path.
 """
 from __future__ import annotations
 
+import os
 from dataclasses import dataclass, field
 
 from mlx_train_perf.errors import DoesNotFitError, PlanInputError
@@ -34,22 +36,54 @@ def dtype_bytes(dtype: str) -> int:
 class LossBytes:
     forward_peak: int
     backward_workspace: int
+    # The backward's cached transposed head (kernel impl; resident from the first backward for as
+    # long as the head lives, so it adds to the forward of later steps too).
+    transposed_head: int = 0
+    # dL/dW of a trainable head, in the head's dtype (the reference's `d_w` term,
+    # plan/estimate.py:245-271).
+    head_grad: int = 0
+
+    @property
+    def backward_peak(self) -> int:
+        return self.backward_workspace + self.head_grad
+
+    @property
+    def peak(self) -> int:
+        """The loss layer's peak over a training step, beyond its inputs and dH."""
+        return self.transposed_head + max(self.forward_peak, self.backward_peak)
+
+
+def transposed_head_bytes(*, d: int, v: int, enabled: bool | None = None) -> int:
+    """One cached transposed head, bf16 [d][round_up(v, 256) + 64] (mtp_lce_head_t_ld), which the
+    kernel backward keeps per head when `MTP_LCE_TRANSPOSED_HEAD` is not "0" and d % 64 == 0."""
+    if enabled is None:
+        enabled = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "1") != "0"
+    if not enabled or d % 64:
+        return 0
+    return d * (-(-v // _launch.TILE) * _launch.TILE + _launch.G_PITCH_PAD) * 2
 
 
 def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf16", chunk: int | None = None,
-               bwd_budget: int | None = None) -> LossBytes:
-    """Loss-layer memory beyond its inputs: forward marginal peak and backward workspace.
-    The backward's returned dH (n*d*dtype) is the caller's gradient, not counted here."""
+               bwd_budget: int | None = None, trainable: bool = False,
+               transposed_head: bool | None = None) -> LossBytes:
+    """Loss-layer memory beyond its inputs: forward marginal peak, backward workspace, and (kernel
+    impl) the cached transposed head; a trainable head adds its dL/dW and, on the kernel impl, takes
+    every row in one backward block. The backward's returned dH (n*d*dtype) is the caller's gradient,
+    not counted here."""
     if n < 1 or d < 1 or v < 1:
         raise PlanInputError("n, d, v must be >= 1")
     eb = dtype_bytes(dtype)
+    head_grad = v * d * eb if trainable else 0
     if impl == "kernel":
         fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)
         if chunk:
             bwd = _launch.lce_bwd_workspace_bytes(n, d, v, chunk) + n * 4
         else:
-            p = _launch.lce_plan(n=n, v=v, d=d, budget=bwd_budget or _launch.lce_bwd_budget_bytes())
+            p = _launch.lce_plan(n=n, v=v, d=d, budget=bwd_budget or _launch.lce_bwd_budget_bytes(),
+                                 trainable=trainable)
             bwd = p.bwd_workspace_bytes + n * 4
+        return LossBytes(forward_peak=fwd, backward_workspace=bwd, head_grad=head_grad,
+                         transposed_head=transposed_head_bytes(d=d, v=v, enabled=transposed_head))
     elif impl == "chunked":
         c = chunk or 8192
         fwd = 3 * n * min(c, v) * 4 + 2 * n * 4
@@ -59,7 +93,7 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
         bwd = 2 * n * v * 4
     else:
         raise PlanInputError(f"unknown impl {impl!r}; expected 'naive', 'chunked', or 'kernel'")
-    return LossBytes(forward_peak=fwd, backward_workspace=bwd)
+    return LossBytes(forward_peak=fwd, backward_workspace=bwd, head_grad=head_grad)
 
 
 def flash_saved_state_bytes(*, batch: int, seq_len: int, heads: int, head_dim: int, dtype: str = "bf16") -> int:
@@ -83,12 +117,15 @@ class Plan:
 
 def estimate_peak(*, n_layers: int, batch: int, seq_len: int, hidden: int, vocab: int, heads: int, kv_heads: int,
                   head_dim: int, dtype: str = "bf16", attention: str = "flash", loss_impl: str = "kernel",
-                  weights_bytes: int = 0, optimizer_bytes: int = 0, activation_bytes: int = 0) -> Plan:
-    """Predicted peak bytes of a training step: hot-path terms computed here, model terms supplied."""
+                  weights_bytes: int = 0, optimizer_bytes: int = 0, activation_bytes: int = 0,
+                  trainable_head: bool = False) -> Plan:
+    """Predicted peak bytes of a training step: hot-path terms computed here, model terms supplied.
+    `trainable_head` (full fine-tuning; the reference's `lora_rank == 0`, plan/estimate.py:245-250)
+    adds the head's dL/dW and plans the loss backward with every row in one block."""
     if heads % kv_heads:
         raise PlanInputError(f"heads={heads} must be a multiple of kv_heads={kv_heads}")
     n = batch * seq_len
-    lb = loss_bytes(n=n, d=hidden, v=vocab, impl=loss_impl, dtype=dtype)
+    lb = loss_bytes(n=n, d=hidden, v=vocab, impl=loss_impl, dtype=dtype, trainable=trainable_head)
     if attention == "flash":
         attn = n_layers * flash_saved_state_bytes(batch=batch, seq_len=seq_len, heads=heads, head_dim=head_dim,
                                                   dtype=dtype) + batch * heads * seq_len * 4
@@ -98,7 +135,7 @@ def estimate_peak(*, n_layers: int, batch: int, seq_len: int, hidden: int, vocab
         raise PlanInputError(f"unknown attention {attention!r}; expected 'stock' or 'flash'")
     return Plan(components={
         "weights": weights_bytes, "optimizer": optimizer_bytes, "activations": activation_bytes,
-        "attention": attn, "loss": max(lb.forward_peak, lb.backward_workspace),
+        "attention": attn, "loss": lb.peak,
     })
 
 

@@ -137,7 +137,7 @@ def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int |
     """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD], the fp32 dH accumulator when >1 chunk,
     and the fp32 part tiles of a split dH product (the most any row block and chunk takes)."""
     chunk = min(chunk, -(-v // TILE) * TILE)
-    rows = n if not row_block or row_block > n else row_block
+    rows = n if not row_block or row_block < 1 or row_block > n else row_block
     nchunks = -(-v // chunk)
     last_rows = n - (n - 1) // rows * rows
     last_tiles = -(-(v - (v - 1) // chunk * chunk) // TILE)

@@ -128,7 +128,7 @@ class _Rope(torch.nn.Module):
         self.register_buffer("inv", base ** (-torch.arange(0, dim, 2).float() / dim), persistent=False)
 
     def forward(self, x):
-        pos = torch.arange(x.shape[-2], dtype=torch.float32)
+        pos = torch.arange(x.shape[-2], dtype=torch.float32, device=x.device)
         ang = pos[:, None] * self.inv[None]
         cos, sin = ang.cos().to(x.dtype), ang.sin().to(x.dtype)
         x1, x2 = x[..., : x.shape[-1] // 2], x[..., x.shape[-1] // 2:]

@@ -67,7 +67,8 @@ def test_plans_agree_over_random_shapes(n, d, v, budget_log2):
     assert c == plan.lce_bwd_chunk(n, d, v, budget)
     rb = lib.mtp_lce_bwd_row_block(n, d, v, budget)
     assert rb == plan.lce_bwd_row_block(n, d, v, budget)
-    for rows in (0, n, rb):
+    # 0, a negative count and one above n all mean every row (capi.hip clamps row_block < 1 to n)
+    for rows in (0, -1, -rb, n, n + 1, rb):
         assert lib.mtp_lce_bwd_workspace_bytes(n, d, v, 0, c, rows) == plan.lce_bwd_workspace_bytes(n, d, v, c, rows)
 
 

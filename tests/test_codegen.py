@@ -1,13 +1,16 @@
-"""Code-generation check of this build's own gfx950 code objects (CPU lane).
+"""Code-generation checks of this build's own gfx950 code objects (CPU lane). Each disassembles the
+objects `build()` leaves in `mlx-train-perf_amd/_build/` (the device code object of each, unbundled
+from its fat binary).
 
-A vector store wider than 8 bytes reads its data registers over several cycles, and the compiler
-emits no wait state before a VALU write of those registers when a buffer store takes an SGPR
-offset. Gradient-tile variants whose 16-byte stores were followed at once by such writes gave
-intermittently wrong rows (the pair was one of two suspects; neither was isolated). The shipped
-kernels have no such pair, and this test keeps it that way: it disassembles the objects
-`build()` leaves in `mlx-train-perf_amd/_build/` (the device code object of each, unbundled from
-its fat binary) and fails if a 12- or 16-byte store's data registers are written by either of the
-next two instructions with no `s_nop` between."""
+1. Wide stores: a 12- or 16-byte store's data registers written by either of the next two
+   instructions with no `s_nop` between. Reverted gradient-tile variants with 16-byte stores had
+   this pattern and gave intermittently wrong rows. It is a guard, not an explanation: the
+   documented gfx9 rule (LLVM's GCNHazardRecognizer::createsVALUHazard) asks for that wait state
+   only when the store's soffset is not a register, and those stores took an SGPR soffset, so this
+   pair is probably not what went wrong.
+2. Lane swaps: a `v_permlane{16,32}_swap` whose operands a VALU op writes within 2 wait states
+   (or whose exec a `v_cmpx` writes within 4), the gfx950 hazard the reverted variant's swaps also
+   came close to. The shipped kernels' swaps are inline asm with `s_nop 1` before them."""
 from __future__ import annotations
 
 import re
@@ -83,3 +86,69 @@ def test_the_check_finds_the_pattern():
     ok = ["buffer_store_dwordx4 v[114:117], v255, s[16:19], s2 offen", "s_nop 0", "v_fma_f32 v114, v122, s68, -v229"]
     other = ["global_store_dwordx4 v[18:19], v[14:17], off", "v_mov_b32 v18, 0"]  # rewrites the address only
     assert _store_data_hazards(bad) and not _store_data_hazards(ok) and not _store_data_hazards(other)
+
+
+# gfx950 lane-swap hazards (the VALU-write -> v_permlane{16,32}_swap rule of the gfx950 ISA's hazard
+# table, as LLVM's GCNHazardRecognizer::checkPermlaneHazards applies it): a VALU write of either
+# operand register needs 2 wait states before the swap reads it, and a v_cmpx writing exec needs 4.
+# Every wait state is one instruction, s_nop N counts N + 1.
+SWAP = re.compile(r"^v_permlane(16|32)_swap_b32(_e32|_e64)?\s+(v\d+),\s*(v\d+)")
+_VALU_WAITS, _VCMPX_WAITS = 2, 4
+
+
+def _wait_states(ln: str) -> int:
+    m = re.match(r"^s_nop\s+(\d+|0x[0-9a-fA-F]+)", ln)
+    return int(m.group(1), 0) + 1 if m else 1
+
+
+def _permlane_swap_hazards(lines: list[str]) -> tuple[int, list[str]]:
+    """(swaps seen, swaps whose operands a VALU op writes, or whose exec a v_cmpx writes, closer than
+    the rule allows), scanning back through the preceding instructions of the listing."""
+    n, hits = 0, []
+    code = [ln for ln in lines if ln and not ln.endswith(">:") and not ln.startswith(("Disassembly", "<"))]
+    for i, ln in enumerate(code):
+        m = SWAP.match(ln)
+        if not m:
+            continue
+        n += 1
+        regs = _vgprs(m.group(3)) | _vgprs(m.group(4))
+        waited = 0
+        for prev in reversed(code[max(0, i - 8):i]):
+            if prev.startswith("s_endpgm") or prev.startswith("s_branch"):
+                break   # a block boundary: nothing before it falls through to the swap
+            v = VALU_DST.match(prev)
+            if v and waited < _VALU_WAITS and _vgprs(v.group(2)) & regs:
+                hits.append(f"{prev}  ->({waited} wait states)->  {ln}")
+                break
+            if prev.startswith("v_cmpx") and waited < _VCMPX_WAITS:
+                hits.append(f"{prev}  ->({waited} wait states, exec)->  {ln}")
+                break
+            waited += _wait_states(prev)
+            if waited >= _VCMPX_WAITS:
+                break
+    return n, hits
+
+
+def test_permlane_swap_operands_are_not_written_within_the_hazard_window(tmp_path):
+    objs = sorted(OBJ_DIR.glob("*.o"))
+    if not objs or not (LLVM / "llvm-objdump").exists() or shutil.which(str(LLVM / "clang-offload-bundler")) is None:
+        pytest.skip("built objects or the ROCm LLVM tools are not here (run build() first)")
+    swaps, hits = 0, []
+    for obj in objs:
+        n, h = _permlane_swap_hazards(_disassemble(obj, tmp_path))
+        swaps += n
+        hits += [f"{obj.name}: {x}" for x in h]
+    assert swaps > 0, "no lane swaps found: the attention kernels' row-maximum exchange should use them"
+    assert not hits, "\n".join(hits)
+
+
+def test_the_swap_check_finds_the_pattern():
+    """The scanner itself: a write one wait state before the swap (the reverted variant's pattern) and
+    a v_cmpx within 4 are caught; s_nop 1 (2 wait states) after the last write passes."""
+    one = ["v_mov_b32_e32 v128, v127", "s_nop 0", "v_permlane32_swap_b32_e32 v128, v127"]
+    ok = ["v_max3_f32 v127, v127, v64, v128", "v_mov_b32_e32 v128, v127", "s_nop 1",
+          "v_permlane32_swap_b32_e32 v128, v127"]
+    cmpx = ["v_cmpx_gt_f32_e32 vcc, v1, v2", "s_nop 1", "v_permlane32_swap_b32_e32 v8, v9"]
+    other_reg = ["v_mov_b32_e32 v5, v127", "v_permlane32_swap_b32_e32 v128, v127"]
+    assert _permlane_swap_hazards(one)[1] and _permlane_swap_hazards(cmpx)[1]
+    assert not _permlane_swap_hazards(ok)[1] and not _permlane_swap_hazards(other_reg)[1]

@@ -38,16 +38,81 @@ def test_flash_attention_kernel_matches_eager_logits():
     assert VJP_CALLS.get("flash_attention_kernel_bwd", 0) > before
 
 
-def test_loss_fn_kernel_matches_naive():
+def _default_loss_by_hand(m, batch, lengths):
+    """The mlx-lm trainer's `default_loss` written out independently of the adapter: the model's own
+    trunk, fp64 logits against its lm_head, and the (offset, length) window walked token by token
+    (inputs = batch[:, :-1], targets = batch[:, 1:], step j + 1 counted iff offset <= j + 1 <= length;
+    loss = summed NLL / counted tokens)."""
+    with torch.no_grad():
+        hid = m.model(input_ids=batch[:, :-1]).last_hidden_state.double().cpu()
+    w = m.lm_head.weight.double().cpu()
+    logp = torch.log_softmax(hid @ w.T, dim=-1)
+    tg = batch[:, 1:].cpu()
+    total, count = 0.0, 0
+    for r in range(batch.shape[0]):
+        off, length = (int(x) for x in lengths[r])
+        for j in range(tg.shape[1]):
+            if off <= j + 1 <= length:
+                total -= float(logp[r, j, tg[r, j]])
+                count += 1
+    return total / count, count
+
+
+def test_loss_fn_kernel_matches_default_loss_by_hand():
+    """make_loss_fn on the kernel impl against the documented trainer contract computed without the
+    adapter (a mask or normalization bug in the adapter cannot cancel here)."""
     from mlx_train_perf.adapters.transformers_lm import make_loss_fn
 
     m = _model()
     g = torch.Generator(device="cuda").manual_seed(2)
-    batch = torch.randint(0, 512, (2, 65), device="cuda", generator=g)
-    lengths = torch.tensor([[1, 64], [5, 40]], device="cuda")
+    batch = torch.randint(0, 512, (3, 65), device="cuda", generator=g)
+    lengths = torch.tensor([[1, 64], [5, 40], [64, 64]], device="cuda")
+    want, count = _default_loss_by_hand(m, batch, lengths)
     lk, nk = make_loss_fn(m, impl="kernel")(m, batch, lengths)
-    ln, nn_ = make_loss_fn(m, impl="naive")(m, batch, lengths)
-    assert int(nk) == int(nn_) and abs(lk.item() - ln.item()) < 2e-3 * abs(ln.item())
+    assert int(nk) == count == 64 + 36 + 1
+    assert abs(lk.item() - want) < 2e-3 * abs(want), (lk.item(), want)
+
+
+def test_mlx_style_wrapper_on_kernel_matches_stock():
+    """FlashAttentionWrapper (the mlx-lm-shaped module surgery) with impl="kernel" on the GPU: output
+    and input gradient against the stock block, computed in fp32 on the CPU; the kernel backward runs."""
+    from test_adapters import _mlx_style_model
+
+    from mlx_train_perf.attention import FlashAttentionWrapper, enable_flash_attention
+    from mlx_train_perf.attention.api import VJP_CALLS
+
+    print("[mlx-style FlashAttentionWrapper impl=kernel]", flush=True)
+    stock = _mlx_style_model(layers=1).float()
+    gpu = _mlx_style_model(layers=1).to("cuda", torch.bfloat16)
+    x = torch.randn(2, 130, 64, generator=torch.Generator().manual_seed(6)).to(torch.bfloat16)
+    xr = x.float().requires_grad_(True)
+    ref = stock.model.layers[0].self_attn(xr)
+    ref.backward(torch.ones_like(ref))
+    enable_flash_attention(gpu, impl="kernel", seq_len=130, batch_size=2)
+    wrap = gpu.model.layers[0].self_attn
+    assert isinstance(wrap, FlashAttentionWrapper)
+    xg = x.cuda().requires_grad_(True)
+    before = VJP_CALLS.get("flash_attention_kernel_bwd", 0)
+    out = wrap(xg, mask="causal")
+    out.backward(torch.ones_like(out))
+    assert VJP_CALLS.get("flash_attention_kernel_bwd", 0) == before + 1
+    e_out = float((out.float().cpu() - ref.detach()).norm() / ref.detach().norm())
+    e_dx = float((xg.grad.float().cpu() - xr.grad).norm() / xr.grad.norm())
+    assert e_out < 2e-2 and e_dx < 3e-2, (e_out, e_dx)
+
+
+def test_enable_prewarms_causal_and_packed_kernels():
+    """enable_flash_attention(seq_len=, packed=True) runs the causal and the packed kernels once at the
+    hinted shape (forward and backward), as the reference pre-warms its packed-keyed rate slots."""
+    from mlx_train_perf.attention import enable_flash_attention
+    from mlx_train_perf.attention.api import VJP_CALLS
+
+    m = _model()
+    before = VJP_CALLS.get("flash_attention_kernel_bwd", 0)
+    enable_flash_attention(m, impl="kernel", seq_len=96, batch_size=2, packed=True)
+    assert VJP_CALLS.get("flash_attention_kernel_bwd", 0) == before + 2
+    enable_flash_attention(m, impl="kernel", seq_len=96, batch_size=2)
+    assert VJP_CALLS.get("flash_attention_kernel_bwd", 0) == before + 3
 
 
 def test_packed_loss_kernel_path_runs_and_matches_reference_attention():

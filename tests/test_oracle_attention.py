@@ -121,7 +121,22 @@ def test_single_segment_is_causal():
 
 def test_packed_layout_generator():
     lens = oa.packed_layout(16384, 64, 2048, seed=0)
-    assert sum(lens) == 16384 and all(1 <= n <= 2048 for n in lens)
+    assert sum(lens) == 16384
+    # every document drawn in [64, 2048]; only the last is truncated to fill the row exactly
+    assert all(64 <= n <= 2048 for n in lens[:-1]) and 1 <= lens[-1] <= 2048
+    assert sum(lens[:-1]) < 16384
+    # the seed-0 layout: 13 documents and 12,388,368 visible pairs per head (the Python
+    # random.Random(0) figures quoted for the packed workload, 134.2M when fully causal)
+    assert len(lens) == 13
+    assert sum(n * (n + 1) // 2 for n in lens) == 12_388_368
     sid, sst = oa.segments_from_lengths(lens)
     assert sid[0] == 0 and (sid[1:] >= sid[:-1]).all() and (sst[1:] >= sst[:-1]).all()
     assert (sst <= torch.arange(16384)).all()
+    # gapless ids (steps of 0 or 1) and seg_start = the first position holding the same id
+    assert set((sid[1:] - sid[:-1]).tolist()) <= {0, 1}
+    first = {}
+    for i, s_ in enumerate(sid.tolist()):
+        first.setdefault(s_, i)
+    assert sst.tolist() == [first[s_] for s_ in sid.tolist()]
+    # a different seed gives a different layout (the seed is used)
+    assert oa.packed_layout(16384, 64, 2048, seed=1) != lens

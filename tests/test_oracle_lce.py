@@ -110,6 +110,58 @@ def test_planted_mistakes_fail_autograd_pin(mistake):
     assert not torch.allclose(bad, _autograd_dh(h, w, t, ct), atol=1e-6)
 
 
+def _rne_bf16_bits(x: torch.Tensor) -> torch.Tensor:
+    """bf16 round-to-nearest-even of fp32 values by integer arithmetic on their bits (add 0x7FFF plus
+    the lowest kept bit, clear the low 16 bits): independent of torch's bf16 cast. Finite inputs only."""
+    b = x.to(torch.float32).view(torch.int32).to(torch.int64) & 0xFFFFFFFF
+    b = (b + 0x7FFF + ((b >> 16) & 1)) & 0xFFFF0000
+    return (b - ((b >> 31) << 32)).to(torch.int32).view(torch.float32)
+
+
+def test_bf16_round_known_answers():
+    """olce._bf16_round: bf16 keeps 8 significant bits and rounds half to even (not fp16's 11 bits,
+    not truncation, not the identity)."""
+    x = torch.tensor([1.0, 1 + 2**-8, 1 + 3 * 2**-9, 1 + 2**-9, 1 + 2**-7 + 2**-8, -(1 + 3 * 2**-9), 3.0e-5 * (1 + 2**-9),
+                      65504.0 * 4, 2**-130], dtype=torch.float32)
+    want = torch.tensor([1.0, 1.0, 1 + 2**-7, 1.0, 1 + 2**-6, -(1 + 2**-7), 3.0e-5, 2.0**18, 2**-130],
+                        dtype=torch.float32)
+    # 1 + 2^-8 is halfway between 1 and 1 + 2^-7: ties go to the even mantissa (1.0), and
+    # 1 + 2^-7 + 2^-8 (odd mantissa, halfway) goes up to 1 + 2^-6; 262016 = 2^18 - 128 needs 11
+    # significant bits and rounds up into the next binade
+    want[6] = _rne_bf16_bits(x[6:7])[0]
+    got = olce._bf16_round(x)
+    assert torch.equal(got, want), (got, want)
+    assert torch.equal(got, _rne_bf16_bits(x))
+    assert not torch.equal(got, x.half().float())   # fp16 would keep 1 + 2^-9
+
+
+def test_bf16_round_matches_integer_rne():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(20000, generator=g) * torch.exp(torch.randn(20000, generator=g) * 8)
+    got = olce._bf16_round(x)
+    assert torch.equal(got, _rne_bf16_bits(x))
+    assert (got != x).float().mean() > 0.99   # the rounding is visible on almost every random value
+
+
+def test_backward_rounds_g_to_bf16():
+    """backward(round_g_bf16=True) is the product of the bf16-RNE-rounded g (chunked.py:84-86): equal
+    to g rounded by the integer method, and far from the unrounded and fp16-rounded products."""
+    h, w, t = lce_inputs(24, 32, 300, seed=9)
+    _, lse, _ = olce.forward(h, w, t, dtype=torch.float32)
+    ct = torch.full((24,), 1.0 / 24)
+    got = olce.backward(h, w, t, lse, ct, round_g_bf16=True, dtype=torch.float32, chunk=128)
+    y = t.long()
+    ctm = torch.where(y == -100, 0.0, ct)
+    p = torch.exp(h.float() @ w.float().T - lse.float()[:, None])
+    g = (p - torch.nn.functional.one_hot(y.clamp(min=0), 300).float() * (y >= 0).float()[:, None]) * ctm[:, None]
+    want = _rne_bf16_bits(g) @ w.float()
+    assert torch.allclose(got, want, rtol=1e-5, atol=1e-7)
+    unrounded = olce.backward(h, w, t, lse, ct, round_g_bf16=False, dtype=torch.float32, chunk=128)
+    f16 = g.half().float() @ w.float()
+    for other in (unrounded, f16):
+        assert float((got - other).abs().max()) > 20 * float((got - want).abs().max()) + 1e-7
+
+
 def test_bf16_rounding_of_g_is_small():
     h, w, t = lce_inputs(40, 64, 500, seed=7)
     _, lse, _ = olce.forward(h, w, t)

@@ -200,3 +200,29 @@ def test_memory_planner_terms():
     assert stock.components["attention"] > p.components["attention"]
     with pytest.raises(PlanInputError):
         est.loss_bytes(n=1, d=1, v=1, impl="fast")
+
+
+def test_memory_planner_head_terms():
+    """The cached transposed head and a trainable head's dL/dW (and its all-rows backward block)."""
+    from mlx_train_perf.plan import estimate as est
+
+    n, d, v = 8192, 4096, 151936
+    frozen = est.loss_bytes(n=n, d=d, v=v, transposed_head=True)
+    # [d][round_up(v, 256) + 64] bf16 = 1.246 GB, the copy the backward reads for its dH product
+    assert frozen.transposed_head == d * (152064 + 64) * 2 == 1_246_232_576
+    assert est.loss_bytes(n=n, d=d, v=v, transposed_head=False).transposed_head == 0
+    assert est.loss_bytes(n=n, d=100, v=v, transposed_head=True).transposed_head == 0   # d % 64: no copy
+    assert frozen.head_grad == 0 and frozen.peak == frozen.transposed_head + frozen.backward_workspace
+    # frozen flagship: two 4096-row blocks of one vocab chunk (1.25 GB of gradient tiles)
+    assert frozen.backward_workspace == 4096 * (152064 + 64) * 2 + n * 4
+    tr = est.loss_bytes(n=n, d=d, v=v, trainable=True, transposed_head=False)
+    p = plan.lce_plan(n=n, v=v, d=d, trainable=True)
+    assert p.bwd_row_block == n and p.bwd_chunks == 2
+    assert tr.head_grad == v * d * 2 and tr.backward_workspace == p.bwd_workspace_bytes + n * 4
+    assert tr.backward_peak == tr.backward_workspace + tr.head_grad > 2.8e9
+    step = dict(n_layers=32, batch=1, seq_len=8192, hidden=d, vocab=v, heads=32, kv_heads=8, head_dim=128)
+    full = est.estimate_peak(**step, trainable_head=True).components["loss"]
+    lora = est.estimate_peak(**step).components["loss"]
+    assert full - lora > v * d * 2
+    # the chunked and naive impls carry the dL/dW term too
+    assert est.loss_bytes(n=n, d=d, v=v, impl="chunked", trainable=True).head_grad == v * d * 2
