@@ -62,8 +62,10 @@ def test_planner_matches_measured_loss_peaks(trainable, monkeypatch):
     print(f"  forward {fwd1} B (plan {plan.forward_peak}); backward {bwd1} B (plan {plan.backward_peak} + dH "
           f"{dh_bytes}); first backward {bwd0} B (transposed head {plan.transposed_head})", flush=True)
     assert fwd0 == fwd1 == plan.forward_peak
-    # the cotangent the planner counts (n fp32) is the caller's here; autograd adds at most two more
+    # the cotangent the planner counts (n fp32) is the caller's here; autograd adds at most two more.
+    # torch's caching allocator may hand each large request (workspace, dH, dW) a whole segment,
+    # rounded to 2 MiB, when the remainder is too small to split: up to 2 MiB more per block.
     lo = plan.backward_peak + dh_bytes - N * 4
-    assert lo <= bwd1 <= lo + 3 * N * 4, (bwd1, lo)
+    assert lo <= bwd1 <= lo + 3 * N * 4 + 3 * (2 << 20), (bwd1, lo)
     assert bwd0 - bwd1 == plan.transposed_head == L.transposed_head_cache_bytes()
     L.clear_transposed_head_cache()
