@@ -161,7 +161,8 @@ int mtp_attn_fwd(const void* q, const void* k, const void* v, int64_t b, int64_t
  * 256 bytes; at shapes where the dK/dV pass splits its key blocks (mtp_attn_bwd_dkv_splits > 1 for
  * either value of causal), fp32 dK/dV partials [splits][2][b][hkv][s][dh]; then the int32 work
  * orders a packed call sorts its dQ query blocks and dK/dV key blocks into (one entry per block,
- * each order padded to 256 bytes). */
+ * each order padded to 256 bytes); then the int32 end of each position's segment [b][s] (padded to
+ * 256 bytes), which a packed call fills for its dK/dV pass. */
 size_t mtp_attn_bwd_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh);
 
 /* Workgroups per 128-key block of the dK/dV pass (1, 2, 4 or 8): the launch plan's

@@ -185,7 +185,7 @@ template <int DH, bool PACKED>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, const bf16_t* __restrict__ v,
                                const bf16_t* __restrict__ d_o, const float* __restrict__ lse,
-                               const float* __restrict__ dvec, const int32_t* __restrict__ seg_start,
+                               const float* __restrict__ dvec, const int32_t* __restrict__ seg_end,
                                bf16_t* __restrict__ dk, bf16_t* __restrict__ dv, int B, int Hq, int Hkv, int S,
                                float scale_log2, float scale, int causal, int nsplit,
                                float* __restrict__ part, const int32_t* __restrict__ order) {
@@ -234,7 +234,7 @@ void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   const bool kvalid = kj < S;
 
   const long krow = (long)(bidx * Hkv + kvh) * S;
-  const int32_t* sst = PACKED ? seg_start + (long)bidx * S : nullptr;
+  const int32_t* send = PACKED ? seg_end + (long)bidx * S : nullptr;
 
   // This wave's operand of the first product: K (P wave) or V (dS wave) rows of its keys.
   bf16x8 opf[kDK];
@@ -249,13 +249,13 @@ void attn_bwd_dkv_ab_kernel(const bf16_t* __restrict__ q, const bf16_t* __restri
   int q_end = S;
   if (PACKED) {
     const int klast = (k0 + 127 < S) ? k0 + 127 : S - 1;
-    q_end = __builtin_amdgcn_readfirstlane(first_above(sst, 0, S, klast));
+    q_end = __builtin_amdgcn_readfirstlane(send[klast]);
   }
-  // Queries q with kj <= q < my_lim see key kj (packed: my_lim is the end of kj's segment);
-  // w_lim is the wave's smallest limit, its first key's.
+  // Queries q with kj <= q < my_lim see key kj (packed: my_lim is the end of kj's segment, at most
+  // q_end since seg_end is non-decreasing); w_lim is the wave's smallest limit, its first key's.
   int my_lim = S, w_lim = S;
   if (PACKED) {
-    my_lim = kvalid ? first_above(sst, kj, q_end, kj) : S;
+    my_lim = kvalid ? send[kj] : S;
     w_lim = __builtin_amdgcn_readfirstlane(my_lim);
   }
   const int ntq = (q_end > q_begin) ? (q_end - q_begin + kKT - 1) / kKT : 0;
@@ -1038,8 +1038,19 @@ void attn_kv_kernel(const bf16_t* __restrict__ q, const bf16_t* __restrict__ k, 
 // buckets of cost >> shift; items of one bucket land in any order, which changes only the schedule:
 // every item writes its own outputs.
 constexpr int kSchedBuckets = 2048;
+// Workgroups 2 and up fill seg_end[b][i], the first position after i's segment (the first j > i with
+// seg_start[j] > i, S if none), which the dK/dV pass reads instead of searching seg_start per key.
 __global__ __launch_bounds__(1024) void attn_sched_kernel(const int32_t* __restrict__ seg_start, int B, int S, int P,
-                                                         int32_t* __restrict__ q_order, int32_t* __restrict__ kv_order) {
+                                                         int32_t* __restrict__ q_order, int32_t* __restrict__ kv_order,
+                                                         int32_t* __restrict__ seg_end) {
+  if (blockIdx.x >= 2) {
+    const long i = (long)(blockIdx.x - 2) * 1024 + threadIdx.x;
+    if (i < (long)B * S) {
+      const int b = (int)(i / S), pos = (int)(i % S);
+      seg_end[i] = first_above(seg_start + (long)b * S, pos, S, pos);
+    }
+    return;
+  }
   __shared__ int cnt[kSchedBuckets];
   __shared__ int wsum[16];
   const bool kv = blockIdx.x == 1;
@@ -1127,11 +1138,12 @@ size_t attn_order_offset(int b, int hq, int hkv, int s, int dh) {
 }  // namespace
 
 size_t attn_bwd_workspace(int b, int hq, int hkv, int s, int dh) {
-  // D, the fp32 dK/dV partials when either mode splits (the larger split), and the two work orders
-  // of a packed backward (int32 per dQ query block and per dK/dV key block).
+  // D, the fp32 dK/dV partials when either mode splits (the larger split), the two work orders
+  // of a packed backward (int32 per dQ query block and per dK/dV key block) and its segment ends
+  // (int32 per position).
   const int P = fwd_rows(hq, hkv);
   return attn_order_offset(b, hq, hkv, s, dh) + round256((size_t)b * ((s + P - 1) / P) * 4) +
-         round256((size_t)b * ((s + 127) / 128) * 4);
+         round256((size_t)b * ((s + 127) / 128) * 4) + round256((size_t)b * s * 4);
 }
 
 namespace {
@@ -1164,11 +1176,15 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   char* ws = reinterpret_cast<char*>(dvec);
   int32_t* q_order = nullptr;
   int32_t* kv_order = nullptr;
+  int32_t* seg_end = nullptr;
   if (sid) {
     const int P = fwd_rows(sh.hq, sh.hkv);
     q_order = reinterpret_cast<int32_t*>(ws + attn_order_offset(sh.b, sh.hq, sh.hkv, sh.s, DH));
     kv_order = q_order + round256((size_t)sh.b * ((sh.s + P - 1) / P) * 4) / 4;
-    hipLaunchKernelGGL(attn_sched_kernel, dim3(2), dim3(1024), 0, st, sst, sh.b, sh.s, P, q_order, kv_order);
+    seg_end = kv_order + round256((size_t)sh.b * ((sh.s + 127) / 128) * 4) / 4;
+    const unsigned nse = (unsigned)(((long)sh.b * sh.s + 1023) / 1024);
+    hipLaunchKernelGGL(attn_sched_kernel, dim3(2 + nse), dim3(1024), 0, st, sst, sh.b, sh.s, P, q_order, kv_order,
+                       seg_end);
     e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -1181,7 +1197,7 @@ hipError_t bwd_dh(const AttnShape& sh, const bf16_t* q, const bf16_t* k, const b
   const int ns = attn_dkv_nsplit(sh.b, sh.hq, sh.hkv, sh.s, DH, sh.causal);
   float* part = reinterpret_cast<float*>(ws + attn_dvec_bytes(sh.b, sh.hq, sh.s));
   dim3 sgrid(((sh.s + 127) / 128) * sh.b * sh.hkv * ns);
-  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part, kv_order);
+  if (sid) hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, true>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, seg_end, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part, kv_order);
   else hipLaunchKernelGGL((attn_bwd_dkv_ab_kernel<DH, false>), sgrid, dim3(512), 0, st, q, k, v, d_o, lse, dvec, sst, dk, dv, sh.b, sh.hq, sh.hkv, sh.s, sl2, sh.scale, sh.causal, ns, part, nullptr);
   e = hipGetLastError();
   if (e != hipSuccess || ns == 1) return e;

@@ -196,9 +196,9 @@ def attn_dkv_splits(*, b: int, hq: int, hkv: int, s: int, dh: int = 128, causal:
 
 def attn_bwd_workspace_bytes(*, b: int, hq: int, hkv: int, s: int, dh: int = 128) -> int:
     """D (fp32 per query row, padded to 256 B), the fp32 dK/dV partials of the larger split of the
-    two masks (when either splits), and the two int32 work orders of a packed backward: one entry
-    per dQ query block and one per 128-key dK/dV block, each padded to 256 B
-    (csrc/attn_kernels.hip attn_bwd_workspace)."""
+    two masks (when either splits), the two int32 work orders of a packed backward (one entry per
+    dQ query block and one per 128-key dK/dV block) and its int32 segment end per position, each
+    padded to 256 B (csrc/attn_kernels.hip attn_bwd_workspace)."""
     ns = max(attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=True),
              attn_dkv_splits(b=b, hq=hq, hkv=hkv, s=s, dh=dh, causal=False))
 
@@ -207,7 +207,7 @@ def attn_bwd_workspace_bytes(*, b: int, hq: int, hkv: int, s: int, dh: int = 128
 
     rows = 32 * (4 // attn_heads_per_workgroup(hq, hkv))   # query positions per dQ workgroup
     parts = ns * 2 * b * hkv * s * dh * 4 if ns > 1 else 0
-    return pad(b * hq * s * 4) + parts + pad(4 * b * -(-s // rows)) + pad(4 * b * -(-s // 128))
+    return pad(b * hq * s * 4) + parts + pad(4 * b * -(-s // rows)) + pad(4 * b * -(-s // 128)) + pad(4 * b * s)
 
 
 @dataclass(frozen=True)

@@ -136,8 +136,9 @@ def test_attention_plan():
     assert p.heads_per_workgroup == 4
     assert p.fwd_workgroups == (8192 // 32) * 8
     assert p.dkv_splits == 1 and p.dkv_workgroups == 64 * 8
-    # D, no split at the flagship, the packed work orders (256 query blocks, 64 key blocks)
-    assert p.bwd_workspace_bytes == 32 * 8192 * 4 + 256 * 4 + 256
+    # D, no split at the flagship, the packed work orders (256 query blocks, 64 key blocks), the
+    # packed segment ends (one per position)
+    assert p.bwd_workspace_bytes == 32 * 8192 * 4 + 256 * 4 + 256 + 8192 * 4
     assert plan.attn_heads_per_workgroup(6, 3) == 2 and plan.attn_heads_per_workgroup(3, 1) == 1
 
 
@@ -175,11 +176,12 @@ def test_dkv_split_table(causal):
     assert plan.attn_dkv_splits(b=1, hq=32, hkv=8, s=2048, dh=64) == 4   # the same table for head_dim 64/96
     ws = plan.attn_bwd_workspace_bytes(b=1, hq=32, hkv=8, s=2048)
     # D, 4 splits of fp32 dK and dV, then the packed work orders: 64 query blocks of 32 and 16 key
-    # blocks of 128, an int32 each, each order padded to 256 bytes
-    assert ws == 32 * 2048 * 4 + 4 * 2 * 8 * 2048 * 128 * 4 + 256 + 256
+    # blocks of 128, an int32 each, each order padded to 256 bytes, and an int32 segment end per
+    # position
+    assert ws == 32 * 2048 * 4 + 4 * 2 * 8 * 2048 * 128 * 4 + 256 + 256 + 2048 * 4
     # D padded to 256 bytes before the partials (their 16-byte stores stay aligned); one head per
     # workgroup gives 128-query blocks
-    assert plan.attn_bwd_workspace_bytes(b=1, hq=1, hkv=1, s=61) == 256 + 8 * 2 * 61 * 128 * 4 + 256 + 256
+    assert plan.attn_bwd_workspace_bytes(b=1, hq=1, hkv=1, s=61) == 256 + 8 * 2 * 61 * 128 * 4 + 256 + 256 + 256
 
 
 def test_memory_planner_terms():
