@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTP_ABI_VERSION 2
+#define MTP_ABI_VERSION 3
 
 /* Error codes; the Python layer maps them onto the reference's typed exceptions
  * (src/mlx_train_perf/errors.py:1-76). */
@@ -180,6 +180,57 @@ int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
                  float scale, int32_t causal, const int32_t* seg_id, const int32_t* seg_start,
                  void* d_q, void* d_k, void* d_v, void* workspace, size_t workspace_bytes,
                  void* stream);
+
+/* ---------------------------------------------------------------------------------------------
+ * fp32 inputs. The reference kernels take fp32 as well as bf16 (their element type T is fp32 or
+ * bf16: src/mlx_train_perf/core/loss.py:20-24, attention/api.py:41-43). These entry points take
+ * fp32 hidden states / weights / q, k, v and compute with fp32 MFMA products and fp32
+ * accumulation; every output and gradient is fp32. Semantics, masks, layouts and error codes are
+ * those of the bf16 entry points above; the 4-bit head keeps its packed words and takes fp32
+ * scales and biases [v][d/64].
+ * ------------------------------------------------------------------------------------------- */
+
+/* Workspace bytes of mtp_lce_fwd_f32 (per-token partial maxima and sums per vocab split). */
+size_t mtp_lce_fwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind);
+
+/* fp32 forward, as mtp_lce_fwd. Replaces launch.forward / forward_quantized
+ * (core/kernel/launch.py:75-100,336-373) with T = fp32. */
+int mtp_lce_fwd_f32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales,
+                    const float* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                    int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* Vocab columns per fp32 backward chunk (a multiple of 128) for a workspace budget in bytes. */
+int64_t mtp_lce_bwd_f32_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
+
+/* Workspace bytes of mtp_lce_bwd_f32 at a chunk: the fp32 gradient tile [n][chunk + 4]. */
+size_t mtp_lce_bwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int64_t chunk);
+
+/* fp32 backward, as mtp_lce_bwd with g = (exp(z - lse) - onehot) * d_nll kept in fp32 (the
+ * reference's chunked_backward casts g to the weight dtype, here fp32: core/chunked.py:84-86);
+ * d_hidden fp32 [n][d], d_w (optional, dense head) fp32 [v][d]. chunk: a multiple of 128. */
+int mtp_lce_bwd_f32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales,
+                    const float* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                    int32_t head_kind, int64_t ignore_index, const float* lse, const float* d_nll,
+                    float* d_hidden, float* d_w, int64_t chunk, void* workspace,
+                    size_t workspace_bytes, void* stream);
+
+/* fp32 forward, as mtp_attn_fwd; o fp32. Replaces launch_flash_fwd with T = fp32. */
+int mtp_attn_fwd_f32(const float* q, const float* k, const float* v, int64_t b, int64_t hq,
+                     int64_t hkv, int64_t s, int64_t dh, float scale, int32_t causal,
+                     const int32_t* seg_id, const int32_t* seg_start, float* o, float* lse,
+                     void* stream);
+
+/* Workspace bytes of mtp_attn_bwd_f32: the fp32 row term D [b][hq][s]. */
+size_t mtp_attn_bwd_f32_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh);
+
+/* fp32 backward, as mtp_attn_bwd; dq, dk, dv fp32. Replaces launch_bwd_D / launch_bwd_dq /
+ * launch_bwd_dkv with T = fp32. */
+int mtp_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o,
+                     const float* lse, const float* d_o, int64_t b, int64_t hq, int64_t hkv,
+                     int64_t s, int64_t dh, float scale, int32_t causal, const int32_t* seg_id,
+                     const int32_t* seg_start, float* d_q, float* d_k, float* d_v, void* workspace,
+                     size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -364,4 +364,130 @@ int mtp_attn_bwd(const void* q, const void* k, const void* v, const void* o, con
   return ok();
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp32 inputs
+// ---------------------------------------------------------------------------------------------
+
+static int check_lce32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales,
+                       const float* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
+                       int32_t head_kind) {
+  if (n < 1 || d < 1 || v < 1) return fail(MTP_ERR_INPUT, "n, d, v must be >= 1 (got n=%lld d=%lld v=%lld)", (long long)n, (long long)d, (long long)v);
+  if (n > kMaxDim || d > kMaxDim || v > kMaxDim || n * d > (int64_t(1) << 40)) return fail(MTP_ERR_INPUT, "n, d, v must each be < 2^31");
+  if (!hidden || !targets) return fail(MTP_ERR_INPUT, "hidden and targets must be non-null");
+  if (!aligned16(hidden)) return fail(MTP_ERR_UNSUPPORTED, "hidden must be 16-byte aligned");
+  if (head_kind == MTP_HEAD_DENSE) {
+    if (!w) return fail(MTP_ERR_INPUT, "dense head: w must be non-null");
+    if (!aligned16(w)) return fail(MTP_ERR_UNSUPPORTED, "dense head: w must be 16-byte aligned");
+  } else if (head_kind == MTP_HEAD_Q4) {
+    if (!w_q || !scales || !biases) return fail(MTP_ERR_INPUT, "quantized head: w_q, scales and biases must be non-null");
+    if (d % 64 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires the quantized head's hidden dim to be a multiple of 64 (got d=%lld); use impl='chunked'", (long long)d);
+  } else {
+    return fail(MTP_ERR_UNSUPPORTED, "unknown head_kind %d", (int)head_kind);
+  }
+  return MTP_OK;
+}
+
+static mtp::LceHead32 make_head32(const float* w, const uint32_t* w_q, const float* scales, const float* biases,
+                                  int32_t head_kind) {
+  return mtp::LceHead32{head_kind == MTP_HEAD_Q4, w, w_q, scales, biases};
+}
+
+size_t mtp_lce_fwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind) {
+  (void)d;
+  (void)head_kind;
+  if (n < 1 || v < 1) return 0;
+  return (size_t)2 * (size_t)mtp::lce32_fwd_nsplit((long)n, (long)v) * (size_t)n * sizeof(float);
+}
+
+int mtp_lce_fwd_f32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales, const float* biases,
+                    const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
+                    float* nll, float* lse, float* tgt, void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_lce32(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
+  if (rc) return rc;
+  if (!nll || !lse || !tgt) return fail(MTP_ERR_INPUT, "nll, lse, tgt outputs must be non-null");
+  const size_t need = mtp_lce_fwd_f32_workspace_bytes(n, d, v, head_kind);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "fp32 lce forward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  hipError_t e = mtp::launch_lce32_fwd(make_head32(w, w_q, scales, biases, head_kind), hidden, targets, (int)n, (int)d,
+                                       (int)v, (long long)ignore_index, nll, lse, tgt, static_cast<float*>(workspace),
+                                       static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "fp32 lce forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int64_t mtp_lce_bwd_f32_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+  (void)d;
+  if (n < 1 || v < 1) return 0;
+  const int64_t vpad = round_up(v, 128);
+  int64_t c = ((int64_t)(budget_bytes / ((size_t)n * 4)) - 4) / 128 * 128;
+  if (c < 128) c = 128;
+  return c > vpad ? vpad : c;
+}
+
+size_t mtp_lce_bwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int64_t chunk) {
+  (void)d;
+  if (n < 1 || v < 1 || chunk < 128 || chunk % 128) return 0;
+  if (chunk > round_up(v, 128)) chunk = round_up(v, 128);
+  return (size_t)n * (size_t)(chunk + 4) * sizeof(float);
+}
+
+int mtp_lce_bwd_f32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales, const float* biases,
+                    const int64_t* targets, int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t ignore_index,
+                    const float* lse, const float* d_nll, float* d_hidden, float* d_w, int64_t chunk, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  int rc = check_lce32(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
+  if (rc) return rc;
+  if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
+  if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
+  if (chunk < 128 || chunk % 128) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 128 (got %lld)", (long long)chunk);
+  if (chunk > round_up(v, 128)) chunk = round_up(v, 128);
+  const size_t need = mtp_lce_bwd_f32_workspace_bytes(n, d, v, chunk);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "fp32 lce backward needs a workspace of %zu bytes at chunk=%lld (got %zu)", need, (long long)chunk, workspace ? workspace_bytes : (size_t)0);
+  if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
+  hipError_t e = mtp::launch_lce32_bwd(make_head32(w, w_q, scales, biases, head_kind), hidden, targets, lse, d_nll, (int)n,
+                                       (int)d, (int)v, (long long)ignore_index, (int)chunk, d_hidden, d_w,
+                                       static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "fp32 lce backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int mtp_attn_fwd_f32(const float* q, const float* k, const float* v, int64_t b, int64_t hq, int64_t hkv, int64_t s,
+                     int64_t dh, float scale, int32_t causal, const int32_t* seg_id, const int32_t* seg_start, float* o,
+                     float* lse, void* stream) {
+  int rc = check_attn(q, k, v, b, hq, hkv, s, dh, causal, seg_id, seg_start);
+  if (rc) return rc;
+  if (!o || !lse) return fail(MTP_ERR_INPUT, "o and lse must be non-null");
+  if (!aligned16(o)) return fail(MTP_ERR_UNSUPPORTED, "o must be 16-byte aligned");
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale, (int)causal};
+  hipError_t e = mtp::launch_attn32_fwd(sh, q, k, v, seg_start, o, lse, static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "fp32 attention forward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+size_t mtp_attn_bwd_f32_workspace_bytes(int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh) {
+  (void)dh;
+  if (b < 1 || hq < 1 || hkv < 1 || s < 1 || hq % hkv || b * hq * s > kMaxDim) return 0;
+  return (size_t)b * (size_t)hq * (size_t)s * sizeof(float);
+}
+
+int mtp_attn_bwd_f32(const float* q, const float* k, const float* v, const float* o, const float* lse, const float* d_o,
+                     int64_t b, int64_t hq, int64_t hkv, int64_t s, int64_t dh, float scale, int32_t causal,
+                     const int32_t* seg_id, const int32_t* seg_start, float* d_q, float* d_k, float* d_v,
+                     void* workspace, size_t workspace_bytes, void* stream) {
+  int rc = check_attn(q, k, v, b, hq, hkv, s, dh, causal, seg_id, seg_start);
+  if (rc) return rc;
+  if (!o || !lse || !d_o || !d_q || !d_k || !d_v) return fail(MTP_ERR_INPUT, "o, lse, d_o, d_q, d_k, d_v must be non-null");
+  if (!aligned16(o) || !aligned16(d_o) || !aligned16(d_q) || !aligned16(d_k) || !aligned16(d_v))
+    return fail(MTP_ERR_UNSUPPORTED, "o, d_o, d_q, d_k, d_v must be 16-byte aligned");
+  const size_t need = mtp_attn_bwd_f32_workspace_bytes(b, hq, hkv, s, dh);
+  if (!workspace || workspace_bytes < need)
+    return fail(MTP_ERR_WORKSPACE, "fp32 attention backward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  mtp::AttnShape sh{(int)b, (int)hq, (int)hkv, (int)s, (int)dh, scale, (int)causal};
+  hipError_t e = mtp::launch_attn32_bwd(sh, q, k, v, o, lse, d_o, seg_start, d_q, d_k, d_v,
+                                        static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "fp32 attention backward launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -62,4 +62,26 @@ hipError_t launch_attn_bwd(const AttnShape& sh, const bf16_t* q, const bf16_t* k
                            const int32_t* seg_start, bf16_t* dq, bf16_t* dk, bf16_t* dv, float* dvec,
                            hipStream_t stream);
 
+// fp32 inputs (f32_kernels.hip): fp32 MFMA products, fp32 outputs and gradients.
+struct LceHead32 {
+  int q4;                 // 0: dense fp32 [V][D]; 1: 4-bit affine, group size 64, fp32 scales/biases
+  const float* w;
+  const uint32_t* wq;
+  const float* sc;        // [V][D/64]
+  const float* bi;
+};
+int lce32_fwd_nsplit(long N, long V);
+hipError_t launch_lce32_fwd(const LceHead32& h, const float* H, const int64_t* targets, int N, int D, int V,
+                            long long ignore_index, float* nll, float* lse, float* tgt, float* ws, hipStream_t stream);
+// Gbuf: fp32 [N][chunk + 4]; dH fp32 [N][D]; dW (optional, dense head) fp32 [V][D].
+hipError_t launch_lce32_bwd(const LceHead32& h, const float* H, const int64_t* targets, const float* lse,
+                            const float* dnll, int N, int D, int V, long long ignore_index, int chunk, float* dH,
+                            float* dW, float* Gbuf, hipStream_t stream);
+hipError_t launch_attn32_fwd(const AttnShape& sh, const float* q, const float* k, const float* v,
+                             const int32_t* seg_start, float* o, float* lse, hipStream_t stream);
+// dvec: fp32 [b][hq][s] (D = rowsum(dO * O), formed by the dQ pass for the dK/dV pass).
+hipError_t launch_attn32_bwd(const AttnShape& sh, const float* q, const float* k, const float* v, const float* o,
+                             const float* lse, const float* d_o, const int32_t* seg_start, float* dq, float* dk,
+                             float* dv, float* dvec, hipStream_t stream);
+
 }  // namespace mtp

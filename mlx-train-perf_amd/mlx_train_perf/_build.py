@@ -16,7 +16,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR.parent / "csrc"
 OUT = PKG_DIR / "libmtp_hip.so"
 OBJ_DIR = PKG_DIR.parent / "_build"
-SOURCES = ("capi.hip", "lce_kernels.hip", "attn_kernels.hip", "bench_probe.hip")
+SOURCES = ("capi.hip", "lce_kernels.hip", "attn_kernels.hip", "f32_kernels.hip", "bench_probe.hip")
 ARCH = os.environ.get("MTP_OFFLOAD_ARCH", "gfx950")
 
 HIPCC_FLAGS = [

@@ -31,7 +31,7 @@ from mlx_train_perf.errors import (
 LIB_NAME = "libmtp_hip.so"
 LIB_PATH = Path(os.environ.get("MTP_HIP_LIB", str(Path(__file__).resolve().parent / LIB_NAME)))
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 MTP_OK = 0
 MTP_ERR_INPUT = -1
 MTP_ERR_UNSUPPORTED = -2
@@ -76,6 +76,22 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_attn_bwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                     _i64, _i64, _i64, _i64, _i64, _f32, _i32, _c_void_p, _c_void_p,
                                     _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
+    # fp32 inputs
+    "mtp_lce_fwd_f32_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
+    "mtp_lce_fwd_f32": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                       _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                       _c_void_p, _size, _c_void_p]),
+    "mtp_lce_bwd_f32_chunk": (_i64, [_i64, _i64, _i64, _size]),
+    "mtp_lce_bwd_f32_workspace_bytes": (_size, [_i64, _i64, _i64, _i64]),
+    "mtp_lce_bwd_f32": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                       _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
+                                       _c_void_p, _i64, _c_void_p, _size, _c_void_p]),
+    "mtp_attn_fwd_f32": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i64, _i64, _i64,
+                                        _f32, _i32, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p]),
+    "mtp_attn_bwd_f32_workspace_bytes": (_size, [_i64, _i64, _i64, _i64, _i64]),
+    "mtp_attn_bwd_f32": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
+                                        _i64, _i64, _i64, _i64, _i64, _f32, _i32, _c_void_p, _c_void_p,
+                                        _c_void_p, _c_void_p, _c_void_p, _c_void_p, _size, _c_void_p]),
 }
 
 _lock = threading.Lock()

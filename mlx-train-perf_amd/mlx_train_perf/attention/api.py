@@ -21,7 +21,7 @@ from mlx_train_perf.attention.reference import flash_attention_reference, kv_hea
 from mlx_train_perf.attention.segments import PackedMask, layout_violation, segment_allowed
 from mlx_train_perf.errors import AttentionInputError, UnsupportedAttentionError
 
-_KERNEL_DTYPES = (torch.bfloat16,)
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)   # the reference kernel's T (api.py:41-43)
 _KERNEL_HEAD_DIMS = (64, 96, 128)
 
 VJP_CALLS: dict[str, int] = {}
@@ -98,7 +98,7 @@ def resolve_attention_impl(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *,
         raise AttentionInputError(f"unknown impl {impl!r}; expected one of 'auto', 'kernel', 'reference'")
     if q.dtype not in _KERNEL_DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise UnsupportedAttentionError(
-            f"kernel impl on MI355X supports bf16 q/k/v (got {q.dtype}/{k.dtype}/{v.dtype}); use impl='reference'."
+            f"kernel impl only supports fp32/bf16 (got {q.dtype}/{k.dtype}/{v.dtype}); use impl='reference'."
         )
     head_dim = q.shape[-1]
     if head_dim not in _KERNEL_HEAD_DIMS:
@@ -180,29 +180,30 @@ def kernel_forward(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, *, scale: 
     hkv = k.shape[1]
     o = torch.empty_like(q)
     lse = torch.empty((b, hq, n), dtype=torch.float32, device=q.device)
+    fwd = lib.mtp_attn_fwd_f32 if q.dtype == torch.float32 else lib.mtp_attn_fwd
     with _native.on_device(q):
-        rc = lib.mtp_attn_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale),
-                              int(causal), _native.ptr(seg_id), _native.ptr(seg_start), o.data_ptr(),
-                              lse.data_ptr(), _native.stream_of(q))
+        rc = fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), b, hq, hkv, n, dh, float(scale), int(causal),
+                 _native.ptr(seg_id), _native.ptr(seg_start), o.data_ptr(), lse.data_ptr(), _native.stream_of(q))
     _native.check(rc, domain="attention")
     return o, lse
 
 
 def kernel_backward(q, k, v, o, lse, d_o, *, scale: float, seg_id=None, seg_start=None, causal: bool = True):
-    """(dQ, dK, dV) from mtp_attn_bwd."""
+    """(dQ, dK, dV) from mtp_attn_bwd (mtp_attn_bwd_f32 for fp32 inputs)."""
     lib = _native.load()
     b, hq, n, dh = q.shape
     hkv = k.shape[1]
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
-    ws_bytes = lib.mtp_attn_bwd_workspace_bytes(b, hq, hkv, n, dh)
+    f32 = q.dtype == torch.float32
+    ws_bytes = (lib.mtp_attn_bwd_f32_workspace_bytes if f32 else lib.mtp_attn_bwd_workspace_bytes)(b, hq, hkv, n, dh)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+    bwd = lib.mtp_attn_bwd_f32 if f32 else lib.mtp_attn_bwd
     with _native.on_device(q):
-        rc = lib.mtp_attn_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(),
-                              d_o.data_ptr(), b, hq, hkv, n, dh, float(scale), int(causal), _native.ptr(seg_id),
-                              _native.ptr(seg_start), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), ws.data_ptr(),
-                              ws_bytes, _native.stream_of(q))
+        rc = bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), lse.data_ptr(), d_o.data_ptr(), b, hq, hkv,
+                 n, dh, float(scale), int(causal), _native.ptr(seg_id), _native.ptr(seg_start), dq.data_ptr(),
+                 dk.data_ptr(), dv.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(q))
     _native.check(rc, domain="attention")
     return dq, dk, dv
 

@@ -7,7 +7,8 @@ outside the Function. Aux outputs never leak.
 
 MI355X specifics:
 - `impl="kernel"` (and `"auto"`) runs the HIP kernels of libmtp_hip.so: the logit-free forward and
-  the chunked-recompute dL/dH backward. Hidden and dense weights must be bf16 on a gfx950 device.
+  the chunked-recompute dL/dH backward. Hidden states (and a dense head) are bf16 (bf16 MFMA,
+  fp32 accumulation) or fp32 (fp32 MFMA, fp32 gradients), on a gfx950 device.
 - `ignore_index` (default -100): ignored rows get nll = 0, a zero gradient, and are excluded from
   `reduction="mean"`, which is exactly the trainer adapter's `(nll * mask).sum() / ntoks`
   (adapters/mlx_lm.py:212-216). With no ignored rows every reduction equals the reference's.
@@ -30,8 +31,9 @@ from mlx_train_perf.core.quant import dequantize
 from mlx_train_perf.errors import LossInputError, UnsupportedHeadError
 from mlx_train_perf.plan import launch as _plan
 
-# The MI355X kernels compute in bf16 MFMA with fp32 accumulation.
-_KERNEL_DTYPES = (torch.bfloat16,)
+# The MI355X kernels take bf16 (bf16 MFMA, fp32 accumulation) or fp32 (fp32 MFMA) hidden states,
+# as the reference kernel's element type is fp32 or bf16 (loss.py:20-24).
+_KERNEL_DTYPES = (torch.bfloat16, torch.float32)
 _KERNEL_ROW_TILE = 256  # token rows per workgroup tile (reported as Resolution.row_tiles)
 _DEFAULT_CHUNK = 8192   # chunked-impl vocab chunk (the reference's kernel tile, loss.py:25)
 _WORD_DTYPES = tuple(t for t in (torch.int32, getattr(torch, "uint32", None)) if t is not None)
@@ -76,8 +78,8 @@ def _require_kernel_supported(*, head: HeadRef, dtype: torch.dtype) -> None:
     naming the 'chunked' alternative, for any head/dtype combination the kernel cannot serve."""
     if dtype not in _KERNEL_DTYPES:
         raise UnsupportedHeadError(
-            f"kernel impl on MI355X supports bf16 hidden states (got {dtype}); use impl='chunked' "
-            "for other dtypes."
+            f"kernel impl only supports fp32/bf16 hidden dtype (got {dtype}); "
+            "use impl='chunked' for other dtypes."
         )
     if isinstance(head, QuantizedHead):
         if head.bits != 4:
@@ -101,15 +103,18 @@ def _require_kernel_supported(*, head: HeadRef, dtype: torch.dtype) -> None:
                 f"kernel impl reads w_q as 32-bit words (int32 or uint32 bit patterns); got {head.w_q.dtype}. "
                 "Use impl='chunked'."
             )
+        # bf16 hidden states: the kernels read scales and biases as bf16; fp32: as fp32 (either
+        # stored dtype is converted, losslessly, for the fp32 kernels).
+        sb_ok = (torch.bfloat16,) if dtype == torch.bfloat16 else (torch.bfloat16, torch.float32)
         for name, t in (("scales", head.scales), ("biases", head.biases)):
-            if t.dtype != torch.bfloat16:
+            if t.dtype not in sb_ok:
                 raise UnsupportedHeadError(
-                    f"kernel impl reads the quantized head's {name} as bf16; got {t.dtype}. Use impl='chunked' "
-                    "(it dequantizes in the given dtype) or store them as bf16."
+                    f"kernel impl reads the quantized head's {name} as {'bf16' if dtype == torch.bfloat16 else 'fp32'}; "
+                    f"got {t.dtype}. Use impl='chunked' (it dequantizes in the given dtype) or store them as bf16."
                 )
     else:
         d = head.weight.shape[-1]
-        if d % 8 != 0:
+        if dtype == torch.bfloat16 and d % 8 != 0:
             raise UnsupportedHeadError(
                 f"kernel impl requires the hidden dim to be a multiple of 8 (got d={d}); use impl='chunked'."
             )
@@ -286,7 +291,8 @@ def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_ki
 
 class _KernelLCE(torch.autograd.Function):
     """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only; it also
-    returns dL/dW when the dense head is an input that requires grad (trainable head)."""
+    returns dL/dW when the dense head is an input that requires grad (trainable head). fp32 hidden
+    states run the fp32 entry points (mtp_lce_fwd_f32 / mtp_lce_bwd_f32)."""
 
     @staticmethod
     def forward(ctx, hidden2, targets2, w, w_q, scales, biases, head_kind, ignore_index, bwd_chunk, owner=None):
@@ -294,16 +300,18 @@ class _KernelLCE(torch.autograd.Function):
         n, d = hidden2.shape
         v = w.shape[0] if head_kind == _native.HEAD_DENSE else w_q.shape[0]
         dev = hidden2.device
+        f32 = hidden2.dtype == torch.float32
         nll = torch.empty(n, dtype=torch.float32, device=dev)
         lse = torch.empty(n, dtype=torch.float32, device=dev)
         tgt = torch.empty(n, dtype=torch.float32, device=dev)
-        ws_bytes = lib.mtp_lce_fwd_workspace_bytes(n, d, v, head_kind)
+        ws_fn = lib.mtp_lce_fwd_f32_workspace_bytes if f32 else lib.mtp_lce_fwd_workspace_bytes
+        fwd = lib.mtp_lce_fwd_f32 if f32 else lib.mtp_lce_fwd
+        ws_bytes = ws_fn(n, d, v, head_kind)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         with _native.on_device(hidden2):
-            rc = lib.mtp_lce_fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
-                                 _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ignore_index,
-                                 nll.data_ptr(), lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), ws_bytes,
-                                 _native.stream_of(hidden2))
+            rc = fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases),
+                     targets2.data_ptr(), n, d, v, head_kind, ignore_index, nll.data_ptr(), lse.data_ptr(),
+                     tgt.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         ctx.save_for_backward(hidden2, targets2, lse)
         ctx.head = (w, w_q, scales, biases, head_kind, v)
@@ -321,6 +329,8 @@ class _KernelLCE(torch.autograd.Function):
         w, w_q, scales, biases, head_kind, v = ctx.head
         n, d = hidden2.shape
         d_w = torch.empty_like(w) if (w is not None and ctx.needs_input_grad[2]) else None
+        if hidden2.dtype == torch.float32:
+            return _f32_backward(lib, ctx, hidden2, targets2, lse, d_nll, d_w)
         vpad = (v + 255) // 256 * 256
         if ctx.bwd_chunk:   # an explicit vocab chunk: all rows in one block
             chunk, rows = min(max(256, (ctx.bwd_chunk + 255) // 256 * 256), vpad), n
@@ -341,6 +351,29 @@ class _KernelLCE(torch.autograd.Function):
                                  _native.ptr(d_w), chunk, rows, ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         return d_hidden, None, d_w, None, None, None, None, None, None, None
+
+
+def _f32_backward(lib, ctx, hidden2, targets2, lse, d_nll, d_w):
+    """mtp_lce_bwd_f32: fp32 gradient tiles per vocab chunk (a multiple of 128 planned from the
+    workspace budget, or the caller's chunk), dH (and a trainable head's dW) in fp32."""
+    w, w_q, scales, biases, head_kind, v = ctx.head
+    n, d = hidden2.shape
+    vpad = (v + 127) // 128 * 128
+    if ctx.bwd_chunk:
+        chunk = min(max(128, (ctx.bwd_chunk + 127) // 128 * 128), vpad)
+    else:
+        chunk = lib.mtp_lce_bwd_f32_chunk(n, d, v, _plan.lce_bwd_budget_bytes())
+    ws_bytes = lib.mtp_lce_bwd_f32_workspace_bytes(n, d, v, chunk)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
+    d_hidden = torch.empty_like(hidden2)
+    ct = d_nll.to(torch.float32).contiguous()
+    with _native.on_device(hidden2):
+        rc = lib.mtp_lce_bwd_f32(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales),
+                                 _native.ptr(biases), targets2.data_ptr(), n, d, v, head_kind, ctx.ignore_index,
+                                 lse.data_ptr(), ct.data_ptr(), d_hidden.data_ptr(), _native.ptr(d_w), chunk,
+                                 ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
+    _native.check(rc, domain="loss")
+    return d_hidden, None, d_w, None, None, None, None, None, None, None
 
 
 def _require_same_device(hidden2: torch.Tensor, head: HeadRef, targets2: torch.Tensor) -> None:
@@ -370,7 +403,9 @@ def kernel_forward_parts(hidden2: torch.Tensor, head: HeadRef, targets2: torch.T
             raise UnsupportedHeadError("kernel impl needs a contiguous (V, D) head weight")
         return _KernelLCE.apply(h, t, w, None, None, None, _native.HEAD_DENSE, int(ignore_index), int(bwd_chunk or 0),
                                 head.weight)
-    args = (None, head.w_q.contiguous(), head.scales.contiguous(), head.biases.contiguous(), _native.HEAD_Q4)
+    sb = torch.float32 if h.dtype == torch.float32 else torch.bfloat16   # the fp32 kernels read fp32 scales
+    args = (None, head.w_q.contiguous(), head.scales.to(sb).contiguous(), head.biases.to(sb).contiguous(),
+            _native.HEAD_Q4)
     return _KernelLCE.apply(h, t, *args, int(ignore_index), int(bwd_chunk or 0), head.w_q)
 
 

@@ -11,6 +11,7 @@ import torch
 from mlx_train_perf import DenseHead, QuantizedHead, linear_cross_entropy, resolve_impl, tied_head
 from mlx_train_perf.attention import PackedMask, flash_attention, resolve_attention_impl
 from mlx_train_perf.core import chunked as mchunked
+from mlx_train_perf.core import loss as L
 from mlx_train_perf.errors import (
     AttentionInputError,
     LossInputError,
@@ -54,8 +55,12 @@ def test_loss_input_validation():
 
 def test_kernel_gate_refusals_are_typed():
     bf = torch.bfloat16
-    with pytest.raises(UnsupportedHeadError):  # fp32 hidden: the MI355X kernel is bf16
-        resolve_impl(head=_dense(), dtype=torch.float32, n=8)
+    with pytest.raises(UnsupportedHeadError, match="fp32/bf16"):  # fp16 hidden: the kernels take fp32 or bf16
+        resolve_impl(head=_dense(dtype=torch.float16), dtype=torch.float16, n=8)
+    L._require_kernel_supported(head=_dense(), dtype=torch.float32)          # fp32 passes the dtype gate
+    L._require_kernel_supported(head=_dense(d=12, dtype=bf), dtype=torch.float32)   # no d % 8 for fp32
+    with pytest.raises(UnsupportedHeadError, match="multiple of 8"):
+        L._require_kernel_supported(head=_dense(d=12, dtype=bf), dtype=bf)
     wq, sc, bi = oq.quantize_affine(torch.randn(10, 64))
     with pytest.raises(UnsupportedHeadError):
         resolve_impl(head=QuantizedHead(w_q=wq, scales=sc, biases=bi, bits=8), dtype=bf, n=8)
@@ -130,8 +135,8 @@ def test_attention_validation():
     pm = PackedMask(seg_id=torch.zeros(1, 12, dtype=torch.int32), seg_start=torch.zeros(1, 12, dtype=torch.int32))
     with pytest.raises(UnsupportedAttentionError):
         flash_attention(q, k, v, scale=1.0, causal=False, segments=pm)
-    with pytest.raises(UnsupportedAttentionError):  # fp32: the MI355X kernel is bf16
-        resolve_attention_impl(q, k, v, impl="kernel")
+    with pytest.raises(UnsupportedAttentionError, match="fp32/bf16"):  # fp16: the kernels take fp32 or bf16
+        resolve_attention_impl(q.half(), k.half(), v.half(), impl="kernel")
     qb, kb, vb = _attn(d=80, dtype=torch.bfloat16)
     with pytest.raises(UnsupportedAttentionError):
         resolve_attention_impl(qb, kb, vb, impl="auto")
@@ -169,10 +174,15 @@ def test_quantized_head_kernel_gate_checks_dtypes_and_shapes():
     refused by the kernel gate (naming impl='chunked'), wrong shapes by the input check (any impl)."""
     bf = torch.bfloat16
     wq, sc, bi = oq.quantize_affine(torch.randn(10, 64), scale_dtype=torch.float32)
-    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 scales
+    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 scales with bf16 hidden states
         resolve_impl(head=QuantizedHead(w_q=wq, scales=sc, biases=bi.to(bf)), dtype=bf, n=8)
-    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 biases
+    with pytest.raises(UnsupportedHeadError, match="chunked"):  # fp32 biases with bf16 hidden states
         resolve_impl(head=QuantizedHead(w_q=wq, scales=sc.to(bf), biases=bi), dtype=bf, n=8)
+    # fp32 hidden states: the fp32 kernels take fp32 or bf16 scales and biases, not fp16
+    L._require_kernel_supported(head=QuantizedHead(w_q=wq, scales=sc, biases=bi), dtype=torch.float32)
+    L._require_kernel_supported(head=QuantizedHead(w_q=wq, scales=sc.to(bf), biases=bi.to(bf)), dtype=torch.float32)
+    with pytest.raises(UnsupportedHeadError, match="chunked"):
+        L._require_kernel_supported(head=QuantizedHead(w_q=wq, scales=sc.half(), biases=bi), dtype=torch.float32)
     with pytest.raises(UnsupportedHeadError, match="32-bit"):  # 64-bit words
         resolve_impl(head=QuantizedHead(w_q=wq.long(), scales=sc.to(bf), biases=bi.to(bf)), dtype=bf, n=8)
     h = torch.randn(4, 64).to(bf)

@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(_native.SIGNATURES) >= declared - set()  # every export has a Python signature
-    assert lib.mtp_abi_version() == _native.ABI_VERSION == 2
+    assert lib.mtp_abi_version() == _native.ABI_VERSION == 3
 
 
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1),
@@ -154,6 +154,38 @@ def test_attention_refusals():
     assert fwd(o=False) == _native.MTP_ERR_INPUT
     rc = lib.mtp_attn_bwd(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 4, 2, 16, 64, 0.1, 1, None, None, FAKE, FAKE, FAKE,
                           FAKE, 4, None)
+    assert rc == _native.MTP_ERR_WORKSPACE
+
+
+def test_fp32_entry_points_plan_and_refuse():
+    """The fp32 entry points: workspace sizes, the backward's chunk plan, and validation before any
+    launch (same codes as the bf16 ones; fp32 takes any d for a dense head)."""
+    lib = _native.load()
+    # forward partials: [2][splits][n] fp32, about two workgroups per CU of 128-token tiles
+    assert lib.mtp_lce_fwd_f32_workspace_bytes(1024, 512, 32000, 0) == 2 * 64 * 1024 * 4
+    assert lib.mtp_lce_fwd_f32_workspace_bytes(8192, 4096, 151936, 0) == 2 * 8 * 8192 * 4
+    assert lib.mtp_lce_fwd_f32_workspace_bytes(0, 512, 32000, 0) == 0
+    # backward: one fp32 gradient tile [n][chunk + 4]; the whole padded vocab when it fits the budget
+    assert lib.mtp_lce_bwd_f32_chunk(1024, 512, 32000, 3 << 29) == 32000
+    assert lib.mtp_lce_bwd_f32_workspace_bytes(1024, 512, 32000, 32000) == 1024 * 32004 * 4
+    c = lib.mtp_lce_bwd_f32_chunk(8192, 4096, 151936, 1 << 30)
+    assert c % 128 == 0 and 8192 * (c + 4) * 4 <= 1 << 30 < 8192 * (c + 132) * 4
+    assert lib.mtp_lce_bwd_f32_chunk(8, 64, 100, 1) == 128    # at least one 128-column tile
+    assert lib.mtp_attn_bwd_f32_workspace_bytes(1, 32, 8, 8192, 128) == 32 * 8192 * 4
+    fwd = lambda **kw: lib.mtp_lce_fwd_f32(kw.get("h", FAKE), kw.get("w", FAKE), None, None, None, FAKE, 16,
+                                           kw.get("d", 36), 100, kw.get("head", 0), -100, FAKE, FAKE, FAKE, FAKE,
+                                           kw.get("ws", 0), None)
+    assert fwd() == _native.MTP_ERR_WORKSPACE       # d = 36 is fine for fp32; the workspace is missing
+    assert fwd(h=FAKE + 4) == _native.MTP_ERR_UNSUPPORTED
+    assert fwd(w=None) == _native.MTP_ERR_INPUT
+    assert fwd(head=1) == _native.MTP_ERR_INPUT       # quantized head without its tensors
+    rc = lib.mtp_lce_bwd_f32(FAKE, FAKE, None, None, None, FAKE, 16, 64, 100, 0, -100, FAKE, FAKE, FAKE, None, 100,
+                             FAKE, 1 << 20, None)
+    assert rc == _native.MTP_ERR_INPUT and "multiple of 128" in _native.last_error()
+    rc = lib.mtp_attn_fwd_f32(FAKE, FAKE, FAKE, 1, 4, 2, 16, 80, 0.1, 1, None, None, FAKE, FAKE, None)
+    assert rc == _native.MTP_ERR_UNSUPPORTED
+    rc = lib.mtp_attn_bwd_f32(FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1, 4, 2, 16, 64, 0.1, 1, None, None, FAKE, FAKE,
+                              FAKE, FAKE, 4, None)
     assert rc == _native.MTP_ERR_WORKSPACE
 
 
