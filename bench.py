@@ -43,6 +43,7 @@ sys.path.insert(0, str(ROOT))
 sys.path.insert(0, str(ROOT / "mlx-train-perf_amd"))
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA (no sparsity)
+PEAK_FP32_TFLOPS = 157.3    # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0
 
 N, D, V = 8192, 4096, 151936
@@ -212,7 +213,8 @@ def bench_lce(steps, warmup, head_kind="dense"):
     sec = time_region(step, steps, warmup)
 
     # Roofline kernel: the forward launch (lce_fwd_kernel + its finalize), one event pair per launch on
-    # the stream it is launched on; the median over `steps` launches is the figure the roofline uses.
+    # the stream it is launched on; the mean over `steps` launches is the figure the roofline uses
+    # (the median is reported beside it).
     fwd_ms = event_ms(_fwd_launcher(h.contiguous(), head, t.contiguous(), head_kind), steps, warmup=1)
 
     # Per-phase durations, events on the launch stream: [fwd][bwd] per step.
@@ -281,6 +283,74 @@ def bench_trainable_lce(steps, warmup):
     return {"ms_per_step": sec * 1e3, "tokens_per_s": N / sec, "step_tflops": flops / sec / 1e12,
             "step_mfma_frac": flops / sec / 1e12 / PEAK_BF16_TFLOPS, "bwd_marginal_peak_gb": bwd_peak / 1e9,
             "products_per_step": 4}
+
+
+def lce_footprint_curve(steps=6):
+    """The backward's memory / time trade at the flagship: the step and its backward footprint
+    (marginal peak + the cached transposed head) for workspace budgets of 3, 1.5 (default) and 0.75
+    GiB, and at the default budget without the transposed head (MTP_LCE_TRANSPOSED_HEAD=0)."""
+    import torch
+
+    from mlx_train_perf.core import loss as L
+
+    out = {}
+    saved = {k: os.environ.get(k) for k in ("MTP_LCE_BWD_BUDGET", "MTP_LCE_TRANSPOSED_HEAD")}
+    cases = (("budget_3gib", {"MTP_LCE_BWD_BUDGET": str(3 << 30)}), ("budget_1_5gib_default", {}),
+             ("budget_0_75gib", {"MTP_LCE_BWD_BUDGET": str(3 << 28)}),
+             ("no_head_copy", {"MTP_LCE_TRANSPOSED_HEAD": "0"}))
+    try:
+        for name, env in cases:
+            for k, val in saved.items():   # each case starts from the caller's settings
+                if val is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = val
+            os.environ.update(env)
+            L.clear_transposed_head_cache()
+            torch.cuda.empty_cache()
+            r = bench_lce(steps, 1, "dense")
+            out[name] = {"ms_per_step": r["sec_per_step"] * 1e3, "bwd_row_blocks": r["bwd_row_blocks"],
+                         "bwd_chunks": r["bwd_chunks"], "bwd_marginal_peak_gb": r["bwd_marginal_peak_gb"],
+                         "transposed_head_cache_gb": r["transposed_head_cache_gb"],
+                         "bwd_footprint_gb": r["bwd_footprint_gb"]}
+    finally:
+        for k, val in saved.items():
+            if val is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = val
+        L.clear_transposed_head_cache()
+    return out
+
+
+def bench_lce_fp32_c1(steps, warmup):
+    """BASELINE config 1 in fp32 on the GPU (N=1024, D=512, V=32000, 10% ignore_index): the fp32
+    entry points (fp32 MFMA), fwd+bwd per step, beside the fp32 CPU baseline of the same config."""
+    import torch
+
+    from mlx_train_perf.core import loss as L
+    from mlx_train_perf.core.loss import DenseHead
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    n, d, v = 1024, 512, 32000
+    h = torch.randn(n, d, generator=g, device="cuda")
+    w = torch.randn(v, d, generator=g, device="cuda") * 0.02
+    t = torch.randint(0, v, (n,), generator=g, device="cuda")
+    t[torch.randperm(n, generator=g, device="cuda")[:102]] = IGNORE
+    head = DenseHead(weight=w, trainable=False)
+    hd = h.requires_grad_(True)
+    valid = t != IGNORE
+    ct = (valid.float() / valid.sum()).contiguous()
+
+    def step():
+        hd.grad = None
+        nll, _, _ = L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+        nll.backward(ct)
+
+    sec = time_region(step, steps, warmup)
+    flops = 6.0 * n * v * d
+    return {"ms_per_step": sec * 1e3, "tokens_per_s": n / sec, "tflops": flops / sec / 1e12,
+            "fp32_mfma_frac": flops / sec / 1e12 / PEAK_FP32_TFLOPS, "dtype": "fp32 (fp32 MFMA)"}
 
 
 def lce_ladder(reps=10):
@@ -772,8 +842,9 @@ def main():
     ap.add_argument("--trace-summary", nargs="+", metavar="ARG",
                     help="TRACE_CSV TITLE COMMAND [STATS_CSV]: summarize a rocprofv3 --kernel-trace csv (and the "
                          "same run's --stats csv) into markdown")
-    ap.add_argument("--parts", default="lce,qlora,trainable,attention,ladder",
-                    help="comma list of lce, qlora, trainable, attention, ladder (lce is the headline line)")
+    ap.add_argument("--parts", default="lce,qlora,trainable,attention,ladder,footprint,fp32",
+                    help="comma list of lce, qlora, trainable, attention, ladder, footprint, fp32 (lce is the "
+                         "headline line)")
     args = ap.parse_args()
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary))
@@ -817,6 +888,8 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "lce_fwd_kernel<0> (+ lce_fwd_finalize_kernel in the event window)",
                      "achieved": ach, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": ach / PEAK_BF16_TFLOPS,
                      "traffic": committed_traffic("lce_fwd_kernel<0>"),
+                     "traffic_source": "profiles/pmc_bench_workload_traffic_mfma.md: rocprofv3 --pmc FETCH_SIZE + "
+                                       "WRITE_SIZE of the same kernel and shape (a committed profile, not this run)",
                      "timing": f"mean of {lce['fwd_kernel_launches']} launches (after one warm-up), HIP events on "
                                "the launch stream; the window also holds the 22 us finalize launch"},
         "step_mfma_frac": flops_step / sec / 1e12 / PEAK_BF16_TFLOPS,
@@ -859,6 +932,12 @@ def main():
         result["attention_causal_s8192"] = bench_attention(args.steps, args.warmup, "causal")
         result["attention_packed_s16384"] = bench_attention(args.steps, args.warmup, "packed")
         result["attention_noncausal_s8192"] = bench_attention(args.steps, args.warmup, "full")
+    if not args.no_extras and "footprint" in parts:
+        torch.cuda.empty_cache()
+        result["lce_footprint"] = lce_footprint_curve()
+    if not args.no_extras and "fp32" in parts:
+        torch.cuda.empty_cache()
+        result["lce_fp32_c1"] = bench_lce_fp32_c1(max(5, args.steps), 2)
     if not args.no_extras and "ladder" in parts:
         torch.cuda.empty_cache()
         result["lce_ladder_fwd"] = lce_ladder()

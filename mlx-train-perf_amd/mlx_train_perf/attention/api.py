@@ -3,9 +3,9 @@
 Residual contract (api.py:1-18): the autograd Function returns (O, L); L is a real output, marked
 non-differentiable, and only O reaches the caller. The backward reads q, k, v and the saved O, L.
 
-`impl="auto"`/`"kernel"`: the HIP kernels of libmtp_hip.so (bf16, head_dim in {64, 96, 128},
-causal with optional packed segments, or non-causal -- an extension: the reference kernel refuses
-causal=False, api.py:109-113). `impl="reference"`: the materialized oracle with the hand-written
+`impl="auto"`/`"kernel"`: the HIP kernels of libmtp_hip.so (bf16 on bf16 MFMA, fp32 on fp32 MFMA
+with fp32 outputs and gradients; head_dim in {64, 96, 128}; causal with optional packed segments,
+or non-causal -- an extension: the reference kernel refuses causal=False, api.py:109-113). `impl="reference"`: the materialized oracle with the hand-written
 FlashAttention backward over full tensors -- an explicit opt-in, O(N^2) memory, small N only.
 No silent fallback: unsupported configs raise the reference's typed errors.
 """

@@ -101,7 +101,21 @@ def test_causal_parity_rising_maxima(shape):
     q = (q.float() * 4.0 + 2.0 * u * math.sqrt(d)).to(torch.bfloat16)
     k = (k.float() + ramp).to(torch.bfloat16)
     scale = 1.0 / math.sqrt(d)
-    _check(_run_kernel(q, k, v, do, scale), q, k, v, do, scale)
+    res = _run_kernel(q, k, v, do, scale)
+    _check(res, q, k, v, do, scale)
+    # The backward alone, from the saved state it is given: the fp64 oracle backward fed the kernel's
+    # own bf16 O and L. Against the oracle with the exact O (above) dQ sits near the 1e-2 bar on these
+    # peaked rows, because D = rowsum(dO O) is formed from the stored bf16 O (as in any bf16 kernel;
+    # the forward cannot form D, which needs dO). Here that rounding is common to both sides, so what
+    # remains is the backward kernels' own arithmetic: P and dS rounded to bf16 as MFMA operands
+    # (measured on MI355X: dQ 3.6-3.8e-3, dK 2.8-2.9e-3, dV 2.1-2.2e-3), held to bars 1.6-1.8x above.
+    o, lse = res[0], res[1]
+    bdq, bdk, bdv = oatt.attention_backward(q, k, v, o.double(), lse.double(), do, scale=scale,
+                                            dtype=torch.float64)
+    errs = [rel_l2(got, want) for got, want in ((res[2], bdq), (res[3], bdk), (res[4], bdv))]
+    print("  backward given the kernel's O, L: rel-L2 dQ %.2e dK %.2e dV %.2e" % tuple(errs), flush=True)
+    for err, bar in zip(errs, (6e-3, 5e-3, 4e-3)):
+        assert err <= bar
 
 
 @pytest.mark.parametrize(("lengths", "hq", "hkv", "d"), [
