@@ -738,6 +738,10 @@ def pmc_summary(command: str, *dirs: str) -> str:
         cw = max(max(merged[k]["WRITE_SIZE"].values()) for k in copy if "WRITE_SIZE" in merged[k])
         cal.update(copy_bytes=PMC_COPY_BYTES, fetch_kib=cf, write_kib=cw,
                    fetch_factor=PMC_COPY_BYTES / (cf * 1024.0), write_factor=PMC_COPY_BYTES / (cw * 1024.0))
+    if any("TCC_EA0_RDREQ_DRAM_32B_sum" in merged[k] for k in copy):
+        cd = max(max(merged[k]["TCC_EA0_RDREQ_DRAM_32B_sum"].values()) for k in copy
+                 if "TCC_EA0_RDREQ_DRAM_32B_sum" in merged[k])
+        cal.update(dram_read_32b=cd, dram_read_factor=PMC_COPY_BYTES / (cd * 32.0))
     ceil = next((k for k in merged if "mfma_ceiling" in k), None)
     if ceil and "SQ_VALU_MFMA_BUSY_CYCLES" in mean[ceil]:
         c = mean[ceil]
@@ -762,6 +766,13 @@ def pmc_summary(command: str, *dirs: str) -> str:
             r["executed_bf16_tflop"] = m["SQ_INSTS_VALU_MFMA_MOPS_BF16"] * 512.0 / 1e12
         if "GRBM_GUI_ACTIVE" in m:
             r["gui_active_cycles"] = m["GRBM_GUI_ACTIVE"]
+        if "TCC_EA0_RDREQ_DRAM_32B_sum" in m:
+            r["dram_read_bytes"] = m["TCC_EA0_RDREQ_DRAM_32B_sum"] * 32.0
+        if "TCC_EA0_WRREQ_DRAM_sum" in m:
+            r["dram_write_requests"] = m["TCC_EA0_WRREQ_DRAM_sum"]
+        if "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum" in m and m.get("GRBM_GUI_ACTIVE"):
+            # GRBM_GUI_ACTIVE sums the 8 XCDs' cycles; each XCD has 16 L2 channels
+            r["dram_read_credit_stall_frac"] = m["TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum"] / (16.0 * m["GRBM_GUI_ACTIVE"])
         short = k[len("mtp::"):]
         if short in algorithmic_bytes:
             r["algorithmic_bytes"] = algorithmic_bytes[short]
@@ -778,8 +789,17 @@ def pmc_summary(command: str, *dirs: str) -> str:
         lines += ["MFMA busy = SQ_VALU_MFMA_BUSY_CYCLES / (4 x SQ_BUSY_CU_CYCLES); the register-only MFMA loop "
                   f"(`mfma_ceiling_kernel`) reads {cal['mfma_busy_ceiling_kernel']:.3f}. Executed bf16 TFLOP = "
                   "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512.", ""]
-    lines += ["| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB | MFMA busy | "
-              "executed bf16 TFLOP |", "|---|---:|---:|---:|---:|---:|---:|---:|"]
+    if "dram_read_factor" in cal:
+        lines += [f"DRAM side: TCC_EA0_RDREQ_DRAM_32B_sum counts the L2's read requests to the memory side in "
+                  f"32-byte units; the same copy read {cal['dram_read_32b']:.0f} of them "
+                  f"({cal['dram_read_32b'] * 32 / PMC_COPY_BYTES:.4f} x its bytes). The memory-side cache (MALL) "
+                  "sits behind that interface, so these bytes still include MALL hits: no counter exposed on "
+                  "this image separates MALL from HBM. Read credit stall = "
+                  "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum / (16 channels x GRBM_GUI_ACTIVE): the fraction of L2 "
+                  "channel cycles that waited for memory-side read credits.", ""]
+    lines += ["| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB | DRAM-side read GB | "
+              "read credit stall | MFMA busy | executed bf16 TFLOP |",
+              "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
 
     def f(x, scale=1e9, fmt="{:.3f}"):
         return "" if x is None else fmt.format(x / scale)
@@ -787,6 +807,7 @@ def pmc_summary(command: str, *dirs: str) -> str:
     for k, r in kernels.items():
         lines.append(f"| `{k}` | {r['dispatches']} | {f(r.get('fetch_bytes'))} | {f(r.get('write_bytes'))} | "
                      f"{f(r.get('traffic_bytes'))} | {f(r.get('algorithmic_bytes'))} | "
+                     f"{f(r.get('dram_read_bytes'))} | {f(r.get('dram_read_credit_stall_frac'), 1, '{:.3f}')} | "
                      f"{f(r.get('mfma_busy'), 1, '{:.3f}')} | {f(r.get('executed_bf16_tflop'), 1, '{:.3f}')} |")
     blob = {"calibration": cal, "kernels": kernels}
     lines += ["", "```json", json.dumps(blob, indent=1), "```", ""]

@@ -203,7 +203,7 @@ def _prewarm(model: Any, *, impl: str, seq_len: int, batch_size: int, hq: int, h
     runs the packed instantiations and the backward's work-order sort. A model on the CPU skips it
     (there is nothing to load), as does a dtype the kernels do not take."""
     where = _model_device_dtype(model)
-    if where is None or where[0].type != "cuda" or where[1] != torch.bfloat16:
+    if where is None or where[0].type != "cuda" or where[1] not in (torch.bfloat16, torch.float32):
         return
     dev, dt = where
     q = torch.zeros((batch_size, hq, seq_len, head_dim), dtype=dt, device=dev, requires_grad=True)
@@ -225,7 +225,7 @@ def enable_flash_attention(model: Any, *, impl: str = "auto", seq_len: int | Non
     `impl`: forwarded to `flash_attention` per call ("auto"/"kernel" -> HIP kernels,
     "reference" -> the materialized oracle, small shapes only). `seq_len`/`batch_size`: when given
     with a kernel impl, the launch plan for that shape is computed now, so an unsupported shape fails
-    at enable time, and a model already on the GPU in bf16 runs one zeros forward + backward at that
+    at enable time, and a model already on the GPU in bf16 or fp32 runs one zeros forward + backward at that
     shape (`packed=True`: also one with a single-segment `PackedMask`, the packed kernels a
     `mtp_segments=` / `PackedMask` step will launch), as the reference pre-warms its rate caches."""
     cfg = _config_of(model)
