@@ -742,6 +742,11 @@ def pmc_summary(command: str, *dirs: str) -> str:
         cd = max(max(merged[k]["TCC_EA0_RDREQ_DRAM_32B_sum"].values()) for k in copy
                  if "TCC_EA0_RDREQ_DRAM_32B_sum" in merged[k])
         cal.update(dram_read_32b=cd, dram_read_factor=PMC_COPY_BYTES / (cd * 32.0))
+        big = max((k for k in copy if "TCC_EA0_RDREQ_DRAM_32B_sum" in merged[k]),
+                  key=lambda k: max(merged[k]["TCC_EA0_RDREQ_DRAM_32B_sum"].values()))
+        m = mean[big]
+        if m.get("TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum") is not None and m.get("GRBM_GUI_ACTIVE"):
+            cal["copy_read_credit_stall_frac"] = m["TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum"] / (16.0 * m["GRBM_GUI_ACTIVE"])
     ceil = next((k for k in merged if "mfma_ceiling" in k), None)
     if ceil and "SQ_VALU_MFMA_BUSY_CYCLES" in mean[ceil]:
         c = mean[ceil]
@@ -796,7 +801,10 @@ def pmc_summary(command: str, *dirs: str) -> str:
                   "sits behind that interface, so these bytes still include MALL hits: no counter exposed on "
                   "this image separates MALL from HBM. Read credit stall = "
                   "TCC_EA0_RDREQ_DRAM_CREDIT_STALL_sum / (16 channels x GRBM_GUI_ACTIVE): the fraction of L2 "
-                  "channel cycles that waited for memory-side read credits.", ""]
+                  "channel cycles that waited for memory-side read credits"
+                  + (f". The HBM-bound copy reads {cal['copy_read_credit_stall_frac']:.3f}, so a low value does "
+                     "not show memory-side headroom; only high values mean much."
+                     if "copy_read_credit_stall_frac" in cal else "."), ""]
     lines += ["| kernel | dispatches | fetch GB | write GB | traffic GB | algorithmic GB | DRAM-side read GB | "
               "read credit stall | MFMA busy | executed bf16 TFLOP |",
               "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
