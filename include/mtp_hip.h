@@ -203,7 +203,9 @@ int mtp_lce_fwd_f32(const float* hidden, const float* w, const uint32_t* w_q, co
 /* Vocab columns per fp32 backward chunk (a multiple of 128) for a workspace budget in bytes. */
 int64_t mtp_lce_bwd_f32_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
-/* Workspace bytes of mtp_lce_bwd_f32 at a chunk: the fp32 gradient tile [n][chunk + 4]. */
+/* Workspace bytes of mtp_lce_bwd_f32 at a chunk: the fp32 gradient tile [n][chunk + 4], then, when
+ * the dH product of a chunk splits its contraction to fill the GPU (small n x d, e.g. BASELINE
+ * config 1: 16 parts), fp32 partial dH [parts][n][d] summed in part order. */
 size_t mtp_lce_bwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int64_t chunk);
 
 /* fp32 backward, as mtp_lce_bwd with g = (exp(z - lse) - onehot) * d_nll kept in fp32 (the

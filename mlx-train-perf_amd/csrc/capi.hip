@@ -425,10 +425,10 @@ int64_t mtp_lce_bwd_f32_chunk(int64_t n, int64_t d, int64_t v, size_t budget_byt
 }
 
 size_t mtp_lce_bwd_f32_workspace_bytes(int64_t n, int64_t d, int64_t v, int64_t chunk) {
-  (void)d;
   if (n < 1 || v < 1 || chunk < 128 || chunk % 128) return 0;
   if (chunk > round_up(v, 128)) chunk = round_up(v, 128);
-  return (size_t)n * (size_t)(chunk + 4) * sizeof(float);
+  const int np = mtp::lce32_dh_parts((long)n, (long)d, (long)(chunk < v ? chunk : v), nullptr);
+  return (size_t)n * (size_t)(chunk + 4) * sizeof(float) + (np > 1 ? (size_t)np * (size_t)n * (size_t)d * sizeof(float) : 0);
 }
 
 int mtp_lce_bwd_f32(const float* hidden, const float* w, const uint32_t* w_q, const float* scales, const float* biases,

@@ -390,21 +390,40 @@ __device__ __forceinline__ void gemm_store(const SA& sa, const SB& sb, int K, in
 }
 
 // dH[t][d] (+)= sum_v G[t][v] W[v][d] over one chunk: A = G rows, B = the chunk's W rows read k-major.
+// dH for one vocab chunk, its contraction (the chunk's columns) split into parts of `per` columns
+// (blockIdx.z = part; one part: per >= kcols) so that a small output grid still fills the GPU. With
+// one part the tile goes to dH (written by the first chunk, accumulated by the others); with several,
+// each part's tile goes to its own fp32 slice part_out[z] and lce32_dh_reduce_kernel sums them in
+// part order.
 template <int Q4, bool ACC>
 __global__ __launch_bounds__(256) void lce32_dh_kernel(const float* __restrict__ G, long ldg, const float* __restrict__ W,
                                                        const uint32_t* __restrict__ Wq, const float* __restrict__ Sc,
-                                                       const float* __restrict__ Bi, int D, int c0, int kcols, int nrows,
-                                                       float* __restrict__ dH) {
+                                                       const float* __restrict__ Bi, int D, int c0, int kcols, int per,
+                                                       int nrows, float* __restrict__ dH) {
   __shared__ __attribute__((aligned(16))) float lds[4 * kTileFloats];
   const int m0 = blockIdx.x * kT, n0 = blockIdx.y * kT;
-  RowSrc ga{G + (long)m0 * ldg, ldg, nrows - m0, kcols, ldg % 4 == 0};
+  const int k0 = blockIdx.z * per;
+  const int kn = (kcols - k0 < per) ? kcols - k0 : per;
+  float* out = dH + (long)blockIdx.z * nrows * D;
+  RowSrc ga{G + (long)m0 * ldg + k0, ldg, nrows - m0, kn, ldg % 4 == 0};
   if constexpr (Q4) {
-    Q4ColSrc wb{Q4Geom{Wq, Sc, Bi, D}, c0, D - n0, kcols, n0};
-    gemm_store<RowSrc, Q4ColSrc, ACC>(ga, wb, kcols, nrows, D, dH, D, lds);
+    Q4ColSrc wb{Q4Geom{Wq, Sc, Bi, D}, (long)c0 + k0, D - n0, kn, n0};
+    gemm_store<RowSrc, Q4ColSrc, ACC>(ga, wb, kn, nrows, D, out, D, lds);
   } else {
-    ColSrc wb{W + (long)c0 * D + n0, D, D - n0, kcols, aligned16(W) && D % 4 == 0};
-    gemm_store<RowSrc, ColSrc, ACC>(ga, wb, kcols, nrows, D, dH, D, lds);
+    ColSrc wb{W + (long)(c0 + k0) * D + n0, D, D - n0, kn, aligned16(W) && D % 4 == 0};
+    gemm_store<RowSrc, ColSrc, ACC>(ga, wb, kn, nrows, D, out, D, lds);
   }
+}
+
+// dH (+)= sum over p of parts[p], in part order (deterministic), over the n x d elements.
+template <bool ACC>
+__global__ __launch_bounds__(256) void lce32_dh_reduce_kernel(const float* __restrict__ parts, int nparts, long count,
+                                                              float* __restrict__ dH) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= count) return;
+  float x = ACC ? dH[i] : 0.f;
+  for (int p = 0; p < nparts; ++p) x += parts[(long)p * count + i];
+  dH[i] = x;
 }
 
 // dW[v][d] = sum_t G[t][v] H[t][d] for one chunk's vocab rows (all tokens): A = G read k-major
@@ -733,6 +752,22 @@ hipError_t launch_lce32_fwd(const LceHead32& h, const float* H, const int64_t* t
   return hipGetLastError();
 }
 
+// Contraction parts of the fp32 dH product of a chunk of kcols columns: about two workgroups per
+// CU over the ceil(N/128) x ceil(D/128) output tiles, each part at least 512 columns (32 stages)
+// and a multiple of 16 (one stage); at most 32. *per receives the columns per part.
+int lce32_dh_parts(long N, long D, long kcols, int* per) {
+  const long tiles = ((N + kT - 1) / kT) * ((D + kT - 1) / kT);
+  long np = (2L * kNumCU + tiles - 1) / tiles;
+  if (np > kcols / 512) np = kcols / 512;
+  if (np > 32) np = 32;
+  if (np < 1) np = 1;
+  long pc = (kcols + np - 1) / np;
+  pc = (pc + kBK - 1) / kBK * kBK;
+  np = (kcols + pc - 1) / pc;
+  if (per) *per = (int)(np == 1 ? kcols : pc);
+  return (int)np;
+}
+
 hipError_t launch_lce32_bwd(const LceHead32& h, const float* H, const int64_t* targets, const float* lse,
                             const float* dnll, int N, int D, int V, long long ignore_index, int chunk, float* dH,
                             float* dW, float* Gbuf, hipStream_t st) {
@@ -745,14 +780,28 @@ hipError_t launch_lce32_bwd(const LceHead32& h, const float* H, const int64_t* t
     else hipLaunchKernelGGL(lce32_bwd_g_kernel<0>, ggrid, block, 0, st, H, h.w, h.wq, h.sc, h.bi, targets, lse, dnll, D, V, ignore_index, 0, N, c0, kc, Gbuf, ldg);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    dim3 hgrid((N + kT - 1) / kT, (D + kT - 1) / kT);
     const bool acc = c0 > 0;
-    if (h.q4) {
-      if (acc) hipLaunchKernelGGL((lce32_dh_kernel<1, true>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, N, dH);
-      else hipLaunchKernelGGL((lce32_dh_kernel<1, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, N, dH);
+    int per = kc;
+    const int np = lce32_dh_parts(N, D, kc, &per);
+    dim3 hgrid((N + kT - 1) / kT, (D + kT - 1) / kT, np);
+    if (np == 1) {
+      if (h.q4) {
+        if (acc) hipLaunchKernelGGL((lce32_dh_kernel<1, true>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, dH);
+        else hipLaunchKernelGGL((lce32_dh_kernel<1, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, dH);
+      } else {
+        if (acc) hipLaunchKernelGGL((lce32_dh_kernel<0, true>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, dH);
+        else hipLaunchKernelGGL((lce32_dh_kernel<0, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, dH);
+      }
     } else {
-      if (acc) hipLaunchKernelGGL((lce32_dh_kernel<0, true>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, N, dH);
-      else hipLaunchKernelGGL((lce32_dh_kernel<0, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, N, dH);
+      float* parts = Gbuf + (long)N * ldg;   // after the gradient tile: [np][N][D]
+      if (h.q4) hipLaunchKernelGGL((lce32_dh_kernel<1, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, parts);
+      else hipLaunchKernelGGL((lce32_dh_kernel<0, false>), hgrid, block, 0, st, Gbuf, ldg, h.w, h.wq, h.sc, h.bi, D, c0, kc, per, N, parts);
+      e = hipGetLastError();
+      if (e != hipSuccess) return e;
+      const long count = (long)N * D;
+      dim3 rgrid((unsigned)((count + 255) / 256));
+      if (acc) hipLaunchKernelGGL(lce32_dh_reduce_kernel<true>, rgrid, block, 0, st, parts, np, count, dH);
+      else hipLaunchKernelGGL(lce32_dh_reduce_kernel<false>, rgrid, block, 0, st, parts, np, count, dH);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;

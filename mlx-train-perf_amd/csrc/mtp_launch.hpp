@@ -71,6 +71,7 @@ struct LceHead32 {
   const float* bi;
 };
 int lce32_fwd_nsplit(long N, long V);
+int lce32_dh_parts(long N, long D, long kcols, int* per);
 hipError_t launch_lce32_fwd(const LceHead32& h, const float* H, const int64_t* targets, int N, int D, int V,
                             long long ignore_index, float* nll, float* lse, float* tgt, float* ws, hipStream_t stream);
 // Gbuf: fp32 [N][chunk + 4]; dH fp32 [N][D]; dW (optional, dense head) fp32 [V][D].

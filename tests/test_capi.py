@@ -167,7 +167,12 @@ def test_fp32_entry_points_plan_and_refuse():
     assert lib.mtp_lce_fwd_f32_workspace_bytes(0, 512, 32000, 0) == 0
     # backward: one fp32 gradient tile [n][chunk + 4]; the whole padded vocab when it fits the budget
     assert lib.mtp_lce_bwd_f32_chunk(1024, 512, 32000, 3 << 29) == 32000
-    assert lib.mtp_lce_bwd_f32_workspace_bytes(1024, 512, 32000, 32000) == 1024 * 32004 * 4
+    # config 1: 8 x 4 output tiles of dH -> 16 contraction parts of fp32 partial dH after the g tile
+    assert lib.mtp_lce_bwd_f32_workspace_bytes(1024, 512, 32000, 32000) == 1024 * 32004 * 4 + 16 * 1024 * 512 * 4
+    # a large output grid (64 x 32 tiles) keeps one part: no partials
+    assert lib.mtp_lce_bwd_f32_workspace_bytes(8192, 4096, 151936, 1024) == 8192 * 1028 * 4
+    # a chunk too short for two 512-column parts keeps one part as well
+    assert lib.mtp_lce_bwd_f32_workspace_bytes(1024, 512, 32000, 896) == 1024 * 900 * 4
     c = lib.mtp_lce_bwd_f32_chunk(8192, 4096, 151936, 1 << 30)
     assert c % 128 == 0 and 8192 * (c + 4) * 4 <= 1 << 30 < 8192 * (c + 132) * 4
     assert lib.mtp_lce_bwd_f32_chunk(8, 64, 100, 1) == 128    # at least one 128-column tile

@@ -109,6 +109,14 @@ def test_lce_fp32_config1():
     linear_cross_entropy(hd3, DenseHead(weight=wd3, trainable=True), tc, reduction="mean", chunk_size=128).backward()
     assert rel_l2(hd3.grad.cpu(), odh) < 1e-5 and rel_l2(wd3.grad.cpu(), odw) < 1e-5
 
+    # 4096-column chunks: each chunk's dH product splits its contraction (8 parts, 6 in the last
+    # chunk) and the part sums accumulate into dH over 8 chunks
+    hd4 = hc.clone().requires_grad_(True)
+    linear_cross_entropy(hd4, DenseHead(weight=wc, trainable=False), tc, reduction="mean", chunk_size=4096).backward()
+    r4 = rel_l2(hd4.grad.cpu(), odh)
+    print(f"  dH rel-L2 with 4096-column chunks {r4:.2e}", flush=True)
+    assert r4 < 1e-5
+
 
 def test_lce_fp32_quantized_head():
     """A 4-bit head with fp32 hidden states: against the oracle on the head dequantized in fp64 (the
