@@ -402,10 +402,11 @@ def _attn_inputs(s, seed=0, b=ATT_B, dh=ATT_DH):
     return mk(ATT_HQ), mk(ATT_HKV), mk(ATT_HKV), mk(ATT_HQ)
 
 
-def bench_attention(steps, warmup, mode="causal", s=None, dh=ATT_DH):
+def bench_attention(steps, warmup, mode="causal", s=None, dh=ATT_DH, fp32=False):
     """Flash attention fwd and fwd+bwd at B=1, Hq=32, Hkv=8, head_dim `dh` (128: configs 4, 5). mode:
     "causal" (config 4, S=8192), "packed" (config 5, S=16384, seeded document lengths), "full"
-    (non-causal, S=8192)."""
+    (non-causal, S=8192). `fp32`: the same inputs in fp32 on the fp32 kernels, rated against the fp32
+    MFMA peak."""
     import torch
 
     from mlx_train_perf.attention.api import kernel_backward, kernel_forward
@@ -413,6 +414,8 @@ def bench_attention(steps, warmup, mode="causal", s=None, dh=ATT_DH):
 
     s = s or (16384 if mode == "packed" else 8192)
     q, k, v, do = _attn_inputs(s, dh=dh)
+    if fp32:
+        q, k, v, do = (x.float() for x in (q, k, v, do))
     scale = 1.0 / math.sqrt(dh)
     sid = sst = None
     causal = mode != "full"
@@ -455,7 +458,7 @@ def bench_attention(steps, warmup, mode="causal", s=None, dh=ATT_DH):
     out = {"seq": s, "fwd_ms": fwd_s * 1e3, "fwdbwd_ms": fb_s * 1e3, "bwd_ms": (fb_s - fwd_s) * 1e3,
            "pairs_per_head": pairs, "algorithmic_tflop": flops_fb / 1e12,
            "fwd_tflops": flops_fwd / fwd_s / 1e12, "tflops": flops_fb / fb_s / 1e12,
-           "mfma_frac": flops_fb / fb_s / 1e12 / PEAK_BF16_TFLOPS,
+           "mfma_frac": flops_fb / fb_s / 1e12 / (PEAK_FP32_TFLOPS if fp32 else PEAK_BF16_TFLOPS),
            "fwd_marginal_peak_gb": fwd_peak / 1e9, "fwdbwd_marginal_peak_gb": fb_peak / 1e9}
     if mode == "packed":
         out["segments"] = len(lens)
@@ -967,6 +970,8 @@ def main():
     if not args.no_extras and "fp32" in parts:
         torch.cuda.empty_cache()
         result["lce_fp32_c1"] = bench_lce_fp32_c1(max(5, args.steps), 2)
+        torch.cuda.empty_cache()
+        result["attention_fp32_causal_s8192"] = bench_attention(3, 1, "causal", fp32=True)
     if not args.no_extras and "ladder" in parts:
         torch.cuda.empty_cache()
         result["lce_ladder_fwd"] = lce_ladder()
