@@ -901,29 +901,51 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
   // folded into the exponent's fma.
   auto consume = [&](f32x16 (&acc)[4][kNJ], int v0) {
     const bool tail = (v0 + kTile) > V;
+    if (tail) {
 #pragma unroll
-    for (int j = 0; j < kNJ; ++j) {
-      float mz = kNegInf;
+      for (int j = 0; j < kNJ; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          if (tail) {
+          for (int r = 0; r < 16; ++r) {
             const int v = v0 + 128 * wa + 32 * i + 8 * (r >> 2) + 4 * lhalf + (r & 3);
             if (v >= V) acc[i][j][r] = kNegInf;
           }
-          mz = fmaxf(mz, acc[i][j][r]);
-        }
-      const float mx = mz * kLog2e;
-      const float mn = fmaxf(m[j], mx);
-      const float base = (mn == kNegInf) ? 0.f : mn;
-      float sum = 0.f;
+    }
+    // Four partial maxima and sums per token column, combined in a fixed order: four short
+    // dependency chains instead of one 64 long (forward -1%).
+    float pm[kNJ][4], ps[kNJ][4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < kNJ; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) sum += fast_exp2(__builtin_fmaf(acc[i][j][r], kLog2e, -base));
-      s[j] = s[j] * fast_exp2(m[j] - base) + sum;
-      m[j] = mn;
+      for (int u = 0; u < 4; ++u) pm[j][u] = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j) pm[j][r & 3] = fmaxf(pm[j][r & 3], acc[i][j][r]);
+    float base[kNJ], mn[kNJ];
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+      const float a0 = fmaxf(fmaxf(pm[j][0], pm[j][1]), fmaxf(pm[j][2], pm[j][3]));
+      mn[j] = fmaxf(m[j], a0 * kLog2e);
+      base[j] = (mn[j] == kNegInf) ? 0.f : mn[j];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) ps[j][u] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+#pragma unroll
+        for (int j = 0; j < kNJ; ++j)
+          ps[j][r & 3] += fast_exp2(__builtin_fmaf(acc[i][j][r], kLog2e, -base[j]));
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) {
+      const float sum = (ps[j][0] + ps[j][1]) + (ps[j][2] + ps[j][3]);
+      s[j] = s[j] * fast_exp2(m[j] - base[j]) + sum;
+      m[j] = mn[j];
     }
   };
 
