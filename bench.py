@@ -239,7 +239,9 @@ def bench_lce(steps, warmup, head_kind="dense"):
     fwd_peak, (nll, _, _) = marginal_peak_bytes(lambda: L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE))
     bwd_peak, _ = marginal_peak_bytes(lambda: nll.backward(ct))
     del nll
-    p = plan.lce_plan(n=N, v=V, d=D)
+    staged = (head_kind == "q4" and os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto") != "1"
+              and os.environ.get("MTP_LCE_Q4_STAGE", "1") != "0")
+    p = plan.lce_plan(n=N, v=V, d=D, q4_staged=staged)
     head_t = L.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,
             "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),
@@ -937,25 +939,33 @@ def main():
         q4 = bench_lce(max(3, args.steps // 4), 1, "q4")
         result["qlora_lce"] = {**q4, "tokens_per_s": N / q4["sec_per_step"],
                                "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
-        # The same step without the cached bf16 transposed head (the dH product dequantizes the 4-bit
-        # head in registers as well): the memory / time trade of MTP_LCE_TRANSPOSED_HEAD=0.
+        # The default 4-bit backward stages each vocab chunk of the head, dequantized and transposed,
+        # in its workspace. The same step with the whole head kept as a cached bf16 transposed copy
+        # (MTP_LCE_TRANSPOSED_HEAD=1), and with neither (MTP_LCE_Q4_STAGE=0: the dH product
+        # dequantizes the packed words in registers): the memory / time trades of the 4-bit backward.
         from mlx_train_perf.core import loss as L
-        prev = os.environ.get("MTP_LCE_TRANSPOSED_HEAD")
-        os.environ["MTP_LCE_TRANSPOSED_HEAD"] = "0"
+        keys = ("MTP_LCE_TRANSPOSED_HEAD", "MTP_LCE_Q4_STAGE")
+        prev = {k: os.environ.get(k) for k in keys}
+        runs = {}
         try:
-            L.clear_transposed_head_cache()
-            torch.cuda.empty_cache()
-            q4n = bench_lce(3, 1, "q4")
+            for name, copy, stage in (("head_copy", "1", "1"), ("in_register", "0", "0")):
+                os.environ["MTP_LCE_TRANSPOSED_HEAD"] = copy
+                os.environ["MTP_LCE_Q4_STAGE"] = stage
+                L.clear_transposed_head_cache()
+                torch.cuda.empty_cache()
+                q4n = bench_lce(3, 1, "q4")
+                runs[name] = {"ms_per_step": q4n["sec_per_step"] * 1e3, "tokens_per_s": N / q4n["sec_per_step"],
+                              "bwd_ms": q4n["bwd_ms"], "bwd_chunks": q4n["bwd_chunks"],
+                              "bwd_marginal_peak_gb": q4n["bwd_marginal_peak_gb"],
+                              "bwd_footprint_gb": q4n["bwd_footprint_gb"]}
         finally:
-            # the user's setting (or its absence) holds for the parts that follow
-            if prev is None:
-                del os.environ["MTP_LCE_TRANSPOSED_HEAD"]
-            else:
-                os.environ["MTP_LCE_TRANSPOSED_HEAD"] = prev
-        result["qlora_lce"]["no_head_copy"] = {
-            "ms_per_step": q4n["sec_per_step"] * 1e3, "tokens_per_s": N / q4n["sec_per_step"],
-            "bwd_ms": q4n["bwd_ms"], "bwd_marginal_peak_gb": q4n["bwd_marginal_peak_gb"],
-            "bwd_footprint_gb": q4n["bwd_footprint_gb"]}
+            # the user's settings (or their absence) hold for the parts that follow
+            for k, val in prev.items():
+                if val is None:
+                    os.environ.pop(k, None)
+                else:
+                    os.environ[k] = val
+        result["qlora_lce"].update(runs)
     if not args.no_extras and "trainable" in parts:
         torch.cuda.empty_cache()
         result["trainable_head_lce"] = bench_trainable_lce(max(3, args.steps // 4), 1)

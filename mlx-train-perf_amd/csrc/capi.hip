@@ -55,7 +55,7 @@ int check_lce_common(const void* hidden, const void* w, const uint32_t* w_q, con
     if (!w) return fail(MTP_ERR_INPUT, "dense head: w must be non-null");
     if (!aligned16(w)) return fail(MTP_ERR_UNSUPPORTED, "dense head: w must be 16-byte aligned");
     if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires d %% 8 == 0 for a dense head (got d=%lld); use impl='chunked'", (long long)d);
-  } else if (head_kind == MTP_HEAD_Q4) {
+  } else if (head_kind == MTP_HEAD_Q4 || head_kind == MTP_HEAD_Q4_STAGED) {
     if (!w_q || !scales || !biases) return fail(MTP_ERR_INPUT, "quantized head: w_q, scales and biases must be non-null");
     if (!aligned16(w_q)) return fail(MTP_ERR_UNSUPPORTED, "quantized head: w_q must be 16-byte aligned");
     if (d % 64 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires the quantized head's hidden dim to be a multiple of 64 (got d=%lld); use impl='chunked'", (long long)d);
@@ -67,7 +67,7 @@ int check_lce_common(const void* hidden, const void* w, const uint32_t* w_q, con
 
 mtp::LceHead make_head(const void* w, const uint32_t* w_q, const void* scales, const void* biases, int32_t head_kind) {
   mtp::LceHead h;
-  h.q4 = head_kind == MTP_HEAD_Q4;
+  h.q4 = head_kind == MTP_HEAD_Q4 || head_kind == MTP_HEAD_Q4_STAGED;
   h.w = static_cast<const mtp::bf16_t*>(w);
   h.wt = nullptr;
   h.wq = w_q;
@@ -247,13 +247,37 @@ size_t lce_bwd_parts_offset(int64_t d, int64_t v, int64_t chunk, int64_t row_blo
   return lce_bwd_acc_offset(chunk, row_block) + (nchunks > 1 ? (size_t)row_block * (size_t)d * 4 : 0);
 }
 
+// The staging buffer of MTP_HEAD_Q4_STAGED: one chunk of the head, dequantized and transposed,
+// [d][lce_head_t_ld(chunk)] bf16, after the part tiles (256-byte aligned).
+size_t lce_bwd_stage_offset(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+  return (lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block) + 255) / 256 * 256;
+}
+size_t lce_bwd_stage_bytes(int64_t d, int64_t chunk) { return (size_t)d * (size_t)mtp::lce_head_t_ld((long)chunk) * 2; }
+
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block) {
-  (void)head_kind;
   if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block < 1 || row_block > n) row_block = n;
+  if (head_kind == MTP_HEAD_Q4_STAGED)
+    return lce_bwd_stage_offset(n, d, v, chunk, row_block) + lce_bwd_stage_bytes(d, chunk);
   return lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block);
+}
+
+int64_t mtp_lce_bwd_q4_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+  if (n < 1 || d < 1 || v < 1) return 0;
+  const int64_t vpad = round_up(v, kTile);
+  // All n rows in one block. Per vocab column the gradient tiles take 2 n bytes and the staged head
+  // chunk 2 d; one chunk if the whole padded vocab fits, otherwise the budget also carries the fp32
+  // dH accumulator.
+  const size_t per_col = (size_t)2 * (size_t)(n + d);
+  if (per_col * (size_t)(vpad + mtp::kGPitchPad) <= budget_bytes) return vpad;
+  const size_t acc = (size_t)n * (size_t)d * 4;
+  const size_t rest = budget_bytes > acc ? budget_bytes - acc : 0;
+  int64_t c = ((int64_t)(rest / per_col) - mtp::kGPitchPad) / kTile * kTile;
+  if (c < kTile) c = kTile;
+  if (c > vpad) c = vpad;
+  return c;
 }
 
 int64_t mtp_lce_head_t_ld(int64_t v) { return v < 1 ? 0 : (int64_t)mtp::lce_head_t_ld((long)v); }
@@ -290,6 +314,8 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   if (!aligned16(d_hidden) || (d_w && !aligned16(d_w)))
     return fail(MTP_ERR_UNSUPPORTED, "d_hidden and d_w must be 16-byte aligned");
   if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
+  if (w_t && head_kind == MTP_HEAD_Q4_STAGED)
+    return fail(MTP_ERR_INPUT, "MTP_HEAD_Q4_STAGED stages the transposed head chunk-wise: w_t must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block == 0 || row_block > n) row_block = n;
@@ -304,13 +330,17 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
   float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_acc_offset(chunk, row_block));
   float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_parts_offset(d, v, chunk, row_block));
+  mtp::bf16_t* stage = head_kind == MTP_HEAD_Q4_STAGED
+                           ? reinterpret_cast<mtp::bf16_t*>(static_cast<char*>(workspace) +
+                                                            lce_bwd_stage_offset(n, d, v, chunk, row_block))
+                           : nullptr;
   mtp::LceHead head = make_head(w, w_q, scales, biases, head_kind);
   head.wt = static_cast<const mtp::bf16_t*>(w_t);
   hipError_t e = mtp::launch_lce_bwd(head, static_cast<const mtp::bf16_t*>(hidden),
                                      targets, lse, d_nll, (int)n, (int)d, (int)v, (long long)ignore_index, (int)chunk,
                                      (int)row_block,
                                      static_cast<mtp::bf16_t*>(d_hidden), static_cast<mtp::bf16_t*>(d_w), gbuf, acc32,
-                                     parts, static_cast<hipStream_t>(stream));
+                                     parts, stage, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce backward launch failed: %s", hipGetErrorString(e));
   return ok();
 }

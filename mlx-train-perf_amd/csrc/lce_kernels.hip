@@ -1444,11 +1444,13 @@ __device__ __forceinline__ bool xcd_split_tile(int mtiles, int ntiles, int kspli
 // [p kt / ksplit, (p + 1) kt / ksplit) of the chunk's kt) and stores the fp32 tile to
 // parts[p][tile][256][256] (tile = row tile * dtiles + column tile); lce_bwd_dh_reduce_kernel sums
 // the parts in order and applies the mode.
+// Wt (optional): the transposed head, rows d of pitch ldt, whose column tcol0 holds vocab row
+// v_begin: the whole cached head (tcol0 = v_begin) or one chunk staged in the workspace (0).
 // ------------------------------------------------------------------------------------------
 template <int Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16_t* __restrict__ W,
-                       const bf16_t* __restrict__ Wt, int ldt, const uint32_t* __restrict__ Wq,
+                       const bf16_t* __restrict__ Wt, int ldt, int tcol0, const uint32_t* __restrict__ Wq,
                        const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, int N, int D, int V,
                        int v_begin, int v_end, float* __restrict__ acc32, bf16_t* __restrict__ dH, int mode,
                        int ksplit, int split_a, float* __restrict__ parts) {
@@ -1487,7 +1489,7 @@ void lce_bwd_dh_kernel(const bf16_t* __restrict__ G, int ldg, int kc, const bf16
     DmaRowOp oa;
     oa.init(G + (long)t0 * ldg + koff, ldg, N - t0);
     DmaRowOp ob;
-    ob.init(Wt + (long)d0 * ldt + vb, ldt, D - d0);
+    ob.init(Wt + (long)d0 * ldt + tcol0 + koff, ldt, D - d0);
     gemm_dma(oa, ob, nk, lds, acc, false, false, NoNext{});
   } else if (D % kBK == 0) {
     // G columns past the chunk's last vocab row are zeros, so the head rows they meet only need
@@ -1661,41 +1663,47 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
                                                                  const bf16_t* __restrict__ Bi, int V, int D,
                                                                  int ldt, bf16_t* __restrict__ Wt) {
   __shared__ uint16_t tile[64][64 + 2];
-  const int v0 = blockIdx.x * 64, d0 = blockIdx.y * 64;
+  // One workgroup per 64 vocab rows, walking the hidden dim in 64-wide tiles: the rows' memory lines
+  // (packed words, scales and biases of a 4-bit head) are read by one workgroup in turn and stay in
+  // its L2 between tiles, instead of being fetched once per tile by workgroups on other XCDs.
+  const int v0 = blockIdx.x * 64;
   const int t = threadIdx.x;
+  for (int d0 = 0; d0 < D; d0 += 64) {
 #pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int id = t + 256 * p;
-    const int r = id >> 3, c = id & 7;
-    const int v = v0 + r, d = d0 + 8 * c;
-    u32x4 x = zero4();
-    if (v < V && d < D) {
-      if constexpr (Q4) {
-        const long g = (long)v * (D >> 6) + (d >> 6);
-        x = dequant8(Wq[(long)v * (D >> 3) + (d >> 3)], bf16_to_f32(Sc[g]), bf16_to_f32(Bi[g]));
-      } else {
-        x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
+    for (int p = 0; p < 2; ++p) {
+      const int id = t + 256 * p;
+      const int r = id >> 3, c = id & 7;
+      const int v = v0 + r, d = d0 + 8 * c;
+      u32x4 x = zero4();
+      if (v < V && d < D) {
+        if constexpr (Q4) {
+          const long g = (long)v * (D >> 6) + (d >> 6);
+          x = dequant8(Wq[(long)v * (D >> 3) + (d >> 3)], bf16_to_f32(Sc[g]), bf16_to_f32(Bi[g]));
+        } else {
+          x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        tile[r][8 * c + 2 * e] = (uint16_t)(x[e] & 0xffffu);
+        tile[r][8 * c + 2 * e + 1] = (uint16_t)(x[e] >> 16);
       }
     }
+    __syncthreads();
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      tile[r][8 * c + 2 * e] = (uint16_t)(x[e] & 0xffffu);
-      tile[r][8 * c + 2 * e + 1] = (uint16_t)(x[e] >> 16);
+    for (int p = 0; p < 2; ++p) {
+      const int id = t + 256 * p;
+      const int r = id >> 3, c = id & 7;
+      const int d = d0 + r, v = v0 + 8 * c;
+      if (d < D) {
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = (uint32_t)tile[8 * c + 2 * e][r] | ((uint32_t)tile[8 * c + 2 * e + 1][r] << 16);
+        *reinterpret_cast<u32x4*>(Wt + (long)d * ldt + v) = y;
+      }
     }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int p = 0; p < 2; ++p) {
-    const int id = t + 256 * p;
-    const int r = id >> 3, c = id & 7;
-    const int d = d0 + r, v = v0 + 8 * c;
-    if (d < D) {
-      u32x4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        y[e] = (uint32_t)tile[8 * c + 2 * e][r] | ((uint32_t)tile[8 * c + 2 * e + 1][r] << 16);
-      *reinterpret_cast<u32x4*>(Wt + (long)d * ldt + v) = y;
-    }
+    __syncthreads();
   }
 }
 
@@ -1703,7 +1711,7 @@ long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad
 
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream) {
   const int ldt = (int)lce_head_t_ld(V);
-  dim3 grid(ldt / 64, (D + 63) / 64), block(256);
+  dim3 grid(ldt / 64), block(256);
   if (h.q4) hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
   else hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
   return hipGetLastError();
@@ -1816,7 +1824,7 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 // One block of rows [0, N) of the backward (all its vocab chunks).
 static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                                const float* dnll, int N, int D, int V, long long ignore_index, int chunk,
-                               bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts,
+                               bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, bf16_t* stage,
                                hipStream_t stream) {
   const int rtiles = (N + kTile - 1) / kTile;
   const int dtiles = (D + kTile - 1) / kTile;
@@ -1861,6 +1869,21 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
     else if (c == 0) mode = 0;
     else if (c == nchunks - 1) mode = 2;
     else mode = 1;
+    // A 4-bit head without the cached transposed copy but with a staging buffer: the chunk's rows
+    // of the head, dequantized and transposed into the buffer, then read like the cached copy.
+    const bf16_t* wt = h.wt;
+    int ldw = ldt, tcol0 = vb;
+    if (h.q4 && wt == nullptr && stage != nullptr) {
+      LceHead hc = h;
+      hc.wq = h.wq + (long)vb * (D >> 3);
+      hc.sc = h.sc + (long)vb * (D >> 6);
+      hc.bi = h.bi + (long)vb * (D >> 6);
+      e = launch_lce_head_transpose(hc, ve - vb, D, stage, stream);
+      if (e != hipSuccess) return e;
+      wt = stage;
+      ldw = (int)lce_head_t_ld(ve - vb);
+      tcol0 = 0;
+    }
     const int ks = lce_dh_ksplit(N, D, ctiles);
     const int sa = ks > 1 ? lce_dh_split_a(rtiles, dtiles) : 0;
     dim3 hgrid(8 * rtiles * ((dtiles + 7) / 8));
@@ -1869,11 +1892,11 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
       hgrid = dim3(sa ? (blocks + 7) / 8 * 256 : rtiles * dtiles * ks);
     }
     if (h.q4) {
-      hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
-                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
+      hipLaunchKernelGGL(lce_bwd_dh_kernel<1>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, wt, ldw,
+                         tcol0, h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
     } else {
-      hipLaunchKernelGGL(lce_bwd_dh_kernel<0>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, h.wt, ldt,
-                         h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
+      hipLaunchKernelGGL(lce_bwd_dh_kernel<0>, hgrid, block, 0, stream, Gbuf, ldg, ctiles * kTile, h.w, wt, ldw,
+                         tcol0, h.wq, h.sc, h.bi, N, D, V, vb, ve, acc32, dH, mode, ks, sa, parts);
     }
     e = hipGetLastError();
     if (e != hipSuccess) return e;
@@ -1901,14 +1924,15 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
 // sums over every row, so it takes a single block.
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
-                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, hipStream_t stream) {
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, bf16_t* stage,
+                          hipStream_t stream) {
   if (dW != nullptr || row_block >= N)
-    return lce_bwd_rows(h, H, targets, lse, dnll, N, D, V, ignore_index, chunk, dH, dW, Gbuf, acc32, parts,
+    return lce_bwd_rows(h, H, targets, lse, dnll, N, D, V, ignore_index, chunk, dH, dW, Gbuf, acc32, parts, stage,
                         stream);
   for (int r0 = 0; r0 < N; r0 += row_block) {
     const int rows = (N - r0 < row_block) ? N - r0 : row_block;
     hipError_t e = lce_bwd_rows(h, H + (long)r0 * D, targets + r0, lse + r0, dnll + r0, rows, D, V, ignore_index,
-                                chunk, dH + (long)r0 * D, nullptr, Gbuf, acc32, parts, stream);
+                                chunk, dH + (long)r0 * D, nullptr, Gbuf, acc32, parts, stage, stream);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;

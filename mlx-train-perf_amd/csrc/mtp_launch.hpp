@@ -40,7 +40,8 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,
-                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, hipStream_t stream);
+                          bf16_t* dH, bf16_t* dW, bf16_t* Gbuf, float* acc32, float* parts, bf16_t* stage,
+                          hipStream_t stream);
 
 struct AttnShape {
   int b, hq, hkv, s, dh;

@@ -31,7 +31,7 @@ from mlx_train_perf.errors import (
 LIB_NAME = "libmtp_hip.so"
 LIB_PATH = Path(os.environ.get("MTP_HIP_LIB", str(Path(__file__).resolve().parent / LIB_NAME)))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 MTP_OK = 0
 MTP_ERR_INPUT = -1
 MTP_ERR_UNSUPPORTED = -2
@@ -40,6 +40,7 @@ MTP_ERR_RUNTIME = -4
 
 HEAD_DENSE = 0
 HEAD_Q4 = 1
+HEAD_Q4_STAGED = 2   # the 4-bit head's backward stages each transposed vocab chunk in the workspace
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -61,6 +62,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_lce_fwd_noalloc_max_workspace_bytes": (_size, []),
     "mtp_lce_bwd_row_block": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_chunk": (_i64, [_i64, _i64, _i64, _size]),
+    "mtp_lce_bwd_q4_stage_chunk": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64, _i64]),
     "mtp_lce_head_t_ld": (_i64, [_i64]),
     "mtp_lce_head_transpose": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,

@@ -237,7 +237,8 @@ VJP_CALLS: dict[str, int] = {}
 # Transposed copies of heads for the backward's dH product (mtp_lce_head_transpose): per device, a
 # short most-recently-used list of (owner weakref, data_ptr, shape, version) -> bf16
 # [D][mtp_lce_head_t_ld(V)]. The owner is the caller's weight tensor (the packed w_q of a 4-bit head,
-# whose copy holds the dequantized values); an in-place update through it bumps its version and
+# whose copy holds the dequantized values; kept only with MTP_LCE_TRANSPOSED_HEAD=1, since by default
+# a 4-bit backward stages each vocab chunk of it in its workspace); an in-place update through it bumps its version and
 # replaces its entry. A frozen head is therefore transposed once; a trainable one after every
 # optimizer step. Up to MTP_LCE_HEAD_T_CACHE heads (default 2) are kept per device, so two models
 # (or a model and its reference copy) on one GPU do not evict each other on every call; entries of
@@ -260,19 +261,31 @@ def clear_transposed_head_cache() -> None:
 def transposed_head_cache_bytes() -> int:
     """Device bytes held by the cached transposed heads, over all devices."""
     with _HEAD_T_LOCK:
+        _drop_freed_heads()
         return sum(t.numel() * t.element_size() for ents in _HEAD_T_CACHE.values() for _, t in ents)
+
+
+def _drop_freed_heads() -> None:
+    """Release the copies of heads that no longer exist (caller holds the lock)."""
+    for ents in _HEAD_T_CACHE.values():
+        ents[:] = [e for e in ents if e[0][0]() is not None]
 
 
 def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_kind: int, v: int,
                      d: int) -> torch.Tensor | None:
-    if owner is None or os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "1") == "0" or d % 64 != 0:
+    # MTP_LCE_TRANSPOSED_HEAD: "0" never keeps the copy, "1" keeps it for every head; by default a
+    # dense head keeps it and a 4-bit head does not (its backward stages chunk-wise instead).
+    mode = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
+    with _HEAD_T_LOCK:
+        _drop_freed_heads()
+    if owner is None or mode == "0" or d % 64 != 0 or (head_kind == _native.HEAD_Q4 and mode != "1"):
         return None
     dev = owner.device.index if owner.device.index is not None else torch.cuda.current_device()
     key = (owner.data_ptr(), tuple(owner.shape), owner._version)
     with _HEAD_T_LOCK:
         ents = _HEAD_T_CACHE.setdefault(dev, [])
-        # drop entries whose head was freed, and this head's entry from before an in-place update
-        ents[:] = [e for e in ents if e[0][0]() is not None and not (e[0][0]() is owner and e[0][1:] != key)]
+        # drop this head's entry from before an in-place update
+        ents[:] = [e for e in ents if not (e[0][0]() is owner and e[0][1:] != key)]
         for i, e in enumerate(ents):
             if e[0][0]() is owner:
                 ents.append(ents.pop(i))
@@ -332,8 +345,16 @@ class _KernelLCE(torch.autograd.Function):
         if hidden2.dtype == torch.float32:
             return _f32_backward(lib, ctx, hidden2, targets2, lse, d_nll, d_w)
         vpad = (v + 255) // 256 * 256
+        w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
+        # A 4-bit head without the cached transposed copy stages each vocab chunk of it, dequantized
+        # and transposed, in the workspace (MTP_LCE_Q4_STAGE=0: dequantize it in registers inside the
+        # dH product instead, with no staging buffer).
+        if head_kind == _native.HEAD_Q4 and w_t is None and os.environ.get("MTP_LCE_Q4_STAGE", "1") != "0":
+            head_kind = _native.HEAD_Q4_STAGED
         if ctx.bwd_chunk:   # an explicit vocab chunk: all rows in one block
             chunk, rows = min(max(256, (ctx.bwd_chunk + 255) // 256 * 256), vpad), n
+        elif head_kind == _native.HEAD_Q4_STAGED:   # every row block would stage every chunk again
+            chunk, rows = lib.mtp_lce_bwd_q4_stage_chunk(n, d, v, _plan.lce_bwd_budget_bytes()), n
         else:
             # Row blocks reuse one gradient buffer (a trainable head's dL/dW needs every row at once).
             budget = _plan.lce_bwd_budget_bytes()
@@ -342,7 +363,6 @@ class _KernelLCE(torch.autograd.Function):
         ws_bytes = lib.mtp_lce_bwd_workspace_bytes(n, d, v, head_kind, chunk, rows)
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=hidden2.device)
         d_hidden = torch.empty_like(hidden2)
-        w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
         ct = d_nll.to(torch.float32).contiguous()
         with _native.on_device(hidden2):
             rc = lib.mtp_lce_bwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_t), _native.ptr(w_q),

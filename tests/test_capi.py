@@ -24,6 +24,27 @@ def _declared_symbols() -> set[str]:
     return names
 
 
+@pytest.mark.parametrize("budget", [3 << 29, 3 << 28, 1 << 28, 1 << 30, 1 << 20])
+@pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027),
+                                           (2048, 4096, 151936), (1000, 2048, 8000), (16384, 8192, 262144)])
+def test_q4_staged_plan_agrees_with_python_planner(n, d, v, budget):
+    """The staged 4-bit backward's chunk and workspace (gradient tiles, accumulator, part tiles, then
+    the staging buffer) agree between the library and plan/launch.py, and fit the budget's terms."""
+    from mlx_train_perf import _native as N
+
+    lib = _native.load()
+    c = lib.mtp_lce_bwd_q4_stage_chunk(n, d, v, budget)
+    assert c == plan.lce_q4_stage_chunk(n, d, v, budget)
+    assert c % 256 == 0 and 256 <= c <= (v + 255) // 256 * 256
+    ws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4_STAGED, c, n)
+    assert ws == plan.lce_bwd_workspace_bytes(n, d, v, c, n, staged=True)
+    plain = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4, c, n)
+    assert ws == -(-plain // 256) * 256 + d * lib.mtp_lce_head_t_ld(c) * 2
+    if c > 256:   # a chunk above the minimum fits the budget (the part tiles are outside it)
+        nchunks = -(-v // c)
+        assert 2 * (n + d) * (c + 64) + (n * d * 4 if nchunks > 1 else 0) <= budget
+
+
 def test_library_exports_every_declared_symbol():
     lib = _native.load()
     declared = _declared_symbols()
@@ -31,7 +52,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(_native.SIGNATURES) >= declared - set()  # every export has a Python signature
-    assert lib.mtp_abi_version() == _native.ABI_VERSION == 3
+    assert lib.mtp_abi_version() == _native.ABI_VERSION == 4
 
 
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1),

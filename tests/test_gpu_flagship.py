@@ -131,20 +131,28 @@ def test_c3_flagship_lce_q4(monkeypatch):
     del w
     wdq = oquant.dequantize_affine(wq, sc, bi, group_size=64, dtype=torch.float32)
     head = QuantizedHead(w_q=wq, scales=sc, biases=bi)
+    # the default backward: each vocab chunk of the 4-bit head staged (dequantized, transposed) in
+    # the workspace
+    monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
+    monkeypatch.delenv("MTP_LCE_Q4_STAGE", raising=False)
+    L.clear_transposed_head_cache()
     nll, lse, dh, ct = _kernel_lce(h, head, t)
+    assert L.transposed_head_cache_bytes() == 0
     onll, olse, _ = olce.forward(h, wdq, t, ignore_index=IGN, dtype=torch.float64)
     odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
     _check_lce(nll, lse, dh, onll, olse, odh, t, nll_abs=8e-3)
-    # the backward without the cached transposed head: the 4-bit head dequantized in registers into
-    # the dH product's transposed operand tiles
-    print("[C3] in-register dequant backward (MTP_LCE_TRANSPOSED_HEAD=0)", flush=True)
-    monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", "0")
-    L.clear_transposed_head_cache()
-    _, _, dh2, _ = _kernel_lce(h, head, t)
-    assert (dh2[t == IGN] == 0).all()
-    r = _rel_l2(dh2, odh)
-    print(f"  dH rel-L2 {r:.3e}", flush=True)
-    assert r <= 1e-2
+    # the other two backwards: the whole head kept as a cached transposed copy, and neither copy nor
+    # staging (the packed words dequantized in registers into the dH product's transposed tiles)
+    for copy, stage in (("1", "1"), ("0", "0")):
+        print(f"[C3] backward with MTP_LCE_TRANSPOSED_HEAD={copy} MTP_LCE_Q4_STAGE={stage}", flush=True)
+        monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", copy)
+        monkeypatch.setenv("MTP_LCE_Q4_STAGE", stage)
+        L.clear_transposed_head_cache()
+        _, _, dh2, _ = _kernel_lce(h, head, t)
+        assert (dh2[t == IGN] == 0).all()
+        r = _rel_l2(dh2, odh)
+        print(f"  dH rel-L2 {r:.3e}", flush=True)
+        assert r <= 1e-2
 
 
 @pytest.mark.parametrize(("n", "d", "v"), [(16384, 64, 65536), (16384, 2048, 4096)])

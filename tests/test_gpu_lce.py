@@ -334,9 +334,10 @@ def test_backward_row_blocks_match_all_rows(n, d, v, row_block, head):
     assert rel_l2(outs[1], odh) <= 1e-2
 
 
-def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1):
-    """Forward then backward through the C-ABI (whole vocab in one chunk, all rows in one block);
-    with_wt passes the transposed (4-bit: dequantized) head made by mtp_lce_head_transpose."""
+def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1, chunk=None, staged=False):
+    """Forward then backward through the C-ABI (whole vocab in one chunk unless `chunk`, all rows in
+    one block); with_wt passes the transposed (4-bit: dequantized) head made by
+    mtp_lce_head_transpose; `staged` runs the 4-bit head's backward as MTP_HEAD_Q4_STAGED."""
     from mlx_train_perf import _native
 
     lib = _native.load()
@@ -361,8 +362,9 @@ def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1):
     nll, lse, tgt = (torch.empty(n, device="cuda") for _ in range(3))
     _native.check(lib.mtp_lce_fwd(hd.data_ptr(), *ptrs, td.data_ptr(), n, d, v, kind, IGN, nll.data_ptr(),
                                   lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), fws, stream), domain="loss")
-    chunk = (v + 255) // 256 * 256
-    bws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, kind, chunk, 0)
+    chunk = chunk or (v + 255) // 256 * 256
+    bkind = _native.HEAD_Q4_STAGED if staged else kind
+    bws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, bkind, chunk, 0)
     bw = torch.empty(bws, dtype=torch.uint8, device="cuda")
     ctd = ct.cuda()
     w_ptr, wq_ptr, sc_ptr, bi_ptr = ptrs
@@ -370,7 +372,7 @@ def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1):
     for _ in range(reps):
         dh = torch.full((n, d), 7.0, dtype=torch.bfloat16, device="cuda")
         _native.check(lib.mtp_lce_bwd(hd.data_ptr(), w_ptr, wt_ptr, wq_ptr, sc_ptr, bi_ptr, td.data_ptr(), n, d, v,
-                                      kind, IGN, lse.data_ptr(), ctd.data_ptr(), dh.data_ptr(), None, chunk, 0,
+                                      bkind, IGN, lse.data_ptr(), ctd.data_ptr(), dh.data_ptr(), None, chunk, 0,
                                       bw.data_ptr(), bws, stream), domain="loss")
         torch.cuda.synchronize()
         outs.append(dh.cpu())
@@ -404,3 +406,24 @@ def test_backward_split_contraction(n, d, v, head, with_wt):
     assert rel_l2(outs[0], odh) <= 1e-2
     assert (outs[0].double() - odh).abs().max() <= 5e-3
     assert (outs[0][t == IGN] == 0).all()
+
+
+# (n, d, v, chunk): one chunk and several (the last one partial), a split dH contraction (n = 1000,
+# d = 2048), a tiny grid and a 256-column chunk.
+@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(1000, 512, 6000, 2048), (1000, 2048, 8000, 8192),
+                                                    (300, 256, 3000, 256), (2048, 1024, 20000, 4096)])
+def test_q4_staged_backward_equals_cached_head(n, d, v, chunk):
+    """MTP_HEAD_Q4_STAGED: each vocab chunk of the 4-bit head dequantized and transposed into the
+    workspace, then read as the cached transposed head is. dH equals the cached-head backward's at the
+    same chunk bitwise, repeats bitwise, and matches the oracle."""
+    print(f"[lce q4 staged] n={n} d={d} v={v} chunk={chunk}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n + 3 * d + v, w_std=0.05)
+    ct = _cotangent(t)
+    cached, wf = _capi_backward(h, w, t, ct, head="q4", with_wt=True, chunk=chunk)
+    staged, _ = _capi_backward(h, w, t, ct, head="q4", with_wt=False, chunk=chunk, staged=True, reps=2)
+    assert torch.equal(staged[0], staged[1])
+    assert torch.equal(staged[0], cached[0])
+    _, olse, _ = olce.forward(h, wf, t, ignore_index=IGN)
+    odh = olce.backward(h, wf, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(staged[0], odh) <= 1e-2
+    assert (staged[0][t == IGN] == 0).all()

@@ -69,3 +69,38 @@ def test_planner_matches_measured_loss_peaks(trainable, monkeypatch):
     assert lo <= bwd1 <= lo + 3 * N * 4 + 3 * (2 << 20), (bwd1, lo)
     assert bwd0 - bwd1 == plan.transposed_head == L.transposed_head_cache_bytes()
     L.clear_transposed_head_cache()
+
+
+def test_planner_matches_measured_q4_staged_peaks(monkeypatch):
+    """A 4-bit head (C3) with the default staged backward: no cached copy; the backward's peak is the
+    planned workspace (gradient tiles, fp32 dH accumulator, one staged head chunk) and dH."""
+    from mlx_train_perf.core import loss as L
+    from mlx_train_perf.plan import estimate as est
+    from oracle import quant as oquant
+
+    print("[planner vs measured peaks, C3 staged]", flush=True)
+    monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
+    monkeypatch.delenv("MTP_LCE_Q4_STAGE", raising=False)
+    monkeypatch.delenv("MTP_LCE_BWD_BUDGET", raising=False)
+    h, w, t = _inputs()
+    wq, sc, bi = (x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))
+    del w
+    head = L.QuantizedHead(w_q=wq, scales=sc, biases=bi)
+    ct = torch.where(t == IGN, 0.0, 1.0 / 8192).float()
+    plan = est.loss_bytes(n=N, d=D, v=V, quantized=True)
+    assert plan.transposed_head == 0
+    dh_bytes = N * D * 2
+    L.clear_transposed_head_cache()
+    torch.cuda.empty_cache()
+    peaks = []
+    for _ in range(2):
+        hd = h.clone().requires_grad_(True)
+        fwd, (nll, _, _) = _peak(lambda: L.kernel_forward_parts(hd, head, t, ignore_index=IGN))
+        bwd, _ = _peak(lambda: nll.backward(ct))
+        peaks.append((fwd, bwd))
+    print(f"  forward {peaks[1][0]} B (plan {plan.forward_peak}); backward {peaks[1][1]} B (plan "
+          f"{plan.backward_peak} + dH {dh_bytes})", flush=True)
+    assert peaks[0][0] == peaks[1][0] == plan.forward_peak
+    lo = plan.backward_peak + dh_bytes - N * 4
+    assert lo <= peaks[1][1] <= lo + 3 * N * 4 + 3 * (2 << 20), (peaks[1][1], lo)
+    assert abs(peaks[0][1] - peaks[1][1]) <= 2 << 20 and L.transposed_head_cache_bytes() == 0
