@@ -1661,14 +1661,17 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
                                                                  const uint32_t* __restrict__ Wq,
                                                                  const bf16_t* __restrict__ Sc,
                                                                  const bf16_t* __restrict__ Bi, int V, int D,
-                                                                 int ldt, bf16_t* __restrict__ Wt) {
+                                                                 int ldt, int dspan, bf16_t* __restrict__ Wt) {
   __shared__ uint16_t tile[64][64 + 2];
-  // One workgroup per 64 vocab rows, walking the hidden dim in 64-wide tiles: the rows' memory lines
-  // (packed words, scales and biases of a 4-bit head) are read by one workgroup in turn and stay in
-  // its L2 between tiles, instead of being fetched once per tile by workgroups on other XCDs.
+  // Workgroup (x, y) transposes vocab rows [64 x, 64 x + 64) over hidden dims [dspan y, dspan (y + 1)),
+  // 64 x 64 tiles in turn. A 4-bit head takes the whole hidden dim per workgroup (dspan = D): its rows'
+  // memory lines (packed words, and scales and biases, 2 bytes of a line per 64 dims) are then read
+  // by one workgroup and stay in its L2 between tiles, instead of being fetched once per tile by
+  // workgroups on other XCDs. A dense head takes one tile per workgroup (dspan = 64).
   const int v0 = blockIdx.x * 64;
   const int t = threadIdx.x;
-  for (int d0 = 0; d0 < D; d0 += 64) {
+  const int dend = (blockIdx.y + 1) * dspan < D ? (blockIdx.y + 1) * dspan : D;
+  for (int d0 = blockIdx.y * dspan; d0 < dend; d0 += 64) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int id = t + 256 * p;
@@ -1711,9 +1714,10 @@ long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad
 
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream) {
   const int ldt = (int)lce_head_t_ld(V);
-  dim3 grid(ldt / 64), block(256);
-  if (h.q4) hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
-  else hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, Wt);
+  const int dspan = h.q4 ? D : 64;
+  dim3 grid(ldt / 64, (D + dspan - 1) / dspan), block(256);
+  if (h.q4) hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan, Wt);
+  else hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan, Wt);
   return hipGetLastError();
 }
 
