@@ -239,9 +239,10 @@ def bench_lce(steps, warmup, head_kind="dense"):
     fwd_peak, (nll, _, _) = marginal_peak_bytes(lambda: L.kernel_forward_parts(hd, head, t, ignore_index=IGNORE))
     bwd_peak, _ = marginal_peak_bytes(lambda: nll.backward(ct))
     del nll
-    staged = (head_kind == "q4" and os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto") != "1"
-              and os.environ.get("MTP_LCE_Q4_STAGE", "1") != "0")
-    p = plan.lce_plan(n=N, v=V, d=D, q4_staged=staged)
+    copy = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
+    staged = ((copy == "0" or (head_kind == "q4" and copy != "1"))
+              and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
+    p = plan.lce_plan(n=N, v=V, d=D, staged=staged)
     head_t = L.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,
             "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),
@@ -256,7 +257,9 @@ def bench_lce(steps, warmup, head_kind="dense"):
 def bench_trainable_lce(steps, warmup):
     """LCE fwd+bwd with a trainable dense head at the flagship shape: dL/dH and dL/dW (the dW kernel,
     one owner per (vocab, hidden) output tile). Four vocab-tile products per step (forward logits;
-    backward logits, dH and dW), 2 N V D flops each."""
+    backward logits, dH and dW), 2 N V D flops each. The head's backward stages its transposed vocab
+    chunks in the workspace (the default for a trainable head, whose cached copy an optimizer step
+    would invalidate; this loop takes no optimizer step)."""
     import torch
 
     from mlx_train_perf.core import loss as L
@@ -290,16 +293,20 @@ def bench_trainable_lce(steps, warmup):
 def lce_footprint_curve(steps=6):
     """The backward's memory / time trade at the flagship: the step and its backward footprint
     (marginal peak + the cached transposed head) for workspace budgets of 3, 1.5 (default) and 0.75
-    GiB, and at the default budget without the transposed head (MTP_LCE_TRANSPOSED_HEAD=0)."""
+    GiB; without the transposed head (MTP_LCE_TRANSPOSED_HEAD=0: each vocab chunk of the head staged,
+    transposed, in the workspace) at 1.5 and 0.75 GiB; and with neither copy nor staging
+    (MTP_LCE_STAGE_HEAD=0: the dH product reads W through LDS transpose reads)."""
     import torch
 
     from mlx_train_perf.core import loss as L
 
     out = {}
-    saved = {k: os.environ.get(k) for k in ("MTP_LCE_BWD_BUDGET", "MTP_LCE_TRANSPOSED_HEAD")}
+    saved = {k: os.environ.get(k) for k in ("MTP_LCE_BWD_BUDGET", "MTP_LCE_TRANSPOSED_HEAD", "MTP_LCE_STAGE_HEAD")}
     cases = (("budget_3gib", {"MTP_LCE_BWD_BUDGET": str(3 << 30)}), ("budget_1_5gib_default", {}),
              ("budget_0_75gib", {"MTP_LCE_BWD_BUDGET": str(3 << 28)}),
-             ("no_head_copy", {"MTP_LCE_TRANSPOSED_HEAD": "0"}))
+             ("no_head_copy", {"MTP_LCE_TRANSPOSED_HEAD": "0"}),
+             ("no_head_copy_0_75gib", {"MTP_LCE_TRANSPOSED_HEAD": "0", "MTP_LCE_BWD_BUDGET": str(3 << 28)}),
+             ("no_head_copy_transposed_reads", {"MTP_LCE_TRANSPOSED_HEAD": "0", "MTP_LCE_STAGE_HEAD": "0"}))
     try:
         for name, env in cases:
             for k, val in saved.items():   # each case starts from the caller's settings
@@ -941,16 +948,16 @@ def main():
                                "step_mfma_frac": flops_step / q4["sec_per_step"] / 1e12 / PEAK_BF16_TFLOPS}
         # The default 4-bit backward stages each vocab chunk of the head, dequantized and transposed,
         # in its workspace. The same step with the whole head kept as a cached bf16 transposed copy
-        # (MTP_LCE_TRANSPOSED_HEAD=1), and with neither (MTP_LCE_Q4_STAGE=0: the dH product
+        # (MTP_LCE_TRANSPOSED_HEAD=1), and with neither (MTP_LCE_STAGE_HEAD=0: the dH product
         # dequantizes the packed words in registers): the memory / time trades of the 4-bit backward.
         from mlx_train_perf.core import loss as L
-        keys = ("MTP_LCE_TRANSPOSED_HEAD", "MTP_LCE_Q4_STAGE")
+        keys = ("MTP_LCE_TRANSPOSED_HEAD", "MTP_LCE_STAGE_HEAD")
         prev = {k: os.environ.get(k) for k in keys}
         runs = {}
         try:
             for name, copy, stage in (("head_copy", "1", "1"), ("in_register", "0", "0")):
                 os.environ["MTP_LCE_TRANSPOSED_HEAD"] = copy
-                os.environ["MTP_LCE_Q4_STAGE"] = stage
+                os.environ["MTP_LCE_STAGE_HEAD"] = stage
                 L.clear_transposed_head_cache()
                 torch.cuda.empty_cache()
                 q4n = bench_lce(3, 1, "q4")

@@ -46,8 +46,13 @@ extern "C" {
  * chunk of the head into a transposed bf16 staging buffer at the end of its workspace and reads it
  * as it reads a cached transposed head: the reference's chunk-sized dequantization in its QLoRA vjp
  * (core/loss.py:333-343), with no copy of the whole head. mtp_lce_bwd and
- * mtp_lce_bwd_workspace_bytes take it; mtp_lce_fwd and mtp_lce_fwd_noalloc treat it as MTP_HEAD_Q4. */
+ * mtp_lce_bwd_workspace_bytes take it; mtp_lce_fwd and mtp_lce_fwd_noalloc treat it as MTP_HEAD_Q4
+ * (and MTP_HEAD_DENSE_STAGED below as MTP_HEAD_DENSE). */
 #define MTP_HEAD_Q4_STAGED 2
+/* The dense head of MTP_HEAD_DENSE (d a multiple of 64) whose backward stages each vocab chunk of
+ * the head, transposed, in its workspace in the same way: the alternative to keeping a transposed
+ * copy of the whole head (w_t) when memory is short. */
+#define MTP_HEAD_DENSE_STAGED 3
 
 const char* mtp_last_error(void);
 int mtp_abi_version(void);
@@ -109,14 +114,14 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
  * an fp32 [row_block][d] dH accumulator when more than one chunk is needed, and, when a block's dH
  * product splits its vocab contraction to fill the GPU, its fp32 part tiles
  * [parts][tiles][256][256] (the most any row block and chunk of the plan takes); for
- * MTP_HEAD_Q4_STAGED then the staging buffer bf16 [d][mtp_lce_head_t_ld(chunk)]. */
+ * the staged head kinds then the staging buffer bf16 [d][mtp_lce_head_t_ld(chunk)]. */
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block);
 
-/* Vocab columns per chunk (a multiple of 256) of an MTP_HEAD_Q4_STAGED backward over all n rows for
+/* Vocab columns per chunk (a multiple of 256) of a staged-head backward over all n rows for
  * a workspace budget in bytes: the gradient tiles (2 n bytes per column), the staged head chunk
  * (2 d bytes per column) and, with more than one chunk, the fp32 dH accumulator fit the budget. */
-int64_t mtp_lce_bwd_q4_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
+int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
 /* Row pitch (elements) of the transposed dense head used by mtp_lce_bwd: round_up(v, 256) + 64. */
 int64_t mtp_lce_head_t_ld(int64_t v);
@@ -136,9 +141,9 @@ int mtp_lce_head_transpose(const void* w, const uint32_t* w_q, const void* scale
  * is frozen and must pass d_w = NULL. lse is the forward's saved output (no recompute of the forward).
  * w_t (optional) is the head transposed by mtp_lce_head_transpose; it must hold the values the
  * kernels use for the head and only changes how the dH product reads it (faster when given).
- * head_kind MTP_HEAD_Q4_STAGED (w_t null) stages each vocab chunk of the 4-bit head, dequantized and
- * transposed, in the workspace instead; every row block stages every chunk again, so plan it over
- * all rows (mtp_lce_bwd_q4_stage_chunk). Results equal those with w_t given.
+ * head_kind MTP_HEAD_Q4_STAGED / MTP_HEAD_DENSE_STAGED (w_t null) stages each vocab chunk of the
+ * head, transposed (4-bit: dequantized), in the workspace instead; every row block stages every chunk
+ * again, so plan it over all rows (mtp_lce_bwd_stage_chunk). Results equal those with w_t given.
  * row_block (0 = all rows; else a multiple of 256) processes the rows in blocks that reuse one
  * gradient buffer; d_w requires all rows in one block.
  * Replaces: the kernel-path vjps _ce_vjp / _ce_frozen_vjp / quantized _ce_vjp

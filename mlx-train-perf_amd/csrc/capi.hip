@@ -51,10 +51,12 @@ int check_lce_common(const void* hidden, const void* w, const uint32_t* w_q, con
   if (n > kMaxDim || d > kMaxDim || v > kMaxDim) return fail(MTP_ERR_INPUT, "n, d, v must each be < 2^31");
   if (!hidden || !targets) return fail(MTP_ERR_INPUT, "hidden and targets must be non-null");
   if (!aligned16(hidden)) return fail(MTP_ERR_UNSUPPORTED, "hidden must be 16-byte aligned");
-  if (head_kind == MTP_HEAD_DENSE) {
+  if (head_kind == MTP_HEAD_DENSE || head_kind == MTP_HEAD_DENSE_STAGED) {
     if (!w) return fail(MTP_ERR_INPUT, "dense head: w must be non-null");
     if (!aligned16(w)) return fail(MTP_ERR_UNSUPPORTED, "dense head: w must be 16-byte aligned");
     if (d % 8 != 0) return fail(MTP_ERR_UNSUPPORTED, "kernel impl requires d %% 8 == 0 for a dense head (got d=%lld); use impl='chunked'", (long long)d);
+    if (head_kind == MTP_HEAD_DENSE_STAGED && d % 64 != 0)
+      return fail(MTP_ERR_UNSUPPORTED, "MTP_HEAD_DENSE_STAGED requires d %% 64 == 0 (got d=%lld)", (long long)d);
   } else if (head_kind == MTP_HEAD_Q4 || head_kind == MTP_HEAD_Q4_STAGED) {
     if (!w_q || !scales || !biases) return fail(MTP_ERR_INPUT, "quantized head: w_q, scales and biases must be non-null");
     if (!aligned16(w_q)) return fail(MTP_ERR_UNSUPPORTED, "quantized head: w_q must be 16-byte aligned");
@@ -225,7 +227,7 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) 
 
 // Bytes of the fp32 part tiles of a split dH product: the most any (row block, vocab chunk) of the
 // backward takes (the last row block and the last chunk may be shorter and split otherwise).
-size_t lce_dh_parts_max(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+static size_t lce_dh_parts_max(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
   const int64_t last_rows = n - (n - 1) / row_block * row_block;
   const int64_t last_tiles = (v - (v - 1) / chunk * chunk + kTile - 1) / kTile;
   size_t most = 0;
@@ -239,32 +241,34 @@ size_t lce_dh_parts_max(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t 
 
 // Gradient tiles [row_block][chunk + kGPitchPad] bf16, then the fp32 dH accumulator
 // [row_block][d] when the vocab takes more than one chunk, then the split dH's fp32 part tiles.
-size_t lce_bwd_acc_offset(int64_t chunk, int64_t row_block) {
+static size_t lce_bwd_acc_offset(int64_t chunk, int64_t row_block) {
   return (size_t)row_block * (size_t)(chunk + mtp::kGPitchPad) * 2;
 }
-size_t lce_bwd_parts_offset(int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+static size_t lce_bwd_parts_offset(int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
   const int64_t nchunks = (v + chunk - 1) / chunk;
   return lce_bwd_acc_offset(chunk, row_block) + (nchunks > 1 ? (size_t)row_block * (size_t)d * 4 : 0);
 }
 
-// The staging buffer of MTP_HEAD_Q4_STAGED: one chunk of the head, dequantized and transposed,
-// [d][lce_head_t_ld(chunk)] bf16, after the part tiles (256-byte aligned).
-size_t lce_bwd_stage_offset(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
+static bool staged_kind(int32_t head_kind) { return head_kind == MTP_HEAD_Q4_STAGED || head_kind == MTP_HEAD_DENSE_STAGED; }
+
+// The staging buffer of the MTP_HEAD_*_STAGED kinds: one chunk of the head, transposed (a 4-bit head
+// dequantized), [d][lce_head_t_ld(chunk)] bf16, after the part tiles (256-byte aligned).
+static size_t lce_bwd_stage_offset(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
   return (lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block) + 255) / 256 * 256;
 }
-size_t lce_bwd_stage_bytes(int64_t d, int64_t chunk) { return (size_t)d * (size_t)mtp::lce_head_t_ld((long)chunk) * 2; }
+static size_t lce_bwd_stage_bytes(int64_t d, int64_t chunk) { return (size_t)d * (size_t)mtp::lce_head_t_ld((long)chunk) * 2; }
 
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block) {
   if (n < 1 || d < 1 || v < 1 || chunk < kTile || chunk % kTile) return 0;
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block < 1 || row_block > n) row_block = n;
-  if (head_kind == MTP_HEAD_Q4_STAGED)
+  if (staged_kind(head_kind))
     return lce_bwd_stage_offset(n, d, v, chunk, row_block) + lce_bwd_stage_bytes(d, chunk);
   return lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block);
 }
 
-int64_t mtp_lce_bwd_q4_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
   if (n < 1 || d < 1 || v < 1) return 0;
   const int64_t vpad = round_up(v, kTile);
   // All n rows in one block. Per vocab column the gradient tiles take 2 n bytes and the staged head
@@ -313,9 +317,10 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   if (!lse || !d_nll || !d_hidden) return fail(MTP_ERR_INPUT, "lse, d_nll and d_hidden must be non-null");
   if (!aligned16(d_hidden) || (d_w && !aligned16(d_w)))
     return fail(MTP_ERR_UNSUPPORTED, "d_hidden and d_w must be 16-byte aligned");
-  if (d_w && head_kind != MTP_HEAD_DENSE) return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
-  if (w_t && head_kind == MTP_HEAD_Q4_STAGED)
-    return fail(MTP_ERR_INPUT, "MTP_HEAD_Q4_STAGED stages the transposed head chunk-wise: w_t must be null");
+  if (d_w && head_kind != MTP_HEAD_DENSE && head_kind != MTP_HEAD_DENSE_STAGED)
+    return fail(MTP_ERR_UNSUPPORTED, "a quantized head is frozen: d_w must be null");
+  if (w_t && staged_kind(head_kind))
+    return fail(MTP_ERR_INPUT, "the staged head kinds transpose the head chunk-wise: w_t must be null");
   if (chunk < kTile || chunk % kTile) return fail(MTP_ERR_INPUT, "chunk must be a positive multiple of 256 (got %lld)", (long long)chunk);
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block == 0 || row_block > n) row_block = n;
@@ -330,7 +335,7 @@ int mtp_lce_bwd(const void* hidden, const void* w, const void* w_t, const uint32
   mtp::bf16_t* gbuf = static_cast<mtp::bf16_t*>(workspace);
   float* acc32 = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_acc_offset(chunk, row_block));
   float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + lce_bwd_parts_offset(d, v, chunk, row_block));
-  mtp::bf16_t* stage = head_kind == MTP_HEAD_Q4_STAGED
+  mtp::bf16_t* stage = staged_kind(head_kind)
                            ? reinterpret_cast<mtp::bf16_t*>(static_cast<char*>(workspace) +
                                                             lce_bwd_stage_offset(n, d, v, chunk, row_block))
                            : nullptr;

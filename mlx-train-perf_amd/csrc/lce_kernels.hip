@@ -1873,15 +1873,19 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
     else if (c == 0) mode = 0;
     else if (c == nchunks - 1) mode = 2;
     else mode = 1;
-    // A 4-bit head without the cached transposed copy but with a staging buffer: the chunk's rows
-    // of the head, dequantized and transposed into the buffer, then read like the cached copy.
+    // A head without the cached transposed copy but with a staging buffer: the chunk's rows of the
+    // head, transposed (a 4-bit head dequantized) into the buffer, then read like the cached copy.
     const bf16_t* wt = h.wt;
     int ldw = ldt, tcol0 = vb;
-    if (h.q4 && wt == nullptr && stage != nullptr) {
+    if (wt == nullptr && stage != nullptr && D % kBK == 0) {
       LceHead hc = h;
-      hc.wq = h.wq + (long)vb * (D >> 3);
-      hc.sc = h.sc + (long)vb * (D >> 6);
-      hc.bi = h.bi + (long)vb * (D >> 6);
+      if (h.q4) {
+        hc.wq = h.wq + (long)vb * (D >> 3);
+        hc.sc = h.sc + (long)vb * (D >> 6);
+        hc.bi = h.bi + (long)vb * (D >> 6);
+      } else {
+        hc.w = h.w + (long)vb * D;
+      }
       e = launch_lce_head_transpose(hc, ve - vb, D, stage, stream);
       if (e != hipSuccess) return e;
       wt = stage;

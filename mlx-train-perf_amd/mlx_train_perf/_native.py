@@ -40,7 +40,8 @@ MTP_ERR_RUNTIME = -4
 
 HEAD_DENSE = 0
 HEAD_Q4 = 1
-HEAD_Q4_STAGED = 2   # the 4-bit head's backward stages each transposed vocab chunk in the workspace
+HEAD_Q4_STAGED = 2      # backward kinds that stage each transposed (4-bit: dequantized) vocab chunk
+HEAD_DENSE_STAGED = 3   # of the head in the workspace instead of reading a cached transposed copy
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -62,7 +63,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_lce_fwd_noalloc_max_workspace_bytes": (_size, []),
     "mtp_lce_bwd_row_block": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_chunk": (_i64, [_i64, _i64, _i64, _size]),
-    "mtp_lce_bwd_q4_stage_chunk": (_i64, [_i64, _i64, _i64, _size]),
+    "mtp_lce_bwd_stage_chunk": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64, _i64]),
     "mtp_lce_head_t_ld": (_i64, [_i64]),
     "mtp_lce_head_transpose": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,

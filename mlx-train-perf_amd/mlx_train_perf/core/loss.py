@@ -274,7 +274,8 @@ def _drop_freed_heads() -> None:
 def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_kind: int, v: int,
                      d: int) -> torch.Tensor | None:
     # MTP_LCE_TRANSPOSED_HEAD: "0" never keeps the copy, "1" keeps it for every head; by default a
-    # dense head keeps it and a 4-bit head does not (its backward stages chunk-wise instead).
+    # frozen dense head keeps it, and a 4-bit or trainable head does not (its backward stages
+    # chunk-wise instead).
     mode = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
     with _HEAD_T_LOCK:
         _drop_freed_heads()
@@ -345,16 +346,20 @@ class _KernelLCE(torch.autograd.Function):
         if hidden2.dtype == torch.float32:
             return _f32_backward(lib, ctx, hidden2, targets2, lse, d_nll, d_w)
         vpad = (v + 255) // 256 * 256
-        w_t = _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d)
-        # A 4-bit head without the cached transposed copy stages each vocab chunk of it, dequantized
-        # and transposed, in the workspace (MTP_LCE_Q4_STAGE=0: dequantize it in registers inside the
-        # dH product instead, with no staging buffer).
-        if head_kind == _native.HEAD_Q4 and w_t is None and os.environ.get("MTP_LCE_Q4_STAGE", "1") != "0":
-            head_kind = _native.HEAD_Q4_STAGED
+        # A trainable head changes at every optimizer step, so a cached copy would be rebuilt every
+        # step and held between them: by default its backward stages its chunks instead.
+        w_t = (None if d_w is not None and os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto") != "1"
+               else _transposed_head(ctx.owner, w, w_q, scales, biases, head_kind, v, d))
+        # A head without the cached transposed copy stages each vocab chunk of it, transposed (a 4-bit
+        # head dequantized), in the workspace (MTP_LCE_STAGE_HEAD=0: the dH product reads W through
+        # LDS transpose reads, or dequantizes the packed words in registers, with no staging buffer).
+        staged = w_t is None and d % 64 == 0 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+        if staged:
+            head_kind = _native.HEAD_Q4_STAGED if head_kind == _native.HEAD_Q4 else _native.HEAD_DENSE_STAGED
         if ctx.bwd_chunk:   # an explicit vocab chunk: all rows in one block
             chunk, rows = min(max(256, (ctx.bwd_chunk + 255) // 256 * 256), vpad), n
-        elif head_kind == _native.HEAD_Q4_STAGED:   # every row block would stage every chunk again
-            chunk, rows = lib.mtp_lce_bwd_q4_stage_chunk(n, d, v, _plan.lce_bwd_budget_bytes()), n
+        elif staged:   # every row block would stage every chunk again
+            chunk, rows = lib.mtp_lce_bwd_stage_chunk(n, d, v, _plan.lce_bwd_budget_bytes()), n
         else:
             # Row blocks reuse one gradient buffer (a trainable head's dL/dW needs every row at once).
             budget = _plan.lce_bwd_budget_bytes()

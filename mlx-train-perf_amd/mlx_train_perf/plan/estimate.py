@@ -8,7 +8,8 @@ build's kernels and workspaces:
   fp32 dH accumulator; chunked = fp32 logits chunk x 3; naive = the full (N, V) fp32 logits plus
   softmax intermediates; a trainable head adds its dL/dW (the reference's `d_w` term) and takes
   every row in one backward block; the kernel backward also keeps a transposed copy of the head, or,
-  for a 4-bit head without it, stages one transposed vocab chunk of the head in its workspace;
+  without it (a 4-bit head by default), stages one transposed vocab chunk of the head in its
+  workspace;
 - flash-attention saved state (`_flash_saved_state_bytes`, plan/estimate.py:210-220): O in the
   compute dtype plus the fp32 L per layer, and the backward's fp32 D vector.
 Whole-model terms (weights, optimizer, activations) are caller-supplied because they depend on the
@@ -54,13 +55,14 @@ class LossBytes:
         return self.transposed_head + max(self.forward_peak, self.backward_peak)
 
 
-def transposed_head_bytes(*, d: int, v: int, enabled: bool | None = None, quantized: bool = False) -> int:
+def transposed_head_bytes(*, d: int, v: int, enabled: bool | None = None, quantized: bool = False,
+                          trainable: bool = False) -> int:
     """One cached transposed head, bf16 [d][round_up(v, 256) + 64] (mtp_lce_head_t_ld), which the
-    kernel backward keeps per head when d % 64 == 0: by default for a dense head and not for a 4-bit
-    one (`MTP_LCE_TRANSPOSED_HEAD` "0": for neither, "1": for both)."""
+    kernel backward keeps per head when d % 64 == 0: by default for a frozen dense head, not for a
+    4-bit or a trainable one (`MTP_LCE_TRANSPOSED_HEAD` "0": for none, "1": for all)."""
     if enabled is None:
         mode = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
-        enabled = mode == "1" or (mode != "0" and not quantized)
+        enabled = mode == "1" or (mode != "0" and not quantized and not trainable)
     if not enabled or d % 64:
         return 0
     return d * (-(-v // _launch.TILE) * _launch.TILE + _launch.G_PITCH_PAD) * 2
@@ -71,22 +73,23 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
                transposed_head: bool | None = None, quantized: bool = False) -> LossBytes:
     """Loss-layer memory beyond its inputs: forward marginal peak, backward workspace, and (kernel
     impl) the cached transposed head; a trainable head adds its dL/dW and, on the kernel impl, takes
-    every row in one backward block. A quantized (4-bit) head without the cached copy stages each
-    vocab chunk of it in the backward's workspace instead (unless `MTP_LCE_Q4_STAGE` is "0"), over
-    all rows. The backward's returned dH (n*d*dtype) is the caller's gradient, not counted here."""
+    every row in one backward block. A head without the cached copy (a 4-bit head by default)
+    stages each vocab chunk of it in the backward's workspace instead (unless `MTP_LCE_STAGE_HEAD`
+    is "0"), over all rows. The backward's returned dH (n*d*dtype) is the caller's gradient, not
+    counted here."""
     if n < 1 or d < 1 or v < 1:
         raise PlanInputError("n, d, v must be >= 1")
     eb = dtype_bytes(dtype)
     head_grad = v * d * eb if trainable else 0
     if impl == "kernel":
-        head_t = transposed_head_bytes(d=d, v=v, enabled=transposed_head, quantized=quantized)
-        staged = quantized and head_t == 0 and os.environ.get("MTP_LCE_Q4_STAGE", "1") != "0"
+        head_t = transposed_head_bytes(d=d, v=v, enabled=transposed_head, quantized=quantized, trainable=trainable)
+        staged = head_t == 0 and d % 64 == 0 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
         fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)
         if chunk:
             bwd = _launch.lce_bwd_workspace_bytes(n, d, v, chunk, staged=staged) + n * 4
         else:
             p = _launch.lce_plan(n=n, v=v, d=d, budget=bwd_budget or _launch.lce_bwd_budget_bytes(),
-                                 trainable=trainable, q4_staged=staged)
+                                 trainable=trainable, staged=staged)
             bwd = p.bwd_workspace_bytes + n * 4
         return LossBytes(forward_peak=fwd, backward_workspace=bwd, head_grad=head_grad, transposed_head=head_t)
     elif impl == "chunked":

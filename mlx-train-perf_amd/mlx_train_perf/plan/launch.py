@@ -137,8 +137,8 @@ def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int |
                             staged: bool = False) -> int:
     """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD], the fp32 dH accumulator when >1 chunk,
     and the fp32 part tiles of a split dH product (the most any row block and chunk takes); `staged`
-    (the 4-bit head's MTP_HEAD_Q4_STAGED backward): then, 256-byte aligned, the staging buffer of one
-    dequantized transposed head chunk, bf16 [d][lce_head_t_ld(chunk)]."""
+    (the MTP_HEAD_*_STAGED backwards): then, 256-byte aligned, the staging buffer of one transposed
+    (4-bit: dequantized) head chunk, bf16 [d][lce_head_t_ld(chunk)]."""
     chunk = min(chunk, -(-v // TILE) * TILE)
     rows = n if not row_block or row_block < 1 or row_block > n else row_block
     nchunks = -(-v // chunk)
@@ -156,8 +156,8 @@ def lce_head_t_ld(v: int) -> int:
     return -(-v // TILE) * TILE + G_PITCH_PAD
 
 
-def lce_q4_stage_chunk(n: int, d: int, v: int, budget: int) -> int:
-    """Vocab columns per chunk (multiple of 256) of the staged 4-bit backward over all n rows: per
+def lce_stage_chunk(n: int, d: int, v: int, budget: int) -> int:
+    """Vocab columns per chunk (multiple of 256) of the staged backward over all n rows: per
     column 2 n bytes of gradient tiles and 2 d of the staged head chunk, plus the fp32 dH accumulator
     when the vocab takes more than one chunk, within the budget."""
     vpad = -(-v // TILE) * TILE
@@ -181,20 +181,20 @@ class LcePlan:
 
 
 def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None, trainable: bool = False,
-             q4_staged: bool = False) -> LcePlan:
+             staged: bool = False) -> LcePlan:
     """Forward splits and backward geometry. A trainable head's dL/dW sums over every row, so its
     backward takes all rows in one block (the vocab is chunked instead when they do not fit); so
-    does the staged 4-bit backward (`q4_staged`: a 4-bit head without the cached transposed copy),
-    whose chunks also carry the staged head chunk."""
+    does the staged backward (`staged`: a head without the cached transposed copy whose chunks are
+    transposed into the workspace), whose chunks also carry the staged head chunk."""
     b = lce_bwd_budget_bytes() if budget is None else budget
-    if q4_staged:
-        rows, chunk = n, lce_q4_stage_chunk(n, d, v, b)
+    if staged:
+        rows, chunk = n, lce_stage_chunk(n, d, v, b)
     else:
         rows = n if trainable else lce_bwd_row_block(n, d, v, b)
         chunk = -(-v // TILE) * TILE if rows < n else lce_bwd_chunk(n, d, v, b)
     return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=lce_fwd_workspace_bytes(n, v),
                    bwd_row_block=rows, bwd_row_blocks=-(-n // rows), bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
-                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows, staged=q4_staged))
+                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows, staged=staged))
 
 
 def attn_heads_per_workgroup(hq: int, hkv: int) -> int:

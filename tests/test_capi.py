@@ -27,17 +27,18 @@ def _declared_symbols() -> set[str]:
 @pytest.mark.parametrize("budget", [3 << 29, 3 << 28, 1 << 28, 1 << 30, 1 << 20])
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027),
                                            (2048, 4096, 151936), (1000, 2048, 8000), (16384, 8192, 262144)])
-def test_q4_staged_plan_agrees_with_python_planner(n, d, v, budget):
+def test_staged_plan_agrees_with_python_planner(n, d, v, budget):
     """The staged 4-bit backward's chunk and workspace (gradient tiles, accumulator, part tiles, then
     the staging buffer) agree between the library and plan/launch.py, and fit the budget's terms."""
     from mlx_train_perf import _native as N
 
     lib = _native.load()
-    c = lib.mtp_lce_bwd_q4_stage_chunk(n, d, v, budget)
-    assert c == plan.lce_q4_stage_chunk(n, d, v, budget)
+    c = lib.mtp_lce_bwd_stage_chunk(n, d, v, budget)
+    assert c == plan.lce_stage_chunk(n, d, v, budget)
     assert c % 256 == 0 and 256 <= c <= (v + 255) // 256 * 256
     ws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4_STAGED, c, n)
     assert ws == plan.lce_bwd_workspace_bytes(n, d, v, c, n, staged=True)
+    assert ws == lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_DENSE_STAGED, c, n)
     plain = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4, c, n)
     assert ws == -(-plain // 256) * 256 + d * lib.mtp_lce_head_t_ld(c) * 2
     if c > 256:   # a chunk above the minimum fits the budget (the part tiles are outside it)

@@ -134,7 +134,7 @@ def test_c3_flagship_lce_q4(monkeypatch):
     # the default backward: each vocab chunk of the 4-bit head staged (dequantized, transposed) in
     # the workspace
     monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
-    monkeypatch.delenv("MTP_LCE_Q4_STAGE", raising=False)
+    monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
     L.clear_transposed_head_cache()
     nll, lse, dh, ct = _kernel_lce(h, head, t)
     assert L.transposed_head_cache_bytes() == 0
@@ -144,9 +144,9 @@ def test_c3_flagship_lce_q4(monkeypatch):
     # the other two backwards: the whole head kept as a cached transposed copy, and neither copy nor
     # staging (the packed words dequantized in registers into the dH product's transposed tiles)
     for copy, stage in (("1", "1"), ("0", "0")):
-        print(f"[C3] backward with MTP_LCE_TRANSPOSED_HEAD={copy} MTP_LCE_Q4_STAGE={stage}", flush=True)
+        print(f"[C3] backward with MTP_LCE_TRANSPOSED_HEAD={copy} MTP_LCE_STAGE_HEAD={stage}", flush=True)
         monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", copy)
-        monkeypatch.setenv("MTP_LCE_Q4_STAGE", stage)
+        monkeypatch.setenv("MTP_LCE_STAGE_HEAD", stage)
         L.clear_transposed_head_cache()
         _, _, dh2, _ = _kernel_lce(h, head, t)
         assert (dh2[t == IGN] == 0).all()

@@ -337,7 +337,7 @@ def test_backward_row_blocks_match_all_rows(n, d, v, row_block, head):
 def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1, chunk=None, staged=False):
     """Forward then backward through the C-ABI (whole vocab in one chunk unless `chunk`, all rows in
     one block); with_wt passes the transposed (4-bit: dequantized) head made by
-    mtp_lce_head_transpose; `staged` runs the 4-bit head's backward as MTP_HEAD_Q4_STAGED."""
+    mtp_lce_head_transpose; `staged` runs the backward as MTP_HEAD_Q4_STAGED / MTP_HEAD_DENSE_STAGED."""
     from mlx_train_perf import _native
 
     lib = _native.load()
@@ -363,7 +363,7 @@ def _capi_backward(h, w, t, ct, *, head, with_wt, reps=1, chunk=None, staged=Fal
     _native.check(lib.mtp_lce_fwd(hd.data_ptr(), *ptrs, td.data_ptr(), n, d, v, kind, IGN, nll.data_ptr(),
                                   lse.data_ptr(), tgt.data_ptr(), ws.data_ptr(), fws, stream), domain="loss")
     chunk = chunk or (v + 255) // 256 * 256
-    bkind = _native.HEAD_Q4_STAGED if staged else kind
+    bkind = kind if not staged else (_native.HEAD_Q4_STAGED if head == "q4" else _native.HEAD_DENSE_STAGED)
     bws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, bkind, chunk, 0)
     bw = torch.empty(bws, dtype=torch.uint8, device="cuda")
     ctd = ct.cuda()
@@ -408,19 +408,24 @@ def test_backward_split_contraction(n, d, v, head, with_wt):
     assert (outs[0][t == IGN] == 0).all()
 
 
-# (n, d, v, chunk): one chunk and several (the last one partial), a split dH contraction (n = 1000,
-# d = 2048), a tiny grid and a 256-column chunk.
-@pytest.mark.parametrize(("n", "d", "v", "chunk"), [(1000, 512, 6000, 2048), (1000, 2048, 8000, 8192),
-                                                    (300, 256, 3000, 256), (2048, 1024, 20000, 4096)])
-def test_q4_staged_backward_equals_cached_head(n, d, v, chunk):
-    """MTP_HEAD_Q4_STAGED: each vocab chunk of the 4-bit head dequantized and transposed into the
-    workspace, then read as the cached transposed head is. dH equals the cached-head backward's at the
-    same chunk bitwise, repeats bitwise, and matches the oracle."""
-    print(f"[lce q4 staged] n={n} d={d} v={v} chunk={chunk}", flush=True)
-    h, w, t = lce_inputs(n, d, v, seed=n + 3 * d + v, w_std=0.05)
+# (n, d, v, chunk, head): one chunk and several (the last one partial), a split dH contraction
+# (n = 1000, d = 2048), a tiny grid and a 256-column chunk; 4-bit and dense heads.
+@pytest.mark.parametrize(("n", "d", "v", "chunk", "head"), [(1000, 512, 6000, 2048, "q4"),
+                                                            (1000, 2048, 8000, 8192, "q4"),
+                                                            (300, 256, 3000, 256, "q4"),
+                                                            (2048, 1024, 20000, 4096, "q4"),
+                                                            (1000, 512, 6000, 2048, "dense"),
+                                                            (1000, 2048, 8000, 8192, "dense"),
+                                                            (2048, 1024, 20000, 4096, "dense")])
+def test_staged_backward_equals_cached_head(n, d, v, chunk, head):
+    """MTP_HEAD_Q4_STAGED / MTP_HEAD_DENSE_STAGED: each vocab chunk of the head transposed (4-bit:
+    dequantized) into the workspace, then read as the cached transposed head is. dH equals the
+    cached-head backward's at the same chunk bitwise, repeats bitwise, and matches the oracle."""
+    print(f"[lce staged] n={n} d={d} v={v} chunk={chunk} head={head}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=n + 3 * d + v, w_std=0.05 if head == "q4" else 0.02)
     ct = _cotangent(t)
-    cached, wf = _capi_backward(h, w, t, ct, head="q4", with_wt=True, chunk=chunk)
-    staged, _ = _capi_backward(h, w, t, ct, head="q4", with_wt=False, chunk=chunk, staged=True, reps=2)
+    cached, wf = _capi_backward(h, w, t, ct, head=head, with_wt=True, chunk=chunk)
+    staged, _ = _capi_backward(h, w, t, ct, head=head, with_wt=False, chunk=chunk, staged=True, reps=2)
     assert torch.equal(staged[0], staged[1])
     assert torch.equal(staged[0], cached[0])
     _, olse, _ = olce.forward(h, wf, t, ignore_index=IGN)

@@ -71,7 +71,7 @@ def test_planner_matches_measured_loss_peaks(trainable, monkeypatch):
     L.clear_transposed_head_cache()
 
 
-def test_planner_matches_measured_q4_staged_peaks(monkeypatch):
+def test_planner_matches_measured_staged_q4_peaks(monkeypatch):
     """A 4-bit head (C3) with the default staged backward: no cached copy; the backward's peak is the
     planned workspace (gradient tiles, fp32 dH accumulator, one staged head chunk) and dH."""
     from mlx_train_perf.core import loss as L
@@ -80,7 +80,7 @@ def test_planner_matches_measured_q4_staged_peaks(monkeypatch):
 
     print("[planner vs measured peaks, C3 staged]", flush=True)
     monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
-    monkeypatch.delenv("MTP_LCE_Q4_STAGE", raising=False)
+    monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
     monkeypatch.delenv("MTP_LCE_BWD_BUDGET", raising=False)
     h, w, t = _inputs()
     wq, sc, bi = (x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))

@@ -217,14 +217,25 @@ def test_memory_planner_head_terms():
     assert frozen.head_grad == 0 and frozen.peak == frozen.transposed_head + frozen.backward_workspace
     # frozen flagship: two 4096-row blocks of one vocab chunk (1.25 GB of gradient tiles)
     assert frozen.backward_workspace == 4096 * (152064 + 64) * 2 + n * 4
+    # a trainable head without the copy: every row in one block, each vocab chunk of the head staged
+    # in the workspace (3 chunks of 59904 columns within the 1.5 GiB budget)
     tr = est.loss_bytes(n=n, d=d, v=v, trainable=True, transposed_head=False)
-    p = plan.lce_plan(n=n, v=v, d=d, trainable=True)
-    assert p.bwd_row_block == n and p.bwd_chunks == 2
+    p = plan.lce_plan(n=n, v=v, d=d, trainable=True, staged=True)
+    assert p.bwd_row_block == n and p.bwd_chunk == 59904 and p.bwd_chunks == 3
     assert tr.head_grad == v * d * 2 and tr.backward_workspace == p.bwd_workspace_bytes + n * 4
+    # and with it (two chunks of gradient tiles, no staging buffer)
+    trc = est.loss_bytes(n=n, d=d, v=v, trainable=True, transposed_head=True)
+    pc = plan.lce_plan(n=n, v=v, d=d, trainable=True)
+    assert pc.bwd_row_block == n and pc.bwd_chunks == 2
+    assert trc.backward_workspace == pc.bwd_workspace_bytes + n * 4
     assert tr.backward_peak == tr.backward_workspace + tr.head_grad > 2.8e9
     step = dict(n_layers=32, batch=1, seq_len=8192, hidden=d, vocab=v, heads=32, kv_heads=8, head_dim=128)
     full = est.estimate_peak(**step, trainable_head=True).components["loss"]
     lora = est.estimate_peak(**step).components["loss"]
-    assert full - lora > v * d * 2
+    # by default a frozen dense head keeps the transposed copy and a trainable one stages its chunks
+    full_lb, lora_lb = est.loss_bytes(n=n, d=d, v=v, trainable=True), est.loss_bytes(n=n, d=d, v=v)
+    assert full == full_lb.peak and lora == lora_lb.peak
+    assert full_lb.head_grad == v * d * 2 and full_lb.transposed_head == 0 < lora_lb.transposed_head
+    assert full_lb.backward_peak > lora_lb.backward_peak + v * d * 2
     # the chunked and naive impls carry the dL/dW term too
     assert est.loss_bytes(n=n, d=d, v=v, impl="chunked", trainable=True).head_grad == v * d * 2
