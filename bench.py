@@ -242,7 +242,7 @@ def bench_lce(steps, warmup, head_kind="dense"):
     copy = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
     staged = ((copy == "0" or (head_kind == "q4" and copy != "1"))
               and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
-    p = plan.lce_plan(n=N, v=V, d=D, staged=staged)
+    p = plan.lce_plan(n=N, v=V, d=D, staged=staged, quantized=head_kind == "q4")
     head_t = L.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,
             "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),

@@ -114,14 +114,17 @@ int64_t mtp_lce_bwd_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
  * an fp32 [row_block][d] dH accumulator when more than one chunk is needed, and, when a block's dH
  * product splits its vocab contraction to fill the GPU, its fp32 part tiles
  * [parts][tiles][256][256] (the most any row block and chunk of the plan takes); for
- * the staged head kinds then the staging buffer bf16 [d][mtp_lce_head_t_ld(chunk)]. */
+ * the staged head kinds then the staging buffer bf16 [d][mtp_lce_head_t_ld(chunk)], followed for
+ * MTP_HEAD_Q4_STAGED by the chunk's dequantized rows bf16 [chunk][d]. */
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block);
 
-/* Vocab columns per chunk (a multiple of 256) of a staged-head backward over all n rows for
- * a workspace budget in bytes: the gradient tiles (2 n bytes per column), the staged head chunk
- * (2 d bytes per column) and, with more than one chunk, the fp32 dH accumulator fit the budget. */
-int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
+/* Vocab columns per chunk (a multiple of 256) of a staged-head backward (head_kind
+ * MTP_HEAD_Q4_STAGED or MTP_HEAD_DENSE_STAGED, else 0) over all n rows for a workspace budget in
+ * bytes: the gradient tiles (2 n bytes per column), the staged head chunk (2 d bytes per column, 4 d
+ * for a 4-bit head, whose dequantized rows are staged as well) and, with more than one chunk, the
+ * fp32 dH accumulator fit the budget. */
+int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, int32_t head_kind, size_t budget_bytes);
 
 /* Row pitch (elements) of the transposed dense head used by mtp_lce_bwd: round_up(v, 256) + 64. */
 int64_t mtp_lce_head_t_ld(int64_t v);

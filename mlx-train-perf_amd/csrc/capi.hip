@@ -252,11 +252,16 @@ static size_t lce_bwd_parts_offset(int64_t d, int64_t v, int64_t chunk, int64_t 
 static bool staged_kind(int32_t head_kind) { return head_kind == MTP_HEAD_Q4_STAGED || head_kind == MTP_HEAD_DENSE_STAGED; }
 
 // The staging buffer of the MTP_HEAD_*_STAGED kinds: one chunk of the head, transposed (a 4-bit head
-// dequantized), [d][lce_head_t_ld(chunk)] bf16, after the part tiles (256-byte aligned).
+// dequantized), [d][lce_head_t_ld(chunk)] bf16, after the part tiles (256-byte aligned); for a 4-bit
+// head the chunk's dequantized rows [chunk][d] bf16 follow (mtp::lce_stage_rows_offset).
 static size_t lce_bwd_stage_offset(int64_t n, int64_t d, int64_t v, int64_t chunk, int64_t row_block) {
   return (lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block) + 255) / 256 * 256;
 }
-static size_t lce_bwd_stage_bytes(int64_t d, int64_t chunk) { return (size_t)d * (size_t)mtp::lce_head_t_ld((long)chunk) * 2; }
+static bool stage_rows(int32_t head_kind) { return head_kind == MTP_HEAD_Q4_STAGED && mtp::kQ4StageRows; }
+static size_t lce_bwd_stage_bytes(int64_t d, int64_t chunk, int32_t head_kind) {
+  if (stage_rows(head_kind)) return ((size_t)mtp::lce_stage_rows_offset((long)d, (long)chunk) + (size_t)chunk * (size_t)d) * 2;
+  return (size_t)d * (size_t)mtp::lce_head_t_ld((long)chunk) * 2;
+}
 
 size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind, int64_t chunk,
                                    int64_t row_block) {
@@ -264,17 +269,17 @@ size_t mtp_lce_bwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
   if (chunk > round_up(v, kTile)) chunk = round_up(v, kTile);
   if (row_block < 1 || row_block > n) row_block = n;
   if (staged_kind(head_kind))
-    return lce_bwd_stage_offset(n, d, v, chunk, row_block) + lce_bwd_stage_bytes(d, chunk);
+    return lce_bwd_stage_offset(n, d, v, chunk, row_block) + lce_bwd_stage_bytes(d, chunk, head_kind);
   return lce_bwd_parts_offset(d, v, chunk, row_block) + lce_dh_parts_max(n, d, v, chunk, row_block);
 }
 
-int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
-  if (n < 1 || d < 1 || v < 1) return 0;
+int64_t mtp_lce_bwd_stage_chunk(int64_t n, int64_t d, int64_t v, int32_t head_kind, size_t budget_bytes) {
+  if (n < 1 || d < 1 || v < 1 || !staged_kind(head_kind)) return 0;
   const int64_t vpad = round_up(v, kTile);
   // All n rows in one block. Per vocab column the gradient tiles take 2 n bytes and the staged head
-  // chunk 2 d; one chunk if the whole padded vocab fits, otherwise the budget also carries the fp32
-  // dH accumulator.
-  const size_t per_col = (size_t)2 * (size_t)(n + d);
+  // chunk 2 d (4 d with a 4-bit chunk's dequantized rows); one chunk if the whole padded vocab fits,
+  // otherwise the budget also carries the fp32 dH accumulator.
+  const size_t per_col = (size_t)2 * (size_t)(n + d) + (stage_rows(head_kind) ? (size_t)2 * (size_t)d : 0);
   if (per_col * (size_t)(vpad + mtp::kGPitchPad) <= budget_bytes) return vpad;
   const size_t acc = (size_t)n * (size_t)d * 4;
   const size_t rest = budget_bytes > acc ? budget_bytes - acc : 0;

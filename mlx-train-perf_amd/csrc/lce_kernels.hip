@@ -1240,7 +1240,8 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
 
 // ------------------------------------------------------------------------------------------
 // Backward step 1, persistent form (hidden dim a multiple of 64), without the one-hot term and
-// the zero padding columns (see lce_bwd_g_fix_kernel). Workgroup (row tile, vocab
+// the zero padding columns (see lce_bwd_g_fix_kernel). Row r of the dense W holds vocab row
+// wrow0 + r (0 for the whole head, the chunk's first row for dequantized rows staged per chunk). Workgroup (row tile, vocab
 // split) walks its split's vocab tiles of the chunk back to back on the DMA core, in the
 // forward's XCD-grouped order; the next tile's first two stages are issued during the current
 // tile's last k-step. Each lane stores its G values straight from the accumulator layout (8-byte
@@ -1258,7 +1259,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
                               const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
                               const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index,
                               int N, int D, int V, int v_begin, int v_end, int ctiles, int nsplit, int ldg,
-                              bf16_t* __restrict__ G) {
+                              int wrow0, bf16_t* __restrict__ G) {
   __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + kQ4SbBytes : kLdsBytes];
 
   const int g = blockIdx.x;
@@ -1315,7 +1316,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
       oa.init(Wq + (long)v1 * (D >> 3), Sc + (long)v1 * (D >> 6), Bi + (long)v1 * (D >> 6), D, vlim - v1,
               lds + kLdsBytes);
     } else {
-      oa.init(W + (long)v1 * D, D, vlim - v1);
+      oa.init(W + (long)(v1 - wrow0) * D, D, vlim - v1);
     }
   };
   init_a(v_begin + vt_begin * kTile);
@@ -1345,7 +1346,7 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
           oa.issue_at(tile_bytes, 1, lds + kDmaStage);
         } else {
           DmaRowOp na;
-          na.init(W + (long)(v0 + kTile) * D, D, vlim - v0 - kTile);
+          na.init(W + (long)(v0 + kTile - wrow0) * D, D, vlim - v0 - kTile);
           na.issue(0, lds);
           na.issue(1, lds + kDmaStage);
         }
@@ -1390,12 +1391,13 @@ void lce_bwd_g_persist_kernel(const bf16_t* __restrict__ H, const bf16_t* __rest
 //  * a row whose target lies in the chunk gets G[t][y_t - v_begin] = bf16((exp(z - lse) - 1) coef),
 //    z = H_t . W_{y_t} as an fp32 dot product (4-bit weights rounded to bf16, as in the product
 //    tiles), overwriting the bf16(exp(z - lse) coef) the persistent kernel stored there.
+// wrow0: the vocab row of the dense W's row 0, as in lce_bwd_g_persist_kernel (0 for a 4-bit head).
 template <int Q4>
 __global__ __launch_bounds__(256) void lce_bwd_g_fix_kernel(
     const bf16_t* __restrict__ H, const bf16_t* __restrict__ W, const uint32_t* __restrict__ Wq,
     const bf16_t* __restrict__ Sc, const bf16_t* __restrict__ Bi, const int64_t* __restrict__ targets,
     const float* __restrict__ lse, const float* __restrict__ dnll, long long ignore_index, int N, int D, int V,
-    int v_begin, int v_end, int kc, int ldg, bf16_t* __restrict__ G) {
+    int v_begin, int v_end, int kc, int ldg, int wrow0, bf16_t* __restrict__ G) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
@@ -1403,7 +1405,7 @@ __global__ __launch_bounds__(256) void lce_bwd_g_fix_kernel(
   for (int c = vlim - v_begin + lane; c < kc; c += 64) G[(long)t * ldg + c] = 0;
   const long long y = targets[t];
   if (y == ignore_index || y < v_begin || y >= vlim) return;
-  const float z = row_dot<Q4, true>(H + (long)t * D, W, Wq, Sc, Bi, y, D, lane);
+  const float z = row_dot<Q4, true>(H + (long)t * D, W, Wq, Sc, Bi, y - wrow0, D, lane);
   if (lane == 0) {
     const float p = fast_exp2(z * kLog2e - lse[t] * kLog2e) - 1.f;
     G[(long)t * ldg + (y - v_begin)] = __builtin_bit_cast(bf16_t, (__bf16)(p * dnll[t]));
@@ -1661,13 +1663,15 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
                                                                  const uint32_t* __restrict__ Wq,
                                                                  const bf16_t* __restrict__ Sc,
                                                                  const bf16_t* __restrict__ Bi, int V, int D,
-                                                                 int ldt, int dspan, bf16_t* __restrict__ Wt) {
+                                                                 int ldt, int dspan, bf16_t* __restrict__ Wt,
+                                                                 bf16_t* __restrict__ rows_out) {
   __shared__ uint16_t tile[64][64 + 2];
   // Workgroup (x, y) transposes vocab rows [64 x, 64 x + 64) over hidden dims [dspan y, dspan (y + 1)),
   // 64 x 64 tiles in turn. A 4-bit head takes the whole hidden dim per workgroup (dspan = D): its rows'
   // memory lines (packed words, and scales and biases, 2 bytes of a line per 64 dims) are then read
   // by one workgroup and stay in its L2 between tiles, instead of being fetched once per tile by
   // workgroups on other XCDs. A dense head takes one tile per workgroup (dspan = 64).
+  // rows_out (optional, 4-bit head): the dequantized rows as well, bf16 [V][D], row-major.
   const int v0 = blockIdx.x * 64;
   const int t = threadIdx.x;
   const int dend = (blockIdx.y + 1) * dspan < D ? (blockIdx.y + 1) * dspan : D;
@@ -1682,6 +1686,7 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
         if constexpr (Q4) {
           const long g = (long)v * (D >> 6) + (d >> 6);
           x = dequant8(Wq[(long)v * (D >> 3) + (d >> 3)], bf16_to_f32(Sc[g]), bf16_to_f32(Bi[g]));
+          if (rows_out != nullptr) *reinterpret_cast<u32x4*>(rows_out + (long)v * D + d) = x;
         } else {
           x = *reinterpret_cast<const u32x4*>(W + (long)v * D + d);
         }
@@ -1712,12 +1717,17 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
 
 long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad; }
 
-hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream) {
+hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
+                                     bf16_t* rows_out) {
   const int ldt = (int)lce_head_t_ld(V);
   const int dspan = h.q4 ? D : 64;
   dim3 grid(ldt / 64, (D + dspan - 1) / dspan), block(256);
-  if (h.q4) hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan, Wt);
-  else hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan, Wt);
+  if (h.q4)
+    hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan,
+                       Wt, rows_out);
+  else
+    hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan,
+                       Wt, nullptr);
   return hipGetLastError();
 }
 
@@ -1840,26 +1850,55 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
     const int vb = c * chunk;
     const int ve = (vb + chunk < V) ? vb + chunk : V;
     const int ctiles = (ve - vb + kTile - 1) / kTile;
+    // A head without the cached transposed copy but with a staging buffer: the chunk's rows of the
+    // head, transposed (a 4-bit head dequantized) into the buffer, then read by the dH product like
+    // the cached copy. A 4-bit chunk's dequantized rows go to the buffer too (kQ4StageRows), and its
+    // gradient tiles are then a dense product over them (row 0 = vocab row vb).
+    const bf16_t* wt = h.wt;
+    int ldw = ldt, tcol0 = vb;
+    const bf16_t* gw = h.w;
+    int gq4 = h.q4, wrow0 = 0;
+    if (wt == nullptr && stage != nullptr && D % kBK == 0) {
+      LceHead hc = h;
+      if (h.q4) {
+        hc.wq = h.wq + (long)vb * (D >> 3);
+        hc.sc = h.sc + (long)vb * (D >> 6);
+        hc.bi = h.bi + (long)vb * (D >> 6);
+      } else {
+        hc.w = h.w + (long)vb * D;
+      }
+      bf16_t* rows = h.q4 && kQ4StageRows ? stage + lce_stage_rows_offset(D, chunk) : nullptr;
+      hipError_t se = launch_lce_head_transpose(hc, ve - vb, D, stage, stream, rows);
+      if (se != hipSuccess) return se;
+      wt = stage;
+      ldw = (int)lce_head_t_ld(ve - vb);
+      tcol0 = 0;
+      if (rows != nullptr) {
+        gw = rows;
+        gq4 = 0;
+        wrow0 = vb;
+      }
+    }
     if (D % kBK == 0) {
       // One resident workgroup per CU (the stages take 128 KiB of LDS, 144 KiB for the 4-bit head).
       const int ns = lce_nsplit(N, (long)ctiles * kTile, 1);
       dim3 pgrid(rtiles * ns);
-      if (h.q4) {
+      if (gq4) {
         hipLaunchKernelGGL(lce_bwd_g_persist_kernel<1>, pgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
-                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, Gbuf);
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, 0, Gbuf);
       } else {
-        hipLaunchKernelGGL(lce_bwd_g_persist_kernel<0>, pgrid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
-                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, Gbuf);
+        hipLaunchKernelGGL(lce_bwd_g_persist_kernel<0>, pgrid, block, 0, stream, H, gw, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles, ns, ldg, wrow0, Gbuf);
       }
       hipError_t pe = hipGetLastError();
       if (pe != hipSuccess) return pe;
       dim3 tgrid((N + 3) / 4), tblock(256);
-      if (h.q4) {
+      if (gq4) {
         hipLaunchKernelGGL(lce_bwd_g_fix_kernel<1>, tgrid, tblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
-                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, Gbuf);
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, 0, Gbuf);
       } else {
-        hipLaunchKernelGGL(lce_bwd_g_fix_kernel<0>, tgrid, tblock, 0, stream, H, h.w, h.wq, h.sc, h.bi, targets,
-                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, Gbuf);
+        hipLaunchKernelGGL(lce_bwd_g_fix_kernel<0>, tgrid, tblock, 0, stream, H, gw, h.wq, h.sc, h.bi, targets,
+                           lse, dnll, ignore_index, N, D, V, vb, ve, ctiles * kTile, ldg, wrow0, Gbuf);
       }
     } else {
       dim3 ggrid(8 * rtiles * ((ctiles + 7) / 8));
@@ -1873,25 +1912,6 @@ static hipError_t lce_bwd_rows(const LceHead& h, const bf16_t* H, const int64_t*
     else if (c == 0) mode = 0;
     else if (c == nchunks - 1) mode = 2;
     else mode = 1;
-    // A head without the cached transposed copy but with a staging buffer: the chunk's rows of the
-    // head, transposed (a 4-bit head dequantized) into the buffer, then read like the cached copy.
-    const bf16_t* wt = h.wt;
-    int ldw = ldt, tcol0 = vb;
-    if (wt == nullptr && stage != nullptr && D % kBK == 0) {
-      LceHead hc = h;
-      if (h.q4) {
-        hc.wq = h.wq + (long)vb * (D >> 3);
-        hc.sc = h.sc + (long)vb * (D >> 6);
-        hc.bi = h.bi + (long)vb * (D >> 6);
-      } else {
-        hc.w = h.w + (long)vb * D;
-      }
-      e = launch_lce_head_transpose(hc, ve - vb, D, stage, stream);
-      if (e != hipSuccess) return e;
-      wt = stage;
-      ldw = (int)lce_head_t_ld(ve - vb);
-      tcol0 = 0;
-    }
     const int ks = lce_dh_ksplit(N, D, ctiles);
     const int sa = ks > 1 ? lce_dh_split_a(rtiles, dtiles) : 0;
     dim3 hgrid(8 * rtiles * ((dtiles + 7) / 8));

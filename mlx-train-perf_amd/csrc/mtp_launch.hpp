@@ -27,12 +27,22 @@ struct LceHead {
 
 int lce_fwd_nsplit(long N, long V);
 long lce_head_t_ld(long V);
+
+// A staged 4-bit chunk (backward without the cached transposed copy) also holds its dequantized rows
+// [chunk][D] bf16, after the transposed chunk [D][lce_head_t_ld(chunk)] (element offset below), so the
+// chunk's gradient tiles are a dense product.
+#ifndef MTP_Q4_STAGE_ROWS
+#define MTP_Q4_STAGE_ROWS 1
+#endif
+constexpr bool kQ4StageRows = MTP_Q4_STAGE_ROWS != 0;
+inline long lce_stage_rows_offset(long D, long chunk) { return (D * lce_head_t_ld(chunk) + 127) / 128 * 128; }
 // Parts of the backward's dH contraction over `ktiles` 256-wide vocab tiles for a block of `rows`
 // rows (1 = one workgroup per output tile), and the fp32 part tiles that takes (0 when 1).
 int lce_dh_ksplit(long rows, long D, long ktiles);
 size_t lce_dh_parts_bytes(long rows, long D, long ktiles);
 
-hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream);
+hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
+                                     bf16_t* rows_out = nullptr);
 
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,

@@ -63,7 +63,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_lce_fwd_noalloc_max_workspace_bytes": (_size, []),
     "mtp_lce_bwd_row_block": (_i64, [_i64, _i64, _i64, _size]),
     "mtp_lce_bwd_chunk": (_i64, [_i64, _i64, _i64, _size]),
-    "mtp_lce_bwd_stage_chunk": (_i64, [_i64, _i64, _i64, _size]),
+    "mtp_lce_bwd_stage_chunk": (_i64, [_i64, _i64, _i64, _i32, _size]),
     "mtp_lce_bwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32, _i64, _i64]),
     "mtp_lce_head_t_ld": (_i64, [_i64]),
     "mtp_lce_head_transpose": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _i64, _i64, _i32,

@@ -359,7 +359,7 @@ class _KernelLCE(torch.autograd.Function):
         if ctx.bwd_chunk:   # an explicit vocab chunk: all rows in one block
             chunk, rows = min(max(256, (ctx.bwd_chunk + 255) // 256 * 256), vpad), n
         elif staged:   # every row block would stage every chunk again
-            chunk, rows = lib.mtp_lce_bwd_stage_chunk(n, d, v, _plan.lce_bwd_budget_bytes()), n
+            chunk, rows = lib.mtp_lce_bwd_stage_chunk(n, d, v, head_kind, _plan.lce_bwd_budget_bytes()), n
         else:
             # Row blocks reuse one gradient buffer (a trainable head's dL/dW needs every row at once).
             budget = _plan.lce_bwd_budget_bytes()

@@ -86,10 +86,10 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
         staged = head_t == 0 and d % 64 == 0 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
         fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)
         if chunk:
-            bwd = _launch.lce_bwd_workspace_bytes(n, d, v, chunk, staged=staged) + n * 4
+            bwd = _launch.lce_bwd_workspace_bytes(n, d, v, chunk, staged=staged, quantized=quantized) + n * 4
         else:
             p = _launch.lce_plan(n=n, v=v, d=d, budget=bwd_budget or _launch.lce_bwd_budget_bytes(),
-                                 trainable=trainable, staged=staged)
+                                 trainable=trainable, staged=staged, quantized=quantized)
             bwd = p.bwd_workspace_bytes + n * 4
         return LossBytes(forward_peak=fwd, backward_workspace=bwd, head_grad=head_grad, transposed_head=head_t)
     elif impl == "chunked":

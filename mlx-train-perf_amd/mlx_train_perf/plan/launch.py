@@ -134,11 +134,12 @@ def lce_bwd_chunk(n: int, d: int, v: int, budget: int) -> int:
 
 
 def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int | None = None, *,
-                            staged: bool = False) -> int:
+                            staged: bool = False, quantized: bool = False) -> int:
     """bf16 gradient tiles [row_block][chunk + G_PITCH_PAD], the fp32 dH accumulator when >1 chunk,
     and the fp32 part tiles of a split dH product (the most any row block and chunk takes); `staged`
     (the MTP_HEAD_*_STAGED backwards): then, 256-byte aligned, the staging buffer of one transposed
-    (4-bit: dequantized) head chunk, bf16 [d][lce_head_t_ld(chunk)]."""
+    (4-bit: dequantized) head chunk, bf16 [d][lce_head_t_ld(chunk)], and for a 4-bit head
+    (`quantized`) the chunk's dequantized rows bf16 [chunk][d] after it."""
     chunk = min(chunk, -(-v // TILE) * TILE)
     rows = n if not row_block or row_block < 1 or row_block > n else row_block
     nchunks = -(-v // chunk)
@@ -147,7 +148,10 @@ def lce_bwd_workspace_bytes(n: int, d: int, v: int, chunk: int, row_block: int |
     parts = max(lce_dh_parts_bytes(r, d, kt) for r in (rows, last_rows) for kt in (chunk // TILE, last_tiles))
     total = rows * (chunk + G_PITCH_PAD) * 2 + (rows * d * 4 if nchunks > 1 else 0) + parts
     if staged:
-        total = -(-total // 256) * 256 + d * lce_head_t_ld(chunk) * 2
+        stage = d * lce_head_t_ld(chunk)
+        if quantized:
+            stage = -(-stage // 128) * 128 + chunk * d
+        total = -(-total // 256) * 256 + stage * 2
     return total
 
 
@@ -156,12 +160,13 @@ def lce_head_t_ld(v: int) -> int:
     return -(-v // TILE) * TILE + G_PITCH_PAD
 
 
-def lce_stage_chunk(n: int, d: int, v: int, budget: int) -> int:
+def lce_stage_chunk(n: int, d: int, v: int, budget: int, *, quantized: bool = False) -> int:
     """Vocab columns per chunk (multiple of 256) of the staged backward over all n rows: per
-    column 2 n bytes of gradient tiles and 2 d of the staged head chunk, plus the fp32 dH accumulator
-    when the vocab takes more than one chunk, within the budget."""
+    column 2 n bytes of gradient tiles and 2 d of the staged head chunk (4 d for a 4-bit head, whose
+    dequantized rows are staged too), plus the fp32 dH accumulator when the vocab takes more than
+    one chunk, within the budget."""
     vpad = -(-v // TILE) * TILE
-    per_col = 2 * (n + d)
+    per_col = 2 * (n + d) + (2 * d if quantized else 0)
     if per_col * (vpad + G_PITCH_PAD) <= budget:
         return vpad
     rest = max(budget - n * d * 4, 0)
@@ -181,20 +186,22 @@ class LcePlan:
 
 
 def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None, trainable: bool = False,
-             staged: bool = False) -> LcePlan:
+             staged: bool = False, quantized: bool = False) -> LcePlan:
     """Forward splits and backward geometry. A trainable head's dL/dW sums over every row, so its
     backward takes all rows in one block (the vocab is chunked instead when they do not fit); so
     does the staged backward (`staged`: a head without the cached transposed copy whose chunks are
-    transposed into the workspace), whose chunks also carry the staged head chunk."""
+    transposed into the workspace), whose chunks also carry the staged head chunk (and, for a 4-bit
+    head, `quantized`, its dequantized rows)."""
     b = lce_bwd_budget_bytes() if budget is None else budget
     if staged:
-        rows, chunk = n, lce_stage_chunk(n, d, v, b)
+        rows, chunk = n, lce_stage_chunk(n, d, v, b, quantized=quantized)
     else:
         rows = n if trainable else lce_bwd_row_block(n, d, v, b)
         chunk = -(-v // TILE) * TILE if rows < n else lce_bwd_chunk(n, d, v, b)
     return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=lce_fwd_workspace_bytes(n, v),
                    bwd_row_block=rows, bwd_row_blocks=-(-n // rows), bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
-                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows, staged=staged))
+                   bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows, staged=staged,
+                                                               quantized=staged and quantized))
 
 
 def attn_heads_per_workgroup(hq: int, hkv: int) -> int:

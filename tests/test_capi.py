@@ -24,26 +24,34 @@ def _declared_symbols() -> set[str]:
     return names
 
 
+@pytest.mark.parametrize("kind", ["q4", "dense"])
 @pytest.mark.parametrize("budget", [3 << 29, 3 << 28, 1 << 28, 1 << 30, 1 << 20])
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027),
                                            (2048, 4096, 151936), (1000, 2048, 8000), (16384, 8192, 262144)])
-def test_staged_plan_agrees_with_python_planner(n, d, v, budget):
-    """The staged 4-bit backward's chunk and workspace (gradient tiles, accumulator, part tiles, then
-    the staging buffer) agree between the library and plan/launch.py, and fit the budget's terms."""
+def test_staged_plan_agrees_with_python_planner(n, d, v, budget, kind):
+    """The staged backward's chunk and workspace (gradient tiles, accumulator, part tiles, then the
+    staging buffer: the transposed chunk, and for a 4-bit head its dequantized rows) agree between
+    the library and plan/launch.py, and fit the budget's terms."""
     from mlx_train_perf import _native as N
 
+    q4 = kind == "q4"
+    hk = N.HEAD_Q4_STAGED if q4 else N.HEAD_DENSE_STAGED
     lib = _native.load()
-    c = lib.mtp_lce_bwd_stage_chunk(n, d, v, budget)
-    assert c == plan.lce_stage_chunk(n, d, v, budget)
+    assert lib.mtp_lce_bwd_stage_chunk(n, d, v, N.HEAD_Q4, budget) == 0   # not a staged kind
+    c = lib.mtp_lce_bwd_stage_chunk(n, d, v, hk, budget)
+    assert c == plan.lce_stage_chunk(n, d, v, budget, quantized=q4)
     assert c % 256 == 0 and 256 <= c <= (v + 255) // 256 * 256
-    ws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4_STAGED, c, n)
-    assert ws == plan.lce_bwd_workspace_bytes(n, d, v, c, n, staged=True)
-    assert ws == lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_DENSE_STAGED, c, n)
+    ws = lib.mtp_lce_bwd_workspace_bytes(n, d, v, hk, c, n)
+    assert ws == plan.lce_bwd_workspace_bytes(n, d, v, c, n, staged=True, quantized=q4)
     plain = lib.mtp_lce_bwd_workspace_bytes(n, d, v, N.HEAD_Q4, c, n)
-    assert ws == -(-plain // 256) * 256 + d * lib.mtp_lce_head_t_ld(c) * 2
+    stage = d * lib.mtp_lce_head_t_ld(c) * 2
+    if q4:   # the rows follow the transposed chunk at a 256-byte boundary
+        stage = -(-stage // 256) * 256 + c * d * 2
+    assert ws == -(-plain // 256) * 256 + stage
     if c > 256:   # a chunk above the minimum fits the budget (the part tiles are outside it)
         nchunks = -(-v // c)
-        assert 2 * (n + d) * (c + 64) + (n * d * 4 if nchunks > 1 else 0) <= budget
+        per_col = 2 * (n + d) + (2 * d if q4 else 0)
+        assert per_col * (c + 64) + (n * d * 4 if nchunks > 1 else 0) <= budget
 
 
 def test_library_exports_every_declared_symbol():
