@@ -170,6 +170,7 @@ def _fwd_launcher(h, head, t, head_kind):
     import torch
 
     from mlx_train_perf import _native
+    from mlx_train_perf.plan import launch as plan
 
     lib = _native.load()
     n_, d_ = h.shape
@@ -177,6 +178,10 @@ def _fwd_launcher(h, head, t, head_kind):
     outs = [torch.empty(n_, dtype=torch.float32, device="cuda") for _ in range(3)]
     kind = _native.HEAD_DENSE if head_kind == "dense" else _native.HEAD_Q4
     ws_b = lib.mtp_lce_fwd_workspace_bytes(n_, d_, v_, kind)
+    if kind == _native.HEAD_Q4 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0":
+        # the loss layer's default 4-bit forward: vocab splits dequantized into the workspace
+        kind = _native.HEAD_Q4_STAGED
+        ws_b = lib.mtp_lce_fwd_stage_workspace_bytes(n_, d_, v_, plan.lce_bwd_budget_bytes())
     ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
     args = ((head.weight.data_ptr(), None, None, None) if head_kind == "dense" else
             (None, head.w_q.data_ptr(), head.scales.data_ptr(), head.biases.data_ptr()))
@@ -242,12 +247,14 @@ def bench_lce(steps, warmup, head_kind="dense"):
     copy = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
     staged = ((copy == "0" or (head_kind == "q4" and copy != "1"))
               and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
-    p = plan.lce_plan(n=N, v=V, d=D, staged=staged, quantized=head_kind == "q4")
+    fwd_staged = head_kind == "q4" and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+    p = plan.lce_plan(n=N, v=V, d=D, staged=staged, quantized=head_kind == "q4", fwd_staged=fwd_staged)
     head_t = L.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,
             "fwd_kernel_ms_median": statistics.median(fwd_ms), "fwd_kernel_ms_mean": sum(fwd_ms) / len(fwd_ms),
             "fwd_kernel_launches": len(fwd_ms),
             "fwd_marginal_peak_gb": fwd_peak / 1e9, "bwd_marginal_peak_gb": bwd_peak / 1e9,
+            "fwd_workspace_gb": p.fwd_workspace_bytes / 1e9,
             "bwd_workspace_gb": p.bwd_workspace_bytes / 1e9, "bwd_row_block": p.bwd_row_block,
             "bwd_row_blocks": p.bwd_row_blocks, "bwd_chunk": p.bwd_chunk, "bwd_chunks": p.bwd_chunks,
             "transposed_head_cache_gb": head_t / 1e9,

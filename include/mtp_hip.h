@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MTP_ABI_VERSION 4
+#define MTP_ABI_VERSION 5
 
 /* Error codes; the Python layer maps them onto the reference's typed exceptions
  * (src/mlx_train_perf/errors.py:1-76). */
@@ -42,12 +42,13 @@ extern "C" {
 /* Head kinds (reference: src/mlx_train_perf/core/loss.py:30-47, DenseHead / QuantizedHead). */
 #define MTP_HEAD_DENSE 0 /* w: bf16 [V][D]                                                        */
 #define MTP_HEAD_Q4 1    /* w_q: u32 [V][D/8] (8 nibbles, low first); scales, biases: bf16 [V][D/64] */
-/* The 4-bit head of MTP_HEAD_Q4 whose backward (mtp_lce_bwd, with w_t null) dequantizes each vocab
- * chunk of the head into a transposed bf16 staging buffer at the end of its workspace and reads it
- * as it reads a cached transposed head: the reference's chunk-sized dequantization in its QLoRA vjp
- * (core/loss.py:333-343), with no copy of the whole head. mtp_lce_bwd and
- * mtp_lce_bwd_workspace_bytes take it; mtp_lce_fwd and mtp_lce_fwd_noalloc treat it as MTP_HEAD_Q4
- * (and MTP_HEAD_DENSE_STAGED below as MTP_HEAD_DENSE). */
+/* The 4-bit head of MTP_HEAD_Q4 (d a multiple of 64) whose kernels dequantize it chunk-wise into
+ * bf16 staging buffers at the end of their workspaces, with no copy of the whole head: the
+ * reference's chunk-sized dequantization in its QLoRA vjp (core/loss.py:333-343). The backward
+ * (mtp_lce_bwd, w_t null) stages each vocab chunk's rows and the chunk transposed, reading the
+ * latter as it reads a cached transposed head; the forward (mtp_lce_fwd) stages runs of its vocab
+ * splits as rows. Results equal MTP_HEAD_Q4's bit for bit. mtp_lce_fwd_noalloc treats it as
+ * MTP_HEAD_Q4 (and MTP_HEAD_DENSE_STAGED below as MTP_HEAD_DENSE). */
 #define MTP_HEAD_Q4_STAGED 2
 /* The dense head of MTP_HEAD_DENSE (d a multiple of 64) whose backward stages each vocab chunk of
  * the head, transposed, in its workspace in the same way: the alternative to keeping a transposed
@@ -62,8 +63,15 @@ int mtp_abi_version(void);
  * ------------------------------------------------------------------------------------------- */
 
 /* Workspace bytes needed by mtp_lce_fwd (per-token partial maxima and sums per vocab split).
- * Replaces the per-tile lse/tgt chaining buffers of core/kernel/launch.py:75-100. */
+ * Replaces the per-tile lse/tgt chaining buffers of core/kernel/launch.py:75-100.
+ * MTP_HEAD_Q4_STAGED: the least it takes, the partials and then (256-byte aligned) a staging buffer
+ * of the largest vocab split's rows, bf16 [rows][d]; a larger workspace stages runs of splits. */
 size_t mtp_lce_fwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind);
+
+/* Workspace bytes of an MTP_HEAD_Q4_STAGED forward planned for a budget: the partials and a staging
+ * buffer of the largest run of whole vocab splits the forward forms within the budget (all v rows
+ * when they fit, at least one split's); 0 unless d is a multiple of 64. */
+size_t mtp_lce_fwd_stage_workspace_bytes(int64_t n, int64_t d, int64_t v, size_t budget_bytes);
 
 /* Forward. hidden: bf16 [n][d]; targets: int64 [n]; outputs fp32 [n] each:
  *   lse[t] = logsumexp_v(hidden[t] . w[v]), tgt[t] = hidden[t] . w[targets[t]],
@@ -73,7 +81,9 @@ size_t mtp_lce_fwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head
  * kernel does when validate_targets=False (core/kernel/source.py:46,143-144).
  * Replaces: launch.forward (core/kernel/launch.py:75-100) + kernel K1 (core/kernel/source.py:25-190)
  * for head_kind DENSE, and launch.forward_quantized (core/kernel/launch.py:336-373) + kernel K2
- * (core/kernel/source.py:199-340) for head_kind Q4. */
+ * (core/kernel/source.py:199-340) for head_kind Q4. head_kind Q4_STAGED: a 16-byte aligned
+ * workspace of at least mtp_lce_fwd_workspace_bytes; the forward dequantizes as many whole vocab
+ * splits at a time as its staging buffer holds, then runs the dense product over them. */
 int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales,
                 const void* biases, const int64_t* targets, int64_t n, int64_t d, int64_t v,
                 int32_t head_kind, int64_t ignore_index, float* nll, float* lse, float* tgt,
@@ -82,8 +92,8 @@ int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
 /* Forward as mtp_lce_fwd, allocating nothing and taking no workspace: the per-split partials live
  * in a fixed device array inside the library (one per GPU, held until the process ends), whose size
  * mtp_lce_fwd_noalloc_max_workspace_bytes() returns (4 MiB: n up to 524288 tokens at any v). A call
- * whose mtp_lce_fwd_workspace_bytes(n, d, v, head_kind) exceeds it returns MTP_ERR_WORKSPACE before
- * any launch. The array used is that of the device `stream` runs on (the current device for the
+ * whose mtp_lce_fwd_workspace_bytes(n, d, v, head_kind) (that of MTP_HEAD_Q4 for the staged 4-bit
+ * kind, which stages nothing here) exceeds it returns MTP_ERR_WORKSPACE before any launch. The array used is that of the device `stream` runs on (the current device for the
  * null stream), whatever device the calling thread has current; the first call on a device looks
  * up that device's array address (no allocation).
  * Outputs are bitwise those of mtp_lce_fwd. Calls on one GPU share its array: two calls whose work

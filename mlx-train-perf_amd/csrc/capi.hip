@@ -137,11 +137,34 @@ const char* mtp_last_error(void) { return g_err; }
 
 int mtp_abi_version(void) { return MTP_ABI_VERSION; }
 
+// MTP_HEAD_Q4_STAGED forward (d % 64 == 0): the partials, then (256-byte aligned) the staging buffer
+// for runs of vocab splits dequantized to bf16 rows of d.
+static bool fwd_staged(int32_t head_kind, int64_t d) { return head_kind == MTP_HEAD_Q4_STAGED && d % 64 == 0; }
+static size_t lce_fwd_stage_offset(int64_t n, int64_t v) { return (lce_fwd_ws(n, v) + 255) / 256 * 256; }
+
 size_t mtp_lce_fwd_workspace_bytes(int64_t n, int64_t d, int64_t v, int32_t head_kind) {
-  (void)d;
-  (void)head_kind;
-  if (n < 1 || v < 1) return 0;
+  if (n < 1 || v < 1 || d < 1) return 0;
+  if (fwd_staged(head_kind, d))
+    return lce_fwd_stage_offset(n, v) + (size_t)mtp::lce_fwd_stage_rows_max((long)n, (long)v) * (size_t)d * 2;
   return lce_fwd_ws(n, v);
+}
+
+size_t mtp_lce_fwd_stage_workspace_bytes(int64_t n, int64_t d, int64_t v, size_t budget_bytes) {
+  if (n < 1 || v < 1 || d < 1 || d % 64 != 0) return 0;
+  const size_t off = lce_fwd_stage_offset(n, v);
+  long cap = budget_bytes > off ? (long)((budget_bytes - off) / ((size_t)d * 2)) : 0;
+  const long least = mtp::lce_fwd_stage_rows_max((long)n, (long)v);
+  if (cap < least) cap = least;
+  // The largest run of whole splits the launcher forms with `cap` rows.
+  const long ns = mtp::lce_fwd_nsplit((long)n, (long)v);
+  long most = 0;
+  for (long s0 = 0; s0 < ns;) {
+    const long s1 = mtp::lce_fwd_stage_group_end((long)n, (long)v, s0, cap);
+    const long r = mtp::lce_fwd_split_rows((long)n, (long)v, s0, s1);
+    if (r > most) most = r;
+    s0 = s1;
+  }
+  return off + (size_t)most * (size_t)d * 2;
 }
 
 int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,
@@ -150,12 +173,19 @@ int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const vo
   int rc = check_lce_common(hidden, w, w_q, scales, biases, targets, n, d, v, head_kind);
   if (rc) return rc;
   if (!nll || !lse || !tgt) return fail(MTP_ERR_INPUT, "nll, lse, tgt outputs must be non-null");
-  const size_t need = lce_fwd_ws(n, v);
+  const size_t need = mtp_lce_fwd_workspace_bytes(n, d, v, head_kind);
   if (!workspace || workspace_bytes < need)
     return fail(MTP_ERR_WORKSPACE, "lce forward needs a workspace of %zu bytes (got %zu)", need, workspace ? workspace_bytes : (size_t)0);
+  mtp::bf16_t* stage = nullptr;
+  long stage_rows = 0;
+  if (fwd_staged(head_kind, d)) {   // as many vocab rows as the workspace holds past the partials
+    if (!aligned16(workspace)) return fail(MTP_ERR_UNSUPPORTED, "workspace must be 16-byte aligned");
+    stage = reinterpret_cast<mtp::bf16_t*>(static_cast<char*>(workspace) + lce_fwd_stage_offset(n, v));
+    stage_rows = (long)((workspace_bytes - lce_fwd_stage_offset(n, v)) / ((size_t)d * 2));
+  }
   hipError_t e = mtp::launch_lce_fwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
                                      targets, (int)n, (int)d, (int)v, (long long)ignore_index, nll, lse, tgt,
-                                     static_cast<float*>(workspace), static_cast<hipStream_t>(stream));
+                                     static_cast<float*>(workspace), stage, stage_rows, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce forward launch failed: %s", hipGetErrorString(e));
   return ok();
 }
@@ -179,7 +209,7 @@ int mtp_lce_fwd_noalloc(const void* hidden, const void* w, const uint32_t* w_q, 
   // per vocab split and token), so the scratch needs no clearing between calls.
   hipError_t e = mtp::launch_lce_fwd(make_head(w, w_q, scales, biases, head_kind), static_cast<const mtp::bf16_t*>(hidden),
                                      targets, (int)n, (int)d, (int)v, (long long)ignore_index, nll, lse, tgt,
-                                     static_cast<float*>(ws), static_cast<hipStream_t>(stream));
+                                     static_cast<float*>(ws), nullptr, 0, static_cast<hipStream_t>(stream));
   if (e != hipSuccess) return fail(MTP_ERR_RUNTIME, "lce forward launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -851,31 +851,35 @@ __device__ __forceinline__ bool xcd_rect_tile(int mtiles, int ntiles, int& m, in
 // ------------------------------------------------------------------------------------------
 // Forward: per (row tile, vocab split) workgroup, running per-token (max, sum exp2) partials.
 // A operand = head rows (vocab), B operand = hidden rows (tokens): every lane then owns whole
-// token columns, so the vocab reduction is lane-local except for one final exchange.
+// token columns, so the vocab reduction is lane-local except for one final exchange. Row r of the
+// dense W holds vocab row wrow0 + r (0 for the whole head, the chunk's first row for a 4-bit head's
+// rows dequantized into a staging buffer, which give the in-register dequantization's values).
 // ------------------------------------------------------------------------------------------
 template <int Q4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
                     const uint32_t* __restrict__ Wq, const bf16_t* __restrict__ Sc,
-                    const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit,
-                    float* __restrict__ part_m, float* __restrict__ part_s) {
+                    const bf16_t* __restrict__ Bi, int N, int D, int V, int nsplit, int split0, int nlocal,
+                    int wrow0, float* __restrict__ part_m, float* __restrict__ part_s) {
   __shared__ __attribute__((aligned(16))) char lds[Q4 ? kLdsBytes + kQ4SbBytes : kLdsBytes];
   // Workgroup g runs on XCD g % 8. When the row tiles divide into 8 groups, XCD x owns row tiles
   // [x R/8, (x+1) R/8) for every split, walked split-major: the ~32 workgroups resident on one XCD
   // then cover R/8 row tiles x 32/(R/8) splits (4 x 8 at the flagship), whose hidden and head
   // slabs overlap in that XCD's L2 more than 16 row tiles x 2 splits would.
+  // A launch runs splits [split0, split0 + nlocal) of the nsplit (all of them, or one staged chunk's).
   const int g = blockIdx.x;
   const int rtiles = (N + kTile - 1) / kTile;
   int split, rt;
-  if (xcd_rect_tile(rtiles, nsplit, rt, split)) {
-  } else if (rtiles % 8 == 0 && nsplit % 8 == 0) {
+  if (xcd_rect_tile(rtiles, nlocal, rt, split)) {
+  } else if (rtiles % 8 == 0 && nlocal % 8 == 0) {
     const int rpx = rtiles / 8, slot = g >> 3;
     rt = (g & 7) * rpx + slot % rpx;
     split = slot / rpx;
   } else {
-    split = g % nsplit;
-    rt = g / nsplit;
+    split = g % nlocal;
+    rt = g / nlocal;
   }
+  split += split0;
   const int vtiles = (V + kTile - 1) / kTile;
   const int vt_begin = (int)(((long)split * vtiles) / nsplit);
   const int vt_end = (int)(((long)(split + 1) * vtiles) / nsplit);
@@ -955,7 +959,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
     DmaRowOp ob;
     ob.init(H + (long)t0 * D, D, N - t0);
     DmaRowOp oa;
-    oa.init(W + (long)vt_begin * kTile * D, D, V - vt_begin * kTile);
+    oa.init(W + (long)(vt_begin * kTile - wrow0) * D, D, V - vt_begin * kTile);
     const long tile_bytes = 2L * kTile * D;
     bool pre = false;
     for (int vt = vt_begin; vt < vt_end; ++vt) {
@@ -975,7 +979,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
           if (nk > 1) oa.issue2_at(tile_bytes, 1, lds + kDmaStage, wsc);
         } else {
           DmaRowOp na;
-          na.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
+          na.init(W + (long)(v0 + kTile - wrow0) * D, D, V - v0 - kTile);
           na.issue2(0, lds, wsc);
           if (nk > 1) na.issue2(1, lds + kDmaStage, wsc);
         }
@@ -987,7 +991,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       pre = has_next;
       if (has_next) {
         if (next_whole) oa.base += tile_bytes;
-        else oa.init(W + (long)(v0 + kTile) * D, D, V - v0 - kTile);
+        else oa.init(W + (long)(v0 + kTile - wrow0) * D, D, V - v0 - kTile);
       }
       consume(acc, v0);
     }
@@ -1038,7 +1042,7 @@ void lce_fwd_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W,
       const bool full = (v0 + kTile <= V) && (t0 + kTile <= N) && (D % kBK == 0);
       f32x16 acc[4][kNJ];
       RowKLoader la;
-      la.base = W + (long)v0 * D;
+      la.base = W + (long)(v0 - wrow0) * D;
       la.ld = D;
       la.nrows = V - v0;
       la.K = D;
@@ -1717,6 +1721,22 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
 
 long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad; }
 
+// Rows of a 4-bit head dequantized to bf16, row-major [rows][D] (D % 64 == 0): thread q expands the
+// four packed words 4q .. 4q + 3 (32 weights of one row and one 64-wide group) with that group's
+// scale and bias, as the product tiles do. nq = rows D / 32.
+__global__ __launch_bounds__(256) void lce_head_dequant_kernel(const uint32_t* __restrict__ Wq,
+                                                               const bf16_t* __restrict__ Sc,
+                                                               const bf16_t* __restrict__ Bi, long nq,
+                                                               bf16_t* __restrict__ out) {
+  const long q = (long)blockIdx.x * 256 + threadIdx.x;
+  if (q >= nq) return;
+  const u32x4 w = *reinterpret_cast<const u32x4*>(Wq + 4 * q);
+  const float sc = bf16_to_f32(Sc[q >> 1]), bi = bf16_to_f32(Bi[q >> 1]);
+  u32x4* o = reinterpret_cast<u32x4*>(out + 32 * q);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = dequant8(w[e], sc, bi);
+}
+
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
                                      bf16_t* rows_out) {
   const int ldt = (int)lce_head_t_ld(V);
@@ -1809,18 +1829,63 @@ static int lce_dh_split_a(int rtiles, int dtiles) {
 
 int lce_fwd_nsplit(long N, long V) { return lce_nsplit(N, V, kFwdWaves); }
 
+long lce_fwd_split_rows(long N, long V, long split0, long split1) {
+  const long ns = lce_fwd_nsplit(N, V), vtiles = (V + kTile - 1) / kTile;
+  const long r0 = split0 * vtiles / ns * kTile, r1 = split1 * vtiles / ns * kTile;
+  return (r1 < V ? r1 : V) - r0;
+}
+
+long lce_fwd_stage_rows_max(long N, long V) {
+  const long ns = lce_fwd_nsplit(N, V);
+  long most = 0;
+  for (long s = 0; s < ns; ++s) {
+    const long r = lce_fwd_split_rows(N, V, s, s + 1);
+    if (r > most) most = r;
+  }
+  return most;
+}
+
+long lce_fwd_stage_group_end(long N, long V, long split0, long stage_rows) {
+  const long ns = lce_fwd_nsplit(N, V);
+  long e = split0 + 1;
+  while (e < ns && lce_fwd_split_rows(N, V, split0, e + 1) <= stage_rows) ++e;
+  return e;
+}
+
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,
-                          hipStream_t stream) {
+                          bf16_t* stage, long stage_rows, hipStream_t stream) {
   const int ns = lce_fwd_nsplit(N, V);
   float* pm = ws;
   float* ps = ws + (long)ns * N;
   const int rtiles = (N + kTile - 1) / kTile;
-  dim3 grid(rtiles * ns), block(kThreads);
-  if (h.q4) {
-    hipLaunchKernelGGL(lce_fwd_kernel<1>, grid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, N, D, V, ns, pm, ps);
+  dim3 block(kThreads);
+  if (h.q4 && stage != nullptr && D % kBK == 0) {
+    // Runs of whole vocab splits whose rows fit the staging buffer: each run's rows dequantized
+    // into it, then the dense product over them. The splits and their tiles are those of the
+    // single launch below, so the partials are too.
+    for (int s0 = 0; s0 < ns;) {
+      const int s1 = (int)lce_fwd_stage_group_end(N, V, s0, stage_rows);
+      const int vtiles = (V + kTile - 1) / kTile;
+      const long r0 = (long)s0 * vtiles / ns * kTile;
+      const long rows = lce_fwd_split_rows(N, V, s0, s1);
+      const long nq = rows * D / 32;
+      hipLaunchKernelGGL(lce_head_dequant_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, stream,
+                         h.wq + r0 * (D >> 3), h.sc + r0 * (D >> 6), h.bi + r0 * (D >> 6), nq, stage);
+      hipError_t de = hipGetLastError();
+      if (de != hipSuccess) return de;
+      hipLaunchKernelGGL(lce_fwd_kernel<0>, dim3(rtiles * (s1 - s0)), block, 0, stream, H, stage, h.wq, h.sc, h.bi,
+                         N, D, V, ns, s0, s1 - s0, (int)r0, pm, ps);
+      de = hipGetLastError();
+      if (de != hipSuccess) return de;
+      s0 = s1;
+    }
+  } else if (h.q4) {
+    hipLaunchKernelGGL(lce_fwd_kernel<1>, dim3(rtiles * ns), block, 0, stream, H, h.w, h.wq, h.sc, h.bi, N, D, V, ns,
+                       0, ns, 0, pm, ps);
   } else {
-    hipLaunchKernelGGL(lce_fwd_kernel<0>, grid, block, 0, stream, H, h.w, h.wq, h.sc, h.bi, N, D, V, ns, pm, ps);
+    hipLaunchKernelGGL(lce_fwd_kernel<0>, dim3(rtiles * ns), block, 0, stream, H, h.w, h.wq, h.sc, h.bi, N, D, V, ns,
+                       0, ns, 0, pm, ps);
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

@@ -44,9 +44,18 @@ size_t lce_dh_parts_bytes(long rows, long D, long ktiles);
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
                                      bf16_t* rows_out = nullptr);
 
+// Vocab rows of forward splits [split0, split1) (N rows, V vocab), the most any one split takes, and
+// the end of the run of whole splits from split0 whose rows fit `stage_rows` (at least split0 + 1).
+long lce_fwd_split_rows(long N, long V, long split0, long split1);
+long lce_fwd_stage_rows_max(long N, long V);
+long lce_fwd_stage_group_end(long N, long V, long split0, long stage_rows);
+
+// stage (optional, 4-bit head with D % 64 == 0): a buffer of stage_rows >= lce_fwd_stage_rows_max rows
+// of D bf16 into which runs of vocab splits are dequantized before a dense product over them (the
+// same partials as the in-register dequantization).
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
                           long long ignore_index, float* nll, float* lse, float* tgt, float* ws,
-                          hipStream_t stream);
+                          bf16_t* stage, long stage_rows, hipStream_t stream);
 
 hipError_t launch_lce_bwd(const LceHead& h, const bf16_t* H, const int64_t* targets, const float* lse,
                           const float* dnll, int N, int D, int V, long long ignore_index, int chunk, int row_block,

@@ -31,7 +31,7 @@ from mlx_train_perf.errors import (
 LIB_NAME = "libmtp_hip.so"
 LIB_PATH = Path(os.environ.get("MTP_HIP_LIB", str(Path(__file__).resolve().parent / LIB_NAME)))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 MTP_OK = 0
 MTP_ERR_INPUT = -1
 MTP_ERR_UNSUPPORTED = -2
@@ -40,8 +40,9 @@ MTP_ERR_RUNTIME = -4
 
 HEAD_DENSE = 0
 HEAD_Q4 = 1
-HEAD_Q4_STAGED = 2      # backward kinds that stage each transposed (4-bit: dequantized) vocab chunk
-HEAD_DENSE_STAGED = 3   # of the head in the workspace instead of reading a cached transposed copy
+HEAD_Q4_STAGED = 2      # kinds that stage the head chunk-wise in the workspace: the backward each
+HEAD_DENSE_STAGED = 3   # transposed (4-bit: dequantized) vocab chunk instead of a cached transposed
+                        # copy, the 4-bit forward runs of vocab splits dequantized to rows
 
 _c_void_p = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -54,6 +55,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "mtp_last_error": (ctypes.c_char_p, []),
     "mtp_abi_version": (ctypes.c_int, []),
     "mtp_lce_fwd_workspace_bytes": (_size, [_i64, _i64, _i64, _i32]),
+    "mtp_lce_fwd_stage_workspace_bytes": (_size, [_i64, _i64, _i64, _size]),
     "mtp_lce_fwd": (ctypes.c_int, [_c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p, _c_void_p,
                                    _i64, _i64, _i64, _i32, _i64, _c_void_p, _c_void_p, _c_void_p,
                                    _c_void_p, _size, _c_void_p]),

@@ -303,6 +303,12 @@ def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_ki
         return wt
 
 
+def _stages_forward(head_kind: int, d: int, f32: bool) -> bool:
+    """A bf16 forward over a 4-bit head stages it (MTP_HEAD_Q4_STAGED) unless MTP_LCE_STAGE_HEAD is "0"."""
+    return (head_kind == _native.HEAD_Q4 and not f32 and d % 64 == 0
+            and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
+
+
 class _KernelLCE(torch.autograd.Function):
     """Forward: mtp_lce_fwd -> (nll, lse, tgt). Backward: mtp_lce_bwd from the saved lse only; it also
     returns dL/dW when the dense head is an input that requires grad (trainable head). fp32 hidden
@@ -320,11 +326,17 @@ class _KernelLCE(torch.autograd.Function):
         tgt = torch.empty(n, dtype=torch.float32, device=dev)
         ws_fn = lib.mtp_lce_fwd_f32_workspace_bytes if f32 else lib.mtp_lce_fwd_workspace_bytes
         fwd = lib.mtp_lce_fwd_f32 if f32 else lib.mtp_lce_fwd
-        ws_bytes = ws_fn(n, d, v, head_kind)
+        fwd_kind = head_kind
+        if _stages_forward(head_kind, d, f32):
+            # runs of vocab splits of the 4-bit head dequantized into the workspace, then a dense product
+            fwd_kind = _native.HEAD_Q4_STAGED
+            ws_bytes = lib.mtp_lce_fwd_stage_workspace_bytes(n, d, v, _plan.lce_bwd_budget_bytes())
+        else:
+            ws_bytes = ws_fn(n, d, v, head_kind)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
         with _native.on_device(hidden2):
             rc = fwd(hidden2.data_ptr(), _native.ptr(w), _native.ptr(w_q), _native.ptr(scales), _native.ptr(biases),
-                     targets2.data_ptr(), n, d, v, head_kind, ignore_index, nll.data_ptr(), lse.data_ptr(),
+                     targets2.data_ptr(), n, d, v, fwd_kind, ignore_index, nll.data_ptr(), lse.data_ptr(),
                      tgt.data_ptr(), ws.data_ptr(), ws_bytes, _native.stream_of(hidden2))
         _native.check(rc, domain="loss")
         ctx.save_for_backward(hidden2, targets2, lse)

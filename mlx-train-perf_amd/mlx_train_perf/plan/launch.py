@@ -98,6 +98,32 @@ def lce_fwd_workspace_bytes(n: int, v: int) -> int:
     return 2 * lce_fwd_splits(n, v) * n * 4
 
 
+def lce_fwd_split_rows(n: int, v: int, s0: int, s1: int) -> int:
+    """Vocab rows of forward splits [s0, s1)."""
+    ns, vtiles = lce_fwd_splits(n, v), -(-v // TILE)
+    return min(v, s1 * vtiles // ns * TILE) - s0 * vtiles // ns * TILE
+
+
+def lce_fwd_stage_workspace_bytes(n: int, d: int, v: int, budget: int) -> int:
+    """The staged 4-bit forward's workspace within a budget (mirror of
+    mtp_lce_fwd_stage_workspace_bytes): the partials, 256-byte aligned, then a bf16 staging buffer of
+    the largest run of whole vocab splits whose rows fit the budget's rest (at least one split)."""
+    if d % 64:
+        return 0
+    ns = lce_fwd_splits(n, v)
+    off = -(-lce_fwd_workspace_bytes(n, v) // 256) * 256
+    cap = max((budget - off) // (2 * d) if budget > off else 0,
+              max(lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns)))
+    most, s0 = 0, 0
+    while s0 < ns:
+        s1 = s0 + 1
+        while s1 < ns and lce_fwd_split_rows(n, v, s0, s1 + 1) <= cap:
+            s1 += 1
+        most = max(most, lce_fwd_split_rows(n, v, s0, s1))
+        s0 = s1
+    return off + most * d * 2
+
+
 def lce_bwd_row_block(n: int, d: int, v: int, budget: int) -> int:
     """Rows per backward block (mirror of mtp_lce_bwd_row_block): all n when the whole padded
     vocab's gradient tiles fit the budget; else n split in 2 or 4 blocks (a multiple of 256 rows)
@@ -186,19 +212,21 @@ class LcePlan:
 
 
 def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None, trainable: bool = False,
-             staged: bool = False, quantized: bool = False) -> LcePlan:
+             staged: bool = False, quantized: bool = False, fwd_staged: bool = False) -> LcePlan:
     """Forward splits and backward geometry. A trainable head's dL/dW sums over every row, so its
     backward takes all rows in one block (the vocab is chunked instead when they do not fit); so
     does the staged backward (`staged`: a head without the cached transposed copy whose chunks are
     transposed into the workspace), whose chunks also carry the staged head chunk (and, for a 4-bit
-    head, `quantized`, its dequantized rows)."""
+    head, `quantized`, its dequantized rows). `fwd_staged`: the 4-bit forward that dequantizes runs
+    of its vocab splits into its workspace (within the same budget)."""
     b = lce_bwd_budget_bytes() if budget is None else budget
     if staged:
         rows, chunk = n, lce_stage_chunk(n, d, v, b, quantized=quantized)
     else:
         rows = n if trainable else lce_bwd_row_block(n, d, v, b)
         chunk = -(-v // TILE) * TILE if rows < n else lce_bwd_chunk(n, d, v, b)
-    return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=lce_fwd_workspace_bytes(n, v),
+    fws = lce_fwd_stage_workspace_bytes(n, d, v, b) if fwd_staged else lce_fwd_workspace_bytes(n, v)
+    return LcePlan(fwd_splits=lce_fwd_splits(n, v), fwd_workspace_bytes=fws,
                    bwd_row_block=rows, bwd_row_blocks=-(-n // rows), bwd_chunk=chunk, bwd_chunks=-(-v // chunk),
                    bwd_workspace_bytes=lce_bwd_workspace_bytes(n, d, v, chunk, rows, staged=staged,
                                                                quantized=staged and quantized))

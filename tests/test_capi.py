@@ -54,6 +54,33 @@ def test_staged_plan_agrees_with_python_planner(n, d, v, budget, kind):
         assert per_col * (c + 64) + (n * d * 4 if nchunks > 1 else 0) <= budget
 
 
+@pytest.mark.parametrize("budget", [3 << 29, 1 << 28, 1 << 24, 0, 1 << 40])
+@pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (4096, 4096, 151936), (1000, 512, 20000),
+                                           (513, 192, 7777), (64, 64, 1000), (2048, 1024, 40000), (100, 96, 500)])
+def test_staged_forward_workspace_agrees_with_python_planner(n, d, v, budget):
+    """The staged 4-bit forward's workspace (partials, then the largest run of whole vocab splits
+    whose rows fit the budget) agrees between the library and plan/launch.py; the least it takes is
+    one split's rows, the most the whole head's; d not a multiple of 64 stages nothing."""
+    from mlx_train_perf import _native as N
+
+    lib = _native.load()
+    ws = lib.mtp_lce_fwd_stage_workspace_bytes(n, d, v, budget)
+    if d % 64:
+        assert ws == 0 == plan.lce_fwd_stage_workspace_bytes(n, d, v, budget)
+        return
+    assert ws == plan.lce_fwd_stage_workspace_bytes(n, d, v, budget)
+    off = -(-plan.lce_fwd_workspace_bytes(n, v) // 256) * 256
+    ns = plan.lce_fwd_splits(n, v)
+    one = max(plan.lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns))
+    assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, N.HEAD_Q4_STAGED) == off + one * d * 2
+    assert off + one * d * 2 <= ws <= off + v * d * 2
+    assert sum(plan.lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns)) == v
+    if budget >= off + v * d * 2:
+        assert ws == off + v * d * 2
+    elif ws > off + one * d * 2:
+        assert ws <= budget
+
+
 def test_library_exports_every_declared_symbol():
     lib = _native.load()
     declared = _declared_symbols()
@@ -61,7 +88,7 @@ def test_library_exports_every_declared_symbol():
     for name in declared:
         assert hasattr(lib, name), name
     assert set(_native.SIGNATURES) >= declared - set()  # every export has a Python signature
-    assert lib.mtp_abi_version() == _native.ABI_VERSION == 4
+    assert lib.mtp_abi_version() == _native.ABI_VERSION == 5
 
 
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (1024, 512, 32000), (65, 192, 1027), (1, 8, 1),

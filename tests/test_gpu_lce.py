@@ -432,3 +432,45 @@ def test_staged_backward_equals_cached_head(n, d, v, chunk, head):
     odh = olce.backward(h, wf, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
     assert rel_l2(staged[0], odh) <= 1e-2
     assert (staged[0][t == IGN] == 0).all()
+
+
+@pytest.mark.parametrize(("n", "d", "v"), [(1000, 512, 20000), (513, 192, 7777), (64, 64, 1000), (2048, 1024, 40000)])
+def test_staged_forward_equals_in_register_dequantization(n, d, v):
+    """mtp_lce_fwd with MTP_HEAD_Q4_STAGED: runs of whole vocab splits dequantized into the workspace,
+    then the dense product over them. nll, lse and tgt equal MTP_HEAD_Q4's (dequantization inside the
+    product) bit for bit at every staging size: the least (one split per run), a few splits per run
+    (also a size that is no whole number of splits), the whole head. The workspace starts as all-ones
+    bytes (bf16 NaN), so a staged row read before it is written would show. A workspace below the
+    least is refused before any launch."""
+    from mlx_train_perf import _native
+
+    print(f"[lce staged forward] n={n} d={d} v={v}", flush=True)
+    lib = _native.load()
+    h, w, t = lce_inputs(n, d, v, seed=n + v)
+    hd, td = h.cuda(), t.cuda()
+    keep = tuple(x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))
+    ptrs = (None, keep[0].data_ptr(), keep[1].data_ptr(), keep[2].data_ptr())
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def run(kind, ws_bytes):
+        ws = torch.full((ws_bytes,), 255, dtype=torch.uint8, device="cuda")
+        outs = [torch.full((n,), 3.0, device="cuda") for _ in range(3)]
+        rc = lib.mtp_lce_fwd(hd.data_ptr(), *ptrs, td.data_ptr(), n, d, v, kind, IGN, outs[0].data_ptr(),
+                             outs[1].data_ptr(), outs[2].data_ptr(), ws.data_ptr(), ws_bytes, stream)
+        torch.cuda.synchronize()
+        return rc, [x.cpu() for x in outs]
+
+    rc, want = run(_native.HEAD_Q4, lib.mtp_lce_fwd_workspace_bytes(n, d, v, _native.HEAD_Q4))
+    _native.check(rc, domain="loss")
+    least = lib.mtp_lce_fwd_workspace_bytes(n, d, v, _native.HEAD_Q4_STAGED)
+    off = -(-lib.mtp_lce_fwd_workspace_bytes(n, d, v, _native.HEAD_Q4) // 256) * 256
+    split = least - off   # bytes of the largest split's rows
+    full = lib.mtp_lce_fwd_stage_workspace_bytes(n, d, v, 1 << 40)
+    assert full == off + v * d * 2 and least < full
+    for ws_bytes in (least, least + 2 * split, least + 2 * split + 37 * d * 2, full):
+        rc, got = run(_native.HEAD_Q4_STAGED, ws_bytes)
+        _native.check(rc, domain="loss")
+        for name, a, b in zip(("nll", "lse", "tgt"), got, want):
+            assert torch.equal(a, b), (name, ws_bytes)
+    rc, _ = run(_native.HEAD_Q4_STAGED, least - 2)
+    assert rc == _native.MTP_ERR_WORKSPACE

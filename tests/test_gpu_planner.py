@@ -72,8 +72,10 @@ def test_planner_matches_measured_loss_peaks(trainable, monkeypatch):
 
 
 def test_planner_matches_measured_staged_q4_peaks(monkeypatch):
-    """A 4-bit head (C3) with the default staged backward: no cached copy; the backward's peak is the
-    planned workspace (gradient tiles, fp32 dH accumulator, one staged head chunk) and dH."""
+    """A 4-bit head (C3) with the default staged forward and backward: no cached copy; the forward's
+    peak is its outputs and the planned workspace (partials, the dequantized head's vocab splits),
+    the backward's the planned workspace (gradient tiles, fp32 dH accumulator, one staged head chunk
+    and its dequantized rows) and dH."""
     from mlx_train_perf.core import loss as L
     from mlx_train_perf.plan import estimate as est
     from oracle import quant as oquant
@@ -100,7 +102,10 @@ def test_planner_matches_measured_staged_q4_peaks(monkeypatch):
         peaks.append((fwd, bwd))
     print(f"  forward {peaks[1][0]} B (plan {plan.forward_peak}); backward {peaks[1][1]} B (plan "
           f"{plan.backward_peak} + dH {dh_bytes})", flush=True)
-    assert peaks[0][0] == peaks[1][0] == plan.forward_peak
+    # the forward's staging workspace (the whole dequantized head here) is one allocation, which the
+    # caching allocator rounds up to a multiple of 2 MiB
+    assert peaks[0][0] == peaks[1][0]
+    assert plan.forward_peak <= peaks[1][0] < plan.forward_peak + (2 << 20)
     lo = plan.backward_peak + dh_bytes - N * 4
     assert lo <= peaks[1][1] <= lo + 3 * N * 4 + 3 * (2 << 20), (peaks[1][1], lo)
     assert abs(peaks[0][1] - peaks[1][1]) <= 2 << 20 and L.transposed_head_cache_bytes() == 0
