@@ -1667,19 +1667,27 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
                                                                  const uint32_t* __restrict__ Wq,
                                                                  const bf16_t* __restrict__ Sc,
                                                                  const bf16_t* __restrict__ Bi, int V, int D,
-                                                                 int ldt, int dspan, bf16_t* __restrict__ Wt,
+                                                                 int ldt, int dspan, int nspan,
+                                                                 bf16_t* __restrict__ Wt,
                                                                  bf16_t* __restrict__ rows_out) {
   __shared__ uint16_t tile[64][64 + 2];
   // Workgroup (x, y) transposes vocab rows [64 x, 64 x + 64) over hidden dims [dspan y, dspan (y + 1)),
-  // 64 x 64 tiles in turn. A 4-bit head takes the whole hidden dim per workgroup (dspan = D): its rows'
-  // memory lines (packed words, and scales and biases, 2 bytes of a line per 64 dims) are then read
-  // by one workgroup and stay in its L2 between tiles, instead of being fetched once per tile by
-  // workgroups on other XCDs. A dense head takes one tile per workgroup (dspan = 64).
+  // 64 x 64 tiles in turn. A dense head takes one tile per workgroup (dspan = 64, 2D grid). A 4-bit
+  // head's row carries its scales and biases in one memory line each (2 bytes per 64 dims): its
+  // nspan <= 8 spans of vocab block x run on one XCD (1D grid, blocks of 8 x 8 workgroups whose
+  // index mod 8 is x mod 8), so those lines are fetched into that XCD's L2 once.
   // rows_out (optional, 4-bit head): the dequantized rows as well, bf16 [V][D], row-major.
-  const int v0 = blockIdx.x * 64;
+  int bx = blockIdx.x, by = blockIdx.y;
+  if (nspan > 0) {
+    const int k = blockIdx.x % (8 * nspan);
+    bx = blockIdx.x / (8 * nspan) * 8 + (k & 7);
+    by = k >> 3;
+    if (bx * 64 >= ldt) return;
+  }
+  const int v0 = bx * 64;
   const int t = threadIdx.x;
-  const int dend = (blockIdx.y + 1) * dspan < D ? (blockIdx.y + 1) * dspan : D;
-  for (int d0 = blockIdx.y * dspan; d0 < dend; d0 += 64) {
+  const int dend = (by + 1) * dspan < D ? (by + 1) * dspan : D;
+  for (int d0 = by * dspan; d0 < dend; d0 += 64) {
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
       const int id = t + 256 * p;
@@ -1721,33 +1729,47 @@ __global__ __launch_bounds__(256) void lce_head_transpose_kernel(const bf16_t* _
 
 long lce_head_t_ld(long V) { return (V + kTile - 1) / kTile * kTile + kGPitchPad; }
 
-// Rows of a 4-bit head dequantized to bf16, row-major [rows][D] (D % 64 == 0): thread q expands the
-// four packed words 4q .. 4q + 3 (32 weights of one row and one 64-wide group) with that group's
-// scale and bias, as the product tiles do. nq = rows D / 32.
+// Rows of a 4-bit head dequantized to bf16, row-major [rows][D] (D % 64 == 0): packed word q (8
+// weights of group q / 8) expands with its group's scale and bias, as the product tiles do, into
+// output bytes [16 q, 16 q + 16). Workgroup b takes words [1024 b, 1024 b + 1024), lane-contiguous:
+// each wave loads 256 bytes and stores 1 KiB per step. nw = rows D / 8.
 __global__ __launch_bounds__(256) void lce_head_dequant_kernel(const uint32_t* __restrict__ Wq,
                                                                const bf16_t* __restrict__ Sc,
-                                                               const bf16_t* __restrict__ Bi, long nq,
+                                                               const bf16_t* __restrict__ Bi, long nw,
                                                                bf16_t* __restrict__ out) {
-  const long q = (long)blockIdx.x * 256 + threadIdx.x;
-  if (q >= nq) return;
-  const u32x4 w = *reinterpret_cast<const u32x4*>(Wq + 4 * q);
-  const float sc = bf16_to_f32(Sc[q >> 1]), bi = bf16_to_f32(Bi[q >> 1]);
-  u32x4* o = reinterpret_cast<u32x4*>(out + 32 * q);
+  const long q0 = (long)blockIdx.x * 1024 + threadIdx.x;
+  uint32_t w[4];
+  float sc[4], bi[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) o[e] = dequant8(w[e], sc, bi);
+  for (int i = 0; i < 4; ++i) {
+    const long q = q0 + 256 * i;
+    w[i] = q < nw ? Wq[q] : 0u;
+    sc[i] = q < nw ? bf16_to_f32(Sc[q >> 3]) : 0.f;
+    bi[i] = q < nw ? bf16_to_f32(Bi[q >> 3]) : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const long q = q0 + 256 * i;
+    if (q < nw) reinterpret_cast<u32x4*>(out)[q] = dequant8(w[i], sc[i], bi[i]);
+  }
 }
 
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
                                      bf16_t* rows_out) {
   const int ldt = (int)lce_head_t_ld(V);
-  const int dspan = h.q4 ? D : 64;
-  dim3 grid(ldt / 64, (D + dspan - 1) / dspan), block(256);
-  if (h.q4)
+  dim3 block(256);
+  if (h.q4) {
+    // at most 8 spans of whole 64-wide tiles
+    const int tiles = (D + 63) / 64, dspan = 64 * ((tiles + 7) / 8), nspan = (D + dspan - 1) / dspan;
+    const int gx = ldt / 64;
+    dim3 grid((gx + 7) / 8 * 8 * nspan);
     hipLaunchKernelGGL(lce_head_transpose_kernel<1>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan,
-                       Wt, rows_out);
-  else
-    hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, dspan,
+                       nspan, Wt, rows_out);
+  } else {
+    dim3 grid(ldt / 64, (D + 63) / 64);
+    hipLaunchKernelGGL(lce_head_transpose_kernel<0>, grid, block, 0, stream, h.w, h.wq, h.sc, h.bi, V, D, ldt, 64, 0,
                        Wt, nullptr);
+  }
   return hipGetLastError();
 }
 
@@ -1869,9 +1891,9 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
       const int vtiles = (V + kTile - 1) / kTile;
       const long r0 = (long)s0 * vtiles / ns * kTile;
       const long rows = lce_fwd_split_rows(N, V, s0, s1);
-      const long nq = rows * D / 32;
-      hipLaunchKernelGGL(lce_head_dequant_kernel, dim3((unsigned)((nq + 255) / 256)), dim3(256), 0, stream,
-                         h.wq + r0 * (D >> 3), h.sc + r0 * (D >> 6), h.bi + r0 * (D >> 6), nq, stage);
+      const long nw = rows * D / 8;
+      hipLaunchKernelGGL(lce_head_dequant_kernel, dim3((unsigned)((nw + 1023) / 1024)), dim3(256), 0, stream,
+                         h.wq + r0 * (D >> 3), h.sc + r0 * (D >> 6), h.bi + r0 * (D >> 6), nw, stage);
       hipError_t de = hipGetLastError();
       if (de != hipSuccess) return de;
       hipLaunchKernelGGL(lce_fwd_kernel<0>, dim3(rtiles * (s1 - s0)), block, 0, stream, H, stage, h.wq, h.sc, h.bi,
