@@ -178,8 +178,9 @@ def _fwd_launcher(h, head, t, head_kind):
     outs = [torch.empty(n_, dtype=torch.float32, device="cuda") for _ in range(3)]
     kind = _native.HEAD_DENSE if head_kind == "dense" else _native.HEAD_Q4
     ws_b = lib.mtp_lce_fwd_workspace_bytes(n_, d_, v_, kind)
-    if kind == _native.HEAD_Q4 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0":
-        # the loss layer's default 4-bit forward: vocab splits dequantized into the workspace
+    if (kind == _native.HEAD_Q4 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+            and plan.lce_fwd_stages_whole_head(n_, d_, v_, plan.lce_bwd_budget_bytes())):
+        # the loss layer's default 4-bit forward: the head dequantized into the workspace
         kind = _native.HEAD_Q4_STAGED
         ws_b = lib.mtp_lce_fwd_stage_workspace_bytes(n_, d_, v_, plan.lce_bwd_budget_bytes())
     ws = torch.empty(ws_b, dtype=torch.uint8, device="cuda")
@@ -247,7 +248,8 @@ def bench_lce(steps, warmup, head_kind="dense"):
     copy = os.environ.get("MTP_LCE_TRANSPOSED_HEAD", "auto")
     staged = ((copy == "0" or (head_kind == "q4" and copy != "1"))
               and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
-    fwd_staged = head_kind == "q4" and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+    fwd_staged = (head_kind == "q4" and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+                  and plan.lce_fwd_stages_whole_head(N, D, V, plan.lce_bwd_budget_bytes()))
     p = plan.lce_plan(n=N, v=V, d=D, staged=staged, quantized=head_kind == "q4", fwd_staged=fwd_staged)
     head_t = L.transposed_head_cache_bytes()
     return {"sec_per_step": sec, "fwd_ms": phase_fwd, "bwd_ms": phase_bwd,

@@ -303,10 +303,16 @@ def _transposed_head(owner: torch.Tensor | None, w, w_q, scales, biases, head_ki
         return wt
 
 
-def _stages_forward(head_kind: int, d: int, f32: bool) -> bool:
-    """A bf16 forward over a 4-bit head stages it (MTP_HEAD_Q4_STAGED) unless MTP_LCE_STAGE_HEAD is "0"."""
-    return (head_kind == _native.HEAD_Q4 and not f32 and d % 64 == 0
-            and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0")
+def _forward_stage_bytes(lib, n: int, d: int, v: int, head_kind: int, f32: bool) -> int:
+    """Workspace of the staged 4-bit forward (MTP_HEAD_Q4_STAGED) when the loss layer runs it, else 0:
+    a bf16 forward over a 4-bit head whose whole dequantization fits the workspace budget, unless
+    MTP_LCE_STAGE_HEAD is "0". With less room the forward would stage runs of its vocab splits one
+    launch each, every launch filling only part of the GPU: slower than dequantizing in registers."""
+    if head_kind != _native.HEAD_Q4 or f32 or d % 64 or os.environ.get("MTP_LCE_STAGE_HEAD", "1") == "0":
+        return 0
+    ws = lib.mtp_lce_fwd_stage_workspace_bytes(n, d, v, _plan.lce_bwd_budget_bytes())
+    whole = -(-lib.mtp_lce_fwd_workspace_bytes(n, d, v, _native.HEAD_Q4) // 256) * 256 + v * d * 2
+    return ws if ws == whole else 0
 
 
 class _KernelLCE(torch.autograd.Function):
@@ -327,10 +333,10 @@ class _KernelLCE(torch.autograd.Function):
         ws_fn = lib.mtp_lce_fwd_f32_workspace_bytes if f32 else lib.mtp_lce_fwd_workspace_bytes
         fwd = lib.mtp_lce_fwd_f32 if f32 else lib.mtp_lce_fwd
         fwd_kind = head_kind
-        if _stages_forward(head_kind, d, f32):
-            # runs of vocab splits of the 4-bit head dequantized into the workspace, then a dense product
+        ws_bytes = _forward_stage_bytes(lib, n, d, v, head_kind, f32)
+        if ws_bytes:
+            # the whole 4-bit head dequantized into the workspace, then the dense product over it
             fwd_kind = _native.HEAD_Q4_STAGED
-            ws_bytes = lib.mtp_lce_fwd_stage_workspace_bytes(n, d, v, _plan.lce_bwd_budget_bytes())
         else:
             ws_bytes = ws_fn(n, d, v, head_kind)
         ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)

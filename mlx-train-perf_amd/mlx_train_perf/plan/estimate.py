@@ -75,9 +75,9 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
     impl) the cached transposed head; a trainable head adds its dL/dW and, on the kernel impl, takes
     every row in one backward block. A head without the cached copy (a 4-bit head by default)
     stages each vocab chunk of it in the backward's workspace instead (unless `MTP_LCE_STAGE_HEAD`
-    is "0"), over all rows; a 4-bit head's bf16 forward stages runs of its vocab splits, dequantized,
-    in its workspace within the same budget. The backward's returned dH (n*d*dtype) is the caller's
-    gradient, not counted here."""
+    is "0"), over all rows; a 4-bit head's bf16 forward stages the whole head, dequantized, in its
+    workspace when that fits the same budget. The backward's returned dH (n*d*dtype) is the
+    caller's gradient, not counted here."""
     if n < 1 or d < 1 or v < 1:
         raise PlanInputError("n, d, v must be >= 1")
     eb = dtype_bytes(dtype)
@@ -86,7 +86,8 @@ def loss_bytes(*, n: int, d: int, v: int, impl: str = "kernel", dtype: str = "bf
         head_t = transposed_head_bytes(d=d, v=v, enabled=transposed_head, quantized=quantized, trainable=trainable)
         staged = head_t == 0 and d % 64 == 0 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
         budget = bwd_budget or _launch.lce_bwd_budget_bytes()
-        if quantized and eb == 2 and d % 64 == 0 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0":
+        if (quantized and eb == 2 and os.environ.get("MTP_LCE_STAGE_HEAD", "1") != "0"
+                and _launch.lce_fwd_stages_whole_head(n, d, v, budget)):
             fwd = 3 * n * 4 + _launch.lce_fwd_stage_workspace_bytes(n, d, v, budget)
         else:
             fwd = 3 * n * 4 + _launch.lce_fwd_workspace_bytes(n, v)

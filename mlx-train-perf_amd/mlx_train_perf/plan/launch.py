@@ -211,6 +211,13 @@ class LcePlan:
     bwd_workspace_bytes: int
 
 
+def lce_fwd_stages_whole_head(n: int, d: int, v: int, budget: int) -> bool:
+    """The loss layer's staged 4-bit forward runs only when the whole dequantized head fits the
+    budget (one launch over every vocab split)."""
+    whole = -(-lce_fwd_workspace_bytes(n, v) // 256) * 256 + v * d * 2
+    return d % 64 == 0 and lce_fwd_stage_workspace_bytes(n, d, v, budget) == whole
+
+
 def lce_plan(*, n: int, v: int, d: int = 4096, budget: int | None = None, trainable: bool = False,
              staged: bool = False, quantized: bool = False, fwd_staged: bool = False) -> LcePlan:
     """Forward splits and backward geometry. A trainable head's dL/dW sums over every row, so its

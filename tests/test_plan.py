@@ -239,3 +239,35 @@ def test_memory_planner_head_terms():
     assert full_lb.backward_peak > lora_lb.backward_peak + v * d * 2
     # the chunked and naive impls carry the dL/dW term too
     assert est.loss_bytes(n=n, d=d, v=v, impl="chunked", trainable=True).head_grad == v * d * 2
+
+
+def test_memory_planner_quantized_head_staging(monkeypatch):
+    """A 4-bit head (QLoRA, config 3): the backward stages each vocab chunk's dequantized rows and the
+    chunk transposed (4 chunks of 44800 columns within 1.5 GiB: 2N + 4D bytes per column); the bf16
+    forward stages the whole dequantized head when it fits the budget (one launch over every vocab
+    split), else it dequantizes in registers with only the split partials; MTP_LCE_STAGE_HEAD=0
+    stages nothing."""
+    from mlx_train_perf.plan import estimate as est
+
+    monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
+    monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
+    n, d, v = 8192, 4096, 151936
+    budget = 3 << 29
+    p = plan.lce_plan(n=n, v=v, d=d, budget=budget, staged=True, quantized=True, fwd_staged=True)
+    assert p.bwd_row_block == n and p.bwd_chunk == 44800 and p.bwd_chunks == 4
+    partials = plan.lce_fwd_workspace_bytes(n, v)
+    whole = -(-partials // 256) * 256 + v * d * 2
+    assert plan.lce_fwd_stages_whole_head(n, d, v, budget) and p.fwd_workspace_bytes == whole
+    q = est.loss_bytes(n=n, d=d, v=v, quantized=True, bwd_budget=budget)
+    assert q.transposed_head == 0
+    assert q.forward_peak == 3 * n * 4 + whole < q.backward_workspace
+    assert q.backward_workspace == p.bwd_workspace_bytes + n * 4
+    # a budget below the whole head: the forward dequantizes in registers
+    small = 3 << 28
+    assert not plan.lce_fwd_stages_whole_head(n, d, v, small)
+    assert est.loss_bytes(n=n, d=d, v=v, quantized=True, bwd_budget=small).forward_peak == 3 * n * 4 + partials
+    # fp32 inputs and d % 64 != 0 never stage the forward
+    assert est.loss_bytes(n=n, d=d, v=v, quantized=True, dtype="fp32", bwd_budget=budget).forward_peak == 3 * n * 4 + partials
+    assert not plan.lce_fwd_stages_whole_head(n, 4000, v, 1 << 40)
+    monkeypatch.setenv("MTP_LCE_STAGE_HEAD", "0")
+    assert est.loss_bytes(n=n, d=d, v=v, quantized=True, bwd_budget=budget).forward_peak == 3 * n * 4 + partials
