@@ -229,6 +229,7 @@ __device__ __forceinline__ int swz32(int r) { return (r ^ ((r >> 3) & 3)) & 7; }
 // XOR the k-step's chunk bits plus the block's 4096 b.
 struct RowFrags {
   static constexpr int kReads = 1;
+  static constexpr bool kAsmReads = false;
   int xo;  // lane offset of block 0, k-step 0: row (first_row + lane % 32), chunk lane / 32
 
   template <int NB>
@@ -308,6 +309,11 @@ struct DmaRowOp : RowFrags {
 // ds_read_b64_tr_b16 (8 consecutive k of one column).
 struct TransFrags {
   static constexpr int kReads = 2;
+  // The reads are inline asm: the compiler's wait insertion treats the ds_read_tr builtin as a
+  // possible reader of every LDS DMA in flight, and put a vmcnt(0) before each stage's first
+  // fragment reads, i.e. a wait for the copies that stage had just issued. gemm_dma waits for the
+  // fragments itself (frags_ready) before the MFMAs that use them.
+  static constexpr bool kAsmReads = true;
   int lo[4];           // per-lane fragment offsets (per 32-column block)
 
   template <int NB>
@@ -323,10 +329,12 @@ struct TransFrags {
     }
   }
   __device__ __forceinline__ bf16x8 read(const char* st, int b, int ks) const {
-    const lds_bf16x4* p = (const lds_bf16x4*)(st + lo[b] + ks * 16 * 512);
-    const bf16x4 x0 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)p);
-    const bf16x4 x1 = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p + 4 * 512 / 8));
-    return bf16x8{x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    const uint32_t a =
+        (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)(st + lo[b] + ks * 16 * 512);
+    u32x2 x0, x1;
+    asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(x0) : "v"(a));
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:2048" : "=v"(x1) : "v"(a));
+    return __builtin_bit_cast(bf16x8, u32x4{x0[0], x0[1], x1[0], x1[1]});
   }
 };
 
@@ -531,6 +539,17 @@ __device__ __forceinline__ void dma_read_frags(const OA& oa, const OB& ob, const
   for (int i = 1; i < 4; ++i) fa[i] = oa.read(st, i, ks);
 }
 
+// Fragments read by inline asm (kAsmReads) are not tracked by the compiler: wait for every LDS
+// operation in flight and mark the fragments as produced here, so the MFMAs that use them stay
+// after the wait. Called where the only LDS reads in flight are those of fa / fb.
+template <class OA, class OB>
+__device__ __forceinline__ void frags_ready(bf16x8 (&fa)[4], bf16x8 (&fb)[kNJ]) {
+  if constexpr (OA::kAsmReads || OB::kAsmReads) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(fa[0]), "+v"(fa[1]), "+v"(fa[2]), "+v"(fa[3]), "+v"(fb[0]), "+v"(fb[1]));
+  }
+}
+
 __device__ __forceinline__ void dma_mfma(const bf16x8 (&fa)[4], const bf16x8 (&fb)[kNJ], f32x16 (&acc)[4][kNJ]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -615,7 +634,9 @@ __device__ __forceinline__ auto& inline_op(OA& oa, OB& ob) {
 template <int PRE_VM = 0, class OA, class OB, class NEXT>
 __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x16 (&acc)[4][kNJ], bool pre,
                                          bool has_next, const NEXT& next, long next_shift = 0) {
-  constexpr int NR = 4 * OA::kReads + kNJ * OB::kReads;
+  // LDS reads per k-step that the scheduling groups place (asm reads are not DS-read instructions
+  // to the scheduler).
+  constexpr int NR = (OA::kAsmReads ? 0 : 4 * OA::kReads) + (OB::kAsmReads ? 0 : kNJ * OB::kReads);
   const int w = threadIdx.x >> 6;
   constexpr bool kCopiers = OA::kPartner && OB::kPartner;
   // The 4-bit operand dequantized in registers (at most one; its tile is A or B of each stage).
@@ -693,26 +714,32 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
       if constexpr (kQ) {
         // 4-bit operand: dequantize slab kt + 1 (qc) into the next stage's tile (free since the
         // last barrier) between this stage's MFMAs.
+        frags_ready<OA, OB>(fa, fb);
         dma_read_frags(oa, ob, cur, 1, ga, gb);
         dma_mfma(fa, fb, acc);
         q.template produce_word<0>(nxt + kQOff);
         q.template produce_word<1>(nxt + kQOff);
         dma_sched_q4<NR, 2>();
+        frags_ready<OA, OB>(ga, gb);
         dma_read_frags(oa, ob, cur, 2, fa, fb);
         dma_mfma(ga, gb, acc);
         q.template produce_word<2>(nxt + kQOff);
         dma_sched_q4<NR, 1>();
+        frags_ready<OA, OB>(fa, fb);
         dma_read_frags(oa, ob, cur, 3, ga, gb);
         dma_mfma(fa, fb, acc);
         q.template produce_word<3>(nxt + kQOff);
         dma_sched_q4<NR, 1>();
       } else {
+        frags_ready<OA, OB>(fa, fb);
         dma_read_frags(oa, ob, cur, 1, ga, gb);
         dma_mfma(fa, fb, acc);
         dma_sched<NR>();
+        frags_ready<OA, OB>(ga, gb);
         dma_read_frags(oa, ob, cur, 2, fa, fb);
         dma_mfma(ga, gb, acc);
         dma_sched<NR>();
+        frags_ready<OA, OB>(fa, fb);
         dma_read_frags(oa, ob, cur, 3, ga, gb);
         dma_mfma(fa, fb, acc);
         dma_sched<NR>();
@@ -735,6 +762,8 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
         if constexpr (R != 2) q.template load_sb<false>(kt + 3);
       }
       const bool live = kt + 2 < nk;
+      // ga / gb landed before the barrier (its lgkmcnt(0)); this only keeps their MFMAs below it.
+      frags_ready<OA, OB>(ga, gb);
       if constexpr (R == 0) {
         oa.issue(kt + 2, cur, live);
         ob.issue(kt + 2, cur + 32768, live);
@@ -774,12 +803,15 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
   // Last stage.
   {
     char* cur = lds + (((nk - 1) & 1) ? kDmaStage : 0);
+    frags_ready<OA, OB>(fa, fb);
     dma_read_frags(oa, ob, cur, 1, ga, gb);
     dma_mfma(fa, fb, acc);
     dma_sched<NR>();
+    frags_ready<OA, OB>(ga, gb);
     dma_read_frags(oa, ob, cur, 2, fa, fb);
     dma_mfma(ga, gb, acc);
     dma_sched<NR>();
+    frags_ready<OA, OB>(fa, fb);
     dma_read_frags(oa, ob, cur, 3, ga, gb);
     dma_mfma(fa, fb, acc);
     dma_sched<NR>();
@@ -787,6 +819,7 @@ __device__ __forceinline__ void gemm_dma(OA& oa, OB& ob, int nk, char* lds, f32x
     wait_vmcnt<0>();
     raw_barrier();
     if (has_next) next();
+    frags_ready<OA, OB>(ga, gb);
     dma_mfma(ga, gb, acc);
     dma_sched<NR>();
   }
