@@ -676,10 +676,12 @@ def committed_traffic(kernel: str):
 
 def pmc_workload():
     """One pass of each profiled workload (no timing): the 1 GiB copy and the MFMA loop
-    (calibrations), the flagship LCE forward + backward (dense and 4-bit), causal attention
-    (S=8192) and packed attention (S=16384, config 5). Each kernel instantiation serves one workload
-    here, so per-kernel counter means are per-workload figures (non-causal attention would share the
-    causal instantiations, and is left out)."""
+    (calibrations), the flagship LCE forward + backward (dense, and 4-bit dequantized in registers),
+    causal attention (S=8192) and packed attention (S=16384, config 5). Each kernel instantiation
+    serves one workload here, so per-kernel counter means are per-workload figures (non-causal
+    attention would share the causal instantiations, and is left out; so would the staged 4-bit
+    path, whose products are the dense instantiations over dequantized rows, so the 4-bit pass runs
+    with MTP_LCE_STAGE_HEAD=0)."""
     import torch
 
     from mlx_train_perf import _native
@@ -700,10 +702,19 @@ def pmc_workload():
         h, w, t = lce_inputs_gpu(N, D, V)
         head = _lce_head(w, kind)
         hd = h.requires_grad_(True)
-        for _ in range(2):
-            nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
-            nll.backward(torch.full_like(nll, 1.0 / N))
-        torch.cuda.synchronize()
+        saved = os.environ.get("MTP_LCE_STAGE_HEAD")
+        if kind == "q4":
+            os.environ["MTP_LCE_STAGE_HEAD"] = "0"
+        try:
+            for _ in range(2):
+                nll, _, _ = kernel_forward_parts(hd, head, t, ignore_index=IGNORE)
+                nll.backward(torch.full_like(nll, 1.0 / N))
+            torch.cuda.synchronize()
+        finally:
+            if saved is None:
+                os.environ.pop("MTP_LCE_STAGE_HEAD", None)
+            else:
+                os.environ["MTP_LCE_STAGE_HEAD"] = saved
         del h, w, t, hd, head
         torch.cuda.empty_cache()
         print(f"pmc workload: lce {kind} done", flush=True)
@@ -803,7 +814,7 @@ def pmc_summary(command: str, *dirs: str) -> str:
         if short in algorithmic_bytes:
             r["algorithmic_bytes"] = algorithmic_bytes[short]
         kernels[short] = r
-    lines = ["# Counters per launch: bench.py --pmc-workload (LCE N=8192 D=4096 V=151936 dense <0> and 4-bit <1>; "
+    lines = ["# Counters per launch: bench.py --pmc-workload (LCE N=8192 D=4096 V=151936 dense <0> and 4-bit dequantized in registers <1>; "
              "attention S=8192 causal <false, *>, S=16384 packed <true, *>)", "",
              "Commands (repository root on the GPU box; one rocprofv3 pass per counter group):", "", "```", command,
              "```", ""]
