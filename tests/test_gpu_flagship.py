@@ -131,8 +131,8 @@ def test_c3_flagship_lce_q4(monkeypatch):
     del w
     wdq = oquant.dequantize_affine(wq, sc, bi, group_size=64, dtype=torch.float32)
     head = QuantizedHead(w_q=wq, scales=sc, biases=bi)
-    # the default backward: each vocab chunk of the 4-bit head staged (dequantized, transposed) in
-    # the workspace
+    # the default: the forward over the whole head dequantized into its workspace, the backward
+    # staging each vocab chunk's dequantized rows and the chunk transposed in its workspace
     monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
     monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
     L.clear_transposed_head_cache()
@@ -142,13 +142,15 @@ def test_c3_flagship_lce_q4(monkeypatch):
     odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
     _check_lce(nll, lse, dh, onll, olse, odh, t, nll_abs=8e-3)
     # the other two backwards: the whole head kept as a cached transposed copy, and neither copy nor
-    # staging (the packed words dequantized in registers into the dH product's transposed tiles)
+    # staging (the packed words dequantized in registers, in the forward too: its nll and lse are
+    # the staged forward's bit for bit)
     for copy, stage in (("1", "1"), ("0", "0")):
         print(f"[C3] backward with MTP_LCE_TRANSPOSED_HEAD={copy} MTP_LCE_STAGE_HEAD={stage}", flush=True)
         monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", copy)
         monkeypatch.setenv("MTP_LCE_STAGE_HEAD", stage)
         L.clear_transposed_head_cache()
-        _, _, dh2, _ = _kernel_lce(h, head, t)
+        nll2, lse2, dh2, _ = _kernel_lce(h, head, t)
+        assert torch.equal(nll2, nll) and torch.equal(lse2, lse)
         assert (dh2[t == IGN] == 0).all()
         r = _rel_l2(dh2, odh)
         print(f"  dH rel-L2 {r:.3e}", flush=True)
