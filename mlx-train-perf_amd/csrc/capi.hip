@@ -156,15 +156,7 @@ size_t mtp_lce_fwd_stage_workspace_bytes(int64_t n, int64_t d, int64_t v, size_t
   const long least = mtp::lce_fwd_stage_rows_max((long)n, (long)v);
   if (cap < least) cap = least;
   // The largest run of whole splits the launcher forms with `cap` rows.
-  const long ns = mtp::lce_fwd_nsplit((long)n, (long)v);
-  long most = 0;
-  for (long s0 = 0; s0 < ns;) {
-    const long s1 = mtp::lce_fwd_stage_group_end((long)n, (long)v, s0, cap);
-    const long r = mtp::lce_fwd_split_rows((long)n, (long)v, s0, s1);
-    if (r > most) most = r;
-    s0 = s1;
-  }
-  return off + (size_t)most * (size_t)d * 2;
+  return off + (size_t)mtp::lce_fwd_stage_rows_used((long)n, (long)v, cap) * (size_t)d * 2;
 }
 
 int mtp_lce_fwd(const void* hidden, const void* w, const uint32_t* w_q, const void* scales, const void* biases,

@@ -1884,9 +1884,10 @@ static int lce_dh_split_a(int rtiles, int dtiles) {
 
 int lce_fwd_nsplit(long N, long V) { return lce_nsplit(N, V, kFwdWaves); }
 
-long lce_fwd_split_rows(long N, long V, long split0, long split1) {
-  const long ns = lce_fwd_nsplit(N, V), vtiles = (V + kTile - 1) / kTile;
-  const long r0 = split0 * vtiles / ns * kTile, r1 = split1 * vtiles / ns * kTile;
+// Vocab rows of splits [s0, s1) of ns over V (the split count computed once by the caller).
+static long split_rows(long V, long ns, long s0, long s1) {
+  const long vtiles = (V + kTile - 1) / kTile;
+  const long r0 = s0 * vtiles / ns * kTile, r1 = s1 * vtiles / ns * kTile;
   return (r1 < V ? r1 : V) - r0;
 }
 
@@ -1894,17 +1895,29 @@ long lce_fwd_stage_rows_max(long N, long V) {
   const long ns = lce_fwd_nsplit(N, V);
   long most = 0;
   for (long s = 0; s < ns; ++s) {
-    const long r = lce_fwd_split_rows(N, V, s, s + 1);
+    const long r = split_rows(V, ns, s, s + 1);
     if (r > most) most = r;
   }
   return most;
 }
 
-long lce_fwd_stage_group_end(long N, long V, long split0, long stage_rows) {
-  const long ns = lce_fwd_nsplit(N, V);
-  long e = split0 + 1;
-  while (e < ns && lce_fwd_split_rows(N, V, split0, e + 1) <= stage_rows) ++e;
+// End of the run of whole splits from s0 whose rows fit stage_rows (at least s0 + 1).
+static long group_end(long V, long ns, long s0, long stage_rows) {
+  long e = s0 + 1;
+  while (e < ns && split_rows(V, ns, s0, e + 1) <= stage_rows) ++e;
   return e;
+}
+
+long lce_fwd_stage_rows_used(long N, long V, long stage_rows) {
+  const long ns = lce_fwd_nsplit(N, V);
+  long most = 0;
+  for (long s0 = 0; s0 < ns;) {
+    const long s1 = group_end(V, ns, s0, stage_rows);
+    const long r = split_rows(V, ns, s0, s1);
+    if (r > most) most = r;
+    s0 = s1;
+  }
+  return most;
 }
 
 hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targets, int N, int D, int V,
@@ -1920,10 +1933,10 @@ hipError_t launch_lce_fwd(const LceHead& h, const bf16_t* H, const int64_t* targ
     // into it, then the dense product over them. The splits and their tiles are those of the
     // single launch below, so the partials are too.
     for (int s0 = 0; s0 < ns;) {
-      const int s1 = (int)lce_fwd_stage_group_end(N, V, s0, stage_rows);
+      const int s1 = (int)group_end(V, ns, s0, stage_rows);
       const int vtiles = (V + kTile - 1) / kTile;
       const long r0 = (long)s0 * vtiles / ns * kTile;
-      const long rows = lce_fwd_split_rows(N, V, s0, s1);
+      const long rows = split_rows(V, ns, s0, s1);
       const long nw = rows * D / 8;
       hipLaunchKernelGGL(lce_head_dequant_kernel, dim3((unsigned)((nw + 1023) / 1024)), dim3(256), 0, stream,
                          h.wq + r0 * (D >> 3), h.sc + r0 * (D >> 6), h.bi + r0 * (D >> 6), nw, stage);

@@ -44,11 +44,10 @@ size_t lce_dh_parts_bytes(long rows, long D, long ktiles);
 hipError_t launch_lce_head_transpose(const LceHead& h, int V, int D, bf16_t* Wt, hipStream_t stream,
                                      bf16_t* rows_out = nullptr);
 
-// Vocab rows of forward splits [split0, split1) (N rows, V vocab), the most any one split takes, and
-// the end of the run of whole splits from split0 whose rows fit `stage_rows` (at least split0 + 1).
-long lce_fwd_split_rows(long N, long V, long split0, long split1);
+// Vocab rows of the forward's largest split (N rows, V vocab), and of its largest run when it
+// stages runs of whole splits into `stage_rows` rows.
 long lce_fwd_stage_rows_max(long N, long V);
-long lce_fwd_stage_group_end(long N, long V, long split0, long stage_rows);
+long lce_fwd_stage_rows_used(long N, long V, long stage_rows);
 
 // stage (optional, 4-bit head with D % 64 == 0): a buffer of stage_rows >= lce_fwd_stage_rows_max rows
 // of D bf16 into which runs of vocab splits are dequantized before a dense product over them (the

@@ -98,9 +98,10 @@ def lce_fwd_workspace_bytes(n: int, v: int) -> int:
     return 2 * lce_fwd_splits(n, v) * n * 4
 
 
-def lce_fwd_split_rows(n: int, v: int, s0: int, s1: int) -> int:
-    """Vocab rows of forward splits [s0, s1)."""
-    ns, vtiles = lce_fwd_splits(n, v), -(-v // TILE)
+def lce_fwd_split_rows(n: int, v: int, s0: int, s1: int, ns: int | None = None) -> int:
+    """Vocab rows of forward splits [s0, s1) (`ns`: the split count, when the caller has it)."""
+    ns = lce_fwd_splits(n, v) if ns is None else ns
+    vtiles = -(-v // TILE)
     return min(v, s1 * vtiles // ns * TILE) - s0 * vtiles // ns * TILE
 
 
@@ -113,13 +114,13 @@ def lce_fwd_stage_workspace_bytes(n: int, d: int, v: int, budget: int) -> int:
     ns = lce_fwd_splits(n, v)
     off = -(-lce_fwd_workspace_bytes(n, v) // 256) * 256
     cap = max((budget - off) // (2 * d) if budget > off else 0,
-              max(lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns)))
+              max(lce_fwd_split_rows(n, v, s, s + 1, ns) for s in range(ns)))
     most, s0 = 0, 0
     while s0 < ns:
         s1 = s0 + 1
-        while s1 < ns and lce_fwd_split_rows(n, v, s0, s1 + 1) <= cap:
+        while s1 < ns and lce_fwd_split_rows(n, v, s0, s1 + 1, ns) <= cap:
             s1 += 1
-        most = max(most, lce_fwd_split_rows(n, v, s0, s1))
+        most = max(most, lce_fwd_split_rows(n, v, s0, s1, ns))
         s0 = s1
     return off + most * d * 2
 

@@ -56,7 +56,8 @@ def test_staged_plan_agrees_with_python_planner(n, d, v, budget, kind):
 
 @pytest.mark.parametrize("budget", [3 << 29, 1 << 28, 1 << 24, 0, 1 << 40])
 @pytest.mark.parametrize(("n", "d", "v"), [(8192, 4096, 151936), (4096, 4096, 151936), (1000, 512, 20000),
-                                           (513, 192, 7777), (64, 64, 1000), (2048, 1024, 40000), (100, 96, 500)])
+                                           (513, 192, 7777), (64, 64, 1000), (2048, 1024, 40000), (100, 96, 500),
+                                           (256, 128, 262144), (512, 64, 200000)])
 def test_staged_forward_workspace_agrees_with_python_planner(n, d, v, budget):
     """The staged 4-bit forward's workspace (partials, then the largest run of whole vocab splits
     whose rows fit the budget) agrees between the library and plan/launch.py; the least it takes is
@@ -71,10 +72,10 @@ def test_staged_forward_workspace_agrees_with_python_planner(n, d, v, budget):
     assert ws == plan.lce_fwd_stage_workspace_bytes(n, d, v, budget)
     off = -(-plan.lce_fwd_workspace_bytes(n, v) // 256) * 256
     ns = plan.lce_fwd_splits(n, v)
-    one = max(plan.lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns))
+    one = max(plan.lce_fwd_split_rows(n, v, s, s + 1, ns) for s in range(ns))
     assert lib.mtp_lce_fwd_workspace_bytes(n, d, v, N.HEAD_Q4_STAGED) == off + one * d * 2
     assert off + one * d * 2 <= ws <= off + v * d * 2
-    assert sum(plan.lce_fwd_split_rows(n, v, s, s + 1) for s in range(ns)) == v
+    assert sum(plan.lce_fwd_split_rows(n, v, s, s + 1, ns) for s in range(ns)) == v
     if budget >= off + v * d * 2:
         assert ws == off + v * d * 2
     elif ws > off + one * d * 2:
