@@ -310,8 +310,8 @@ struct DmaRowOp : RowFrags {
 struct TransFrags {
   static constexpr int kReads = 2;
   // The reads are inline asm: the compiler's wait insertion treats the ds_read_tr builtin as a
-  // possible reader of every LDS DMA in flight, and put a vmcnt(0) before each stage's first
-  // fragment reads, i.e. a wait for the copies that stage had just issued. gemm_dma waits for the
+  // possible reader of every LDS DMA in flight and puts a vmcnt(0) before each stage's first
+  // fragment reads, i.e. a wait for the copies that stage has just issued. gemm_dma waits for the
   // fragments itself (frags_ready) before the MFMAs that use them.
   static constexpr bool kAsmReads = true;
   int lo[4];           // per-lane fragment offsets (per 32-column block)
@@ -1278,9 +1278,9 @@ void lce_bwd_g_kernel(const bf16_t* __restrict__ H, const bf16_t* __restrict__ W
 // ------------------------------------------------------------------------------------------
 // Backward step 1, persistent form (hidden dim a multiple of 64), without the one-hot term and
 // the zero padding columns (see lce_bwd_g_fix_kernel). Row r of the dense W holds vocab row
-// wrow0 + r (0 for the whole head, the chunk's first row for dequantized rows staged per chunk). Workgroup (row tile, vocab
-// split) walks its split's vocab tiles of the chunk back to back on the DMA core, in the
-// forward's XCD-grouped order; the next tile's first two stages are issued during the current
+// wrow0 + r (0 for the whole head, the chunk's first row for dequantized rows staged per chunk).
+// Workgroup (row tile, vocab split) walks its split's vocab tiles of the chunk back to back on the
+// DMA core, in the forward's XCD-grouped order; the next tile's first two stages are issued during the current
 // tile's last k-step. Each lane stores its G values straight from the accumulator layout (8-byte
 // buffer stores of 4 columns; the write-back L2 merges a row's 16 segments into whole lines), so
 // the epilogue needs no barrier and its stores drain while the next tile's MFMAs run: every
