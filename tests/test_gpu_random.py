@@ -43,6 +43,21 @@ for _ in range(6):
     PACKED_CASES.append((_lens, _hkv * _g, _hkv, _R.choice([64, 96, 128])))
 
 
+# "default": the loss layer's head modes (a cached transposed copy for a frozen dense head, staged
+# chunks for 4-bit and trainable heads, the staged 4-bit forward); "reads": no copy and no staging,
+# so the dH products (and dW) read the head through LDS transpose reads, and a 4-bit head is
+# dequantized in registers in every product.
+MODES = ["default", "reads"]
+
+
+def _set_mode(monkeypatch, mode):
+    monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
+    monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
+    if mode == "reads":
+        monkeypatch.setenv("MTP_LCE_TRANSPOSED_HEAD", "0")
+        monkeypatch.setenv("MTP_LCE_STAGE_HEAD", "0")
+
+
 def _lce_kernel(h, w, t, wq=None, sc=None, bi=None):
     from mlx_train_perf.core.loss import DenseHead, QuantizedHead, kernel_forward_parts
 
@@ -53,9 +68,11 @@ def _lce_kernel(h, w, t, wq=None, sc=None, bi=None):
     return hd, nll, lse
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize(("n", "d", "v"), LCE_CASES)
-def test_lce_random_dense(n, d, v):
-    print(f"[lce random dense] n={n} d={d} v={v}", flush=True)
+def test_lce_random_dense(n, d, v, mode, monkeypatch):
+    print(f"[lce random dense] n={n} d={d} v={v} mode={mode}", flush=True)
+    _set_mode(monkeypatch, mode)
     h, w, t = lce_inputs(n, d, v, seed=n * 31 + d + v)
     hd, nll, lse = _lce_kernel(h, w, t)
     onll, olse, _ = olce.forward(h, w, t, ignore_index=IGN)
@@ -70,9 +87,11 @@ def test_lce_random_dense(n, d, v):
         assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize(("n", "d", "v"), [c for c in LCE_CASES if c[1] % 64 == 0])
-def test_lce_random_quantized(n, d, v):
-    print(f"[lce random q4] n={n} d={d} v={v}", flush=True)
+def test_lce_random_quantized(n, d, v, mode, monkeypatch):
+    print(f"[lce random q4] n={n} d={d} v={v} mode={mode}", flush=True)
+    _set_mode(monkeypatch, mode)
     h, w, t = lce_inputs(n, d, v, seed=n * 17 + d + v, w_std=0.05)
     wq, sc, bi = oquant.quantize_affine(w.float(), group_size=64, scale_dtype=torch.bfloat16)
     wdq = oquant.dequantize_affine(wq, sc, bi, group_size=64, dtype=torch.float32)
@@ -88,11 +107,13 @@ def test_lce_random_quantized(n, d, v):
         assert rel_l2(hd.grad.cpu(), odh) <= 1e-2
 
 
+@pytest.mark.parametrize("mode", MODES)
 @pytest.mark.parametrize(("n", "d", "v"), DW_CASES)
-def test_lce_random_trainable_head(n, d, v):
+def test_lce_random_trainable_head(n, d, v, mode, monkeypatch):
     from mlx_train_perf.core.loss import DenseHead, kernel_forward_parts
 
-    print(f"[lce random dw] n={n} d={d} v={v}", flush=True)
+    print(f"[lce random dw] n={n} d={d} v={v} mode={mode}", flush=True)
+    _set_mode(monkeypatch, mode)
     h, w, t = lce_inputs(n, d, v, seed=n * 13 + d + v)
     hd = h.cuda().requires_grad_(True)
     wd = w.cuda().requires_grad_(True)
