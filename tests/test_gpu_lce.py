@@ -475,3 +475,44 @@ def test_staged_forward_equals_in_register_dequantization(n, d, v):
             assert torch.equal(a, b), (name, ws_bytes)
     rc, _ = run(_native.HEAD_Q4_STAGED, least - 2)
     assert rc == _native.MTP_ERR_WORKSPACE
+
+
+def test_quantized_head_small_budget_through_the_loss_layer(monkeypatch):
+    """A budget too small for the whole dequantized head: the loss layer's 4-bit forward dequantizes
+    in registers (nll and lse bit for bit those of the default budget's staged forward), and the
+    staged backward takes many small vocab chunks (dH within the oracle bar)."""
+    from mlx_train_perf import _native
+    from mlx_train_perf.core import loss as L
+    from mlx_train_perf.plan import launch as plan
+
+    n, d, v = 512, 256, 6000
+    print(f"[lce q4 small budget] n={n} d={d} v={v}", flush=True)
+    h, w, t = lce_inputs(n, d, v, seed=77, w_std=0.05)
+    wq, sc, bi = (x.cuda() for x in oquant.quantize_affine(w.float(), scale_dtype=torch.bfloat16))
+    wdq = oquant.dequantize_affine(wq.cpu(), sc.cpu(), bi.cpu(), dtype=torch.float32)
+    head = L.QuantizedHead(w_q=wq, scales=sc, biases=bi)
+    ct = _cotangent(t)
+    monkeypatch.delenv("MTP_LCE_TRANSPOSED_HEAD", raising=False)
+    monkeypatch.delenv("MTP_LCE_STAGE_HEAD", raising=False)
+
+    def run():
+        hd = h.cuda().requires_grad_(True)
+        nll, lse, _ = L.kernel_forward_parts(hd, head, t.cuda(), ignore_index=IGN)
+        nll.backward(ct.cuda())
+        torch.cuda.synchronize()
+        return nll.detach().cpu(), lse.cpu(), hd.grad.cpu()
+
+    monkeypatch.delenv("MTP_LCE_BWD_BUDGET", raising=False)
+    assert plan.lce_fwd_stages_whole_head(n, d, v, plan.lce_bwd_budget_bytes())
+    nll0, lse0, _ = run()
+    small = 2 << 20
+    monkeypatch.setenv("MTP_LCE_BWD_BUDGET", str(small))
+    assert not plan.lce_fwd_stages_whole_head(n, d, v, small)
+    chunk = _native.load().mtp_lce_bwd_stage_chunk(n, d, v, _native.HEAD_Q4_STAGED, small)
+    assert -(-v // chunk) > 4
+    nll1, lse1, dh1 = run()
+    assert torch.equal(nll1, nll0) and torch.equal(lse1, lse0)
+    _, olse, _ = olce.forward(h, wdq, t, ignore_index=IGN)
+    odh = olce.backward(h, wdq, t, olse, ct, ignore_index=IGN, round_g_bf16=True, dtype=torch.float64)
+    assert rel_l2(dh1, odh) <= 1e-2
+    assert (dh1[t == IGN] == 0).all()
